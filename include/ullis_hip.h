@@ -1,0 +1,175 @@
+/*
+ * libullis_hip: MI355X (gfx950) backend for the Ullis packed +-1 linear /
+ * LayerNorm / streamed cross-entropy training hot path.
+ *
+ * This C ABI replaces the GPU runtime that Ullis' model code calls through
+ * `Option<&MetalTrainRuntime>` (src/model.rs:1537-1542), i.e. the hot-path
+ * methods of `MetalRuntime` (src/metal.rs). Every entry point names the
+ * reference method it replaces. Differences by design:
+ *   - arguments are DEVICE pointers that persist across calls (parameters,
+ *     latents, carries, tapes); nothing is copied host<->device implicitly;
+ *   - calls are stream-ordered and asynchronous; ullis_hip_sync() waits
+ *     (MetalRuntime blocks in every submit, src/metal.rs:722-740);
+ *   - GEMM operands (activations) are IEEE fp16, the residual stream and
+ *     gradients fp32; parameters keep the reference's layouts exactly:
+ *     f16 bit patterns as uint16_t, fp32 carries, LSB-first uint32_t sign
+ *     words row-major [out, in] (src/model.rs:2266-2272);
+ *   - errors are status codes (0 ok, negative failure) with a message from
+ *     ullis_hip_last_error() instead of anyhow::Result; shape rules follow
+ *     LinearDispatchShape / check_binary_shape (src/metal.rs:62-87, 3512-3546):
+ *     zero-sized dimensions and > INT32_MAX extents are rejected.
+ * A context is not thread safe (MetalRuntime is !Sync, src/metal.rs:456).
+ */
+#ifndef ULLIS_HIP_H
+#define ULLIS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "ullis_heron_layout.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ULLIS_HIP_OK 0
+#define ULLIS_HIP_ERR_INVALID (-1) /* shape or argument rejected before launch */
+#define ULLIS_HIP_ERR_RUNTIME (-3) /* HIP runtime / kernel error */
+#define ULLIS_HIP_ERR_NOMEM (-4)
+
+#define ULLIS_HIP_F16 1
+#define ULLIS_HIP_F32 2
+
+typedef struct ullis_hip_ctx ullis_hip_ctx;
+typedef struct ullis_hip_heron ullis_hip_heron;
+
+/* ---- context, memory, timing (MetalRuntime::new, src/metal.rs:466-596;
+ *      buffer pool src/metal.rs:342-414, 625-720) ---- */
+int ullis_hip_version(void);
+int ullis_hip_device_count(int* count);
+int ullis_hip_create(int device, ullis_hip_ctx** out);
+void ullis_hip_destroy(ullis_hip_ctx* ctx);
+const char* ullis_hip_last_error(const ullis_hip_ctx* ctx);
+int ullis_hip_sync(ullis_hip_ctx* ctx);
+int ullis_hip_malloc(ullis_hip_ctx* ctx, size_t bytes, void** ptr);
+int ullis_hip_free(ullis_hip_ctx* ctx, void* ptr);
+/* synchronous copies */
+int ullis_hip_upload(ullis_hip_ctx* ctx, void* dst_device, const void* src_host, size_t bytes);
+int ullis_hip_download(ullis_hip_ctx* ctx, void* dst_host, const void* src_device, size_t bytes);
+/* stream-ordered device copy */
+int ullis_hip_copy(ullis_hip_ctx* ctx, void* dst_device, const void* src_device, size_t bytes);
+/* Events on the context stream; slot in [0, 16). */
+int ullis_hip_event_record(ullis_hip_ctx* ctx, int slot);
+int ullis_hip_event_elapsed_ms(ullis_hip_ctx* ctx, int start_slot, int end_slot, float* ms);
+
+/* ---- unit operations ---- */
+
+/* MetalRuntime::layer_norm, src/metal.rs:1590-1626. x fp32 [rows, channels];
+ * weight/bias f16 [channels]; writes y32 and/or y16 (either may be NULL). */
+int ullis_hip_layer_norm(ullis_hip_ctx* ctx, const float* x, const uint16_t* weight,
+                         const uint16_t* bias, size_t rows, size_t channels, float* y32,
+                         uint16_t* y16);
+
+/* MetalRuntime::layer_norm_backward, src/metal.rs:1628-1703. */
+int ullis_hip_layer_norm_backward(ullis_hip_ctx* ctx, const float* x, const float* gy,
+                                  const uint16_t* weight, size_t rows, size_t channels, float* gx,
+                                  float* gw, float* gb);
+
+/* MetalRuntime::binary_linear, src/metal.rs:1705-1751:
+ * y = bias + scale * (x . S^T). x is [rows, in] of x_dtype (ULLIS_HIP_F16 or
+ * ULLIS_HIP_F32); bias may be NULL; y32 / y16 may be NULL. */
+int ullis_hip_binary_linear(ullis_hip_ctx* ctx, const void* x, int x_dtype, const uint32_t* bits,
+                            const uint16_t* scale, const uint16_t* bias, size_t rows, size_t in,
+                            size_t out, float* y32, uint16_t* y16);
+
+/* MetalRuntime::binary_linear_backward, src/metal.rs:2578-2682 (the STE of
+ * PackedBinaryLinear::backward_ste, src/model.rs:745-796): gx, gw, g_scale and
+ * (has_bias) g_bias, all overwritten, fp32. x fp16 [rows, in], gy fp32 [rows, out].
+ * gx / g_bias may be NULL. */
+int ullis_hip_binary_linear_backward(ullis_hip_ctx* ctx, const uint16_t* x16, const float* gy,
+                                     const uint32_t* bits, const uint16_t* scale, int has_bias,
+                                     size_t rows, size_t in, size_t out, float* gx, float* gw,
+                                     float* g_scale, float* g_bias);
+
+/* MetalRuntime::apply_latent_sgd, src/metal.rs:3006-3051: BinaryConnect step
+ * on latent/residual with gradient * ste_scale, then bits = latent >= 0
+ * (and bits_t, the [in, out] transpose bits, when non-NULL). In place. */
+int ullis_hip_apply_latent_sgd(ullis_hip_ctx* ctx, uint16_t* latent, float* residual,
+                               const float* gradient, size_t out, size_t in, float learning_rate,
+                               float ste_scale, uint32_t* bits, uint32_t* bits_t);
+
+/* MetalRuntime::fp16_linear, src/metal.rs:2790-2827: y = x . W^T, W f16 [out, in]. */
+int ullis_hip_fp16_linear(ullis_hip_ctx* ctx, const void* x, int x_dtype, const uint16_t* w,
+                          size_t rows, size_t in, size_t out, float* y32, uint16_t* y16);
+
+/* MetalRuntime::fp16_linear_backward, src/metal.rs:2829-2908: gx = gy . W,
+ * gw = gy^T . x (fp32, overwritten). gx may be NULL. */
+int ullis_hip_fp16_linear_backward(ullis_hip_ctx* ctx, const uint16_t* x16, const float* gy,
+                                   const uint16_t* w, size_t rows, size_t in, size_t out,
+                                   float* gx, float* gw);
+
+/* MetalRuntime::clipped_sgd_fp16 / binaryconnect_sgd_fp16, src/metal.rs:3053-3102. In place. */
+int ullis_hip_clipped_sgd_fp16(ullis_hip_ctx* ctx, uint16_t* params, float* residual,
+                               const float* gradient, size_t n, float learning_rate);
+int ullis_hip_binaryconnect_sgd_fp16(ullis_hip_ctx* ctx, uint16_t* params, float* residual,
+                                     const float* gradient, size_t n, float learning_rate);
+
+/* MetalRuntime::sign_pack_bits (kernel ullis_sign_pack_bits, rwkv8.metal:112-129):
+ * bit i = x[i] > 0, LSB-first. */
+int ullis_hip_sign_pack_bits(ullis_hip_ctx* ctx, const float* x, size_t n, uint32_t* bits);
+
+/* No reference counterpart: bits of the [in, out] transpose of a packed
+ * [out, in] matrix (the GPU input-gradient operand). */
+int ullis_hip_transpose_bits(ullis_hip_ctx* ctx, const uint32_t* bits, size_t out, size_t in,
+                             uint32_t* bits_t);
+
+/* MetalRuntime::packed_head_train_sgd, src/metal.rs:3300-3510, as driven by
+ * UllisHeron::apply_head_ce (src/model.rs:3145-3193): next-token CE over the
+ * packed head with horizon 1, streamed over vocab tiles (no [rows, vocab]
+ * buffer), then the head update: BinaryConnect latent step (ste_scale),
+ * scale clipped SGD at learning_rate and bias clipped SGD at 8 x learning_rate,
+ * then bits / bits_t repack. learning_rate == 0 computes gradients only.
+ * stats4 (device) receives {mean_loss, n_valid, gradient_scale, loss_sum}.
+ * g_scale / g_bias / g_w (device, optional) receive the gradients. */
+int ullis_hip_packed_head_train_sgd(ullis_hip_ctx* ctx, const uint16_t* hidden16, uint32_t* bits,
+                                    uint32_t* bits_t, uint16_t* scale, uint16_t* bias,
+                                    uint16_t* latent, float* latent_residual,
+                                    float* scale_residual, float* bias_residual,
+                                    const uint32_t* targets, size_t rows, size_t time, size_t d,
+                                    size_t vocab, uint32_t ignore_id, float learning_rate,
+                                    float ste_scale, float* row_loss, float* stats4,
+                                    float* g_hidden, float* g_scale, float* g_bias, float* g_w);
+
+/* ---- one Heron train step on the device (UllisHeron::train_step_on,
+ *      src/model.rs:2827-3025, metal branch; rosa_grad = stop_grad_bits) ---- */
+
+/* The parameter arena follows ullis_heron_layout.h. */
+size_t ullis_hip_heron_layout(const ullis_heron_dims* dims, ullis_tensor_desc* out, size_t cap,
+                              uint64_t* bytes);
+int ullis_hip_heron_create(ullis_hip_ctx* ctx, const ullis_heron_dims* dims, size_t batch,
+                           size_t time, ullis_hip_heron** out);
+void ullis_hip_heron_destroy(ullis_hip_heron* h);
+/* Device pointer and byte size of the arena. */
+int ullis_hip_heron_arena(ullis_hip_heron* h, void** device_ptr, uint64_t* bytes);
+/* Rebuilds every derived "<prefix>.bits_t" from "<prefix>.bits" (after an upload). */
+int ullis_hip_heron_refresh_derived(ullis_hip_heron* h);
+/*
+ * One step from the gathered embedding rows x_emb (fp32 [batch*time, d]) to
+ * the embedding-row gradient g_emb (fp32, same shape); the embedding gather and
+ * scatter stay with the caller, as in the reference's GPU path
+ * (src/model.rs:2866-2873, 2986-2993). labels u32 [batch*time]. rosa_idx is the
+ * suffix-automaton output per layer, channel-major u8 [n_layers][batch][d][time]
+ * (rosa_qkv_batch_packed_channel_major, src/rosa.rs:486-513). Outputs (device):
+ * row_loss fp32 [batch*time]; stats4 {mean_loss, n_valid, gscale, loss_sum};
+ * qkv_bits (may be NULL) u32 [n_layers][3][ceil(batch*time*d/32)], the Q/K/V
+ * sign bit-planes handed to the automaton. All pointers are device pointers.
+ */
+int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels,
+                         uint32_t ignore_id, float learning_rate, const uint8_t* rosa_idx,
+                         float* g_emb, float* row_loss, float* stats4, uint32_t* qkv_bits);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ULLIS_HIP_H */

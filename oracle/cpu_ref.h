@@ -1,0 +1,122 @@
+/*
+ * cpu_ref: TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C restatement of the reference's deterministic CPU backend for the
+ * packed +-1 linear / LayerNorm / streamed-CE hot path (Vladislav-Kalinkin/ullis
+ * 0.10.0, src/precision.rs and src/model.rs). It is the parity oracle for the
+ * HIP library and the CPU throughput baseline in bench.py. Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it; the
+ * product path never calls it.
+ *
+ * Conventions: activations f32, FP16 parameters as raw u16 bit patterns, FP32
+ * carries, packed sign bits as LSB-first u32 words. Every loop keeps the
+ * reference's order of f32 operations (Rust never contracts a*b+c into an
+ * FMA; this file is compiled with -ffp-contract=off).
+ *
+ * Parity pins: see the header of cpu_ref.c for which check pins which function.
+ */
+#ifndef ULLIS_CPU_REF_H
+#define ULLIS_CPU_REF_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../include/ullis_heron_layout.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* a1: IEEE binary16 */
+uint16_t ucr_f16_from_f32(float value);
+float ucr_f16_to_f32(uint16_t bits);
+void ucr_f16_from_f32_array(const float* src, uint16_t* dst, size_t n);
+void ucr_f16_to_f32_array(const uint16_t* src, float* dst, size_t n);
+
+/* a2 / a3: FP16 storage updates with FP32 carry (per element, in order) */
+void ucr_clipped_sgd(uint16_t* values, float* residual, const float* gradient, size_t n,
+                     float learning_rate);
+void ucr_binaryconnect_sgd(uint16_t* values, float* residual, const float* gradient, size_t n,
+                           float learning_rate, float gradient_scale);
+
+/* a4: bit packing */
+size_t ucr_packed_word_count(size_t weights);
+void ucr_pack_latent_bits(const uint16_t* latent, size_t n, uint32_t* bits);
+void ucr_sign_pack_bits(const float* x, size_t n, uint32_t* bits);
+void ucr_transpose_bits(const uint32_t* bits, size_t out, size_t in, uint32_t* bits_t);
+size_t ucr_bit_flip_count(const uint32_t* before, const uint32_t* after, size_t words);
+
+/* a5-a8: packed +-1 linear */
+int ucr_packed_forward(const float* x, size_t rows, size_t in, size_t out, const uint32_t* bits,
+                       const uint16_t* scale, const uint16_t* bias, float* y);
+int ucr_packed_backward_ste(const float* x, const float* gy, size_t rows, size_t in, size_t out,
+                            const uint32_t* bits, const uint16_t* scale, float* g_w, float* g_x,
+                            float* g_scale, float* g_bias);
+/* a9: latent BinaryConnect SGD, then scale and bias clipped SGD, then rebinarize */
+int ucr_packed_apply_sgd(size_t in, size_t out, uint16_t* latent, float* latent_res,
+                         uint16_t* scale, float* scale_res, uint16_t* bias, float* bias_res,
+                         uint32_t* bits, const float* g_w, const float* g_scale,
+                         const float* g_bias, float learning_rate, float ste_scale);
+
+/* a10 / a11: LayerNorm */
+int ucr_layer_norm_forward(const float* x, size_t rows, size_t ch, const uint16_t* weight,
+                           const uint16_t* bias, float* y);
+int ucr_layer_norm_backward(const float* x, const float* gy, size_t rows, size_t ch,
+                            const uint16_t* weight, float* gx, float* gw, float* gb);
+
+/* a12 */
+int ucr_causal_ce_row_valid(size_t row, size_t time, size_t horizon, const uint32_t* targets,
+                            size_t n_targets, uint32_t ignore_id);
+float ucr_causal_ce_gradient_scale(size_t n_valid, size_t time);
+
+/* a13: packed head + next-token CE (CPU branch of apply_head_ce), no update */
+int ucr_head_ce(const float* hidden, size_t rows, size_t time, size_t d, size_t vocab,
+                const uint32_t* bits, const uint16_t* scale, const uint16_t* bias,
+                const uint32_t* targets, uint32_t ignore_id, float* mean_loss, size_t* n_valid,
+                float* row_loss, float* g_hidden, float* g_w, float* g_scale, float* g_bias);
+
+/* a14: FP16 linear (CMix value) */
+int ucr_fp16_forward(const float* x, size_t rows, size_t in, size_t out, const uint16_t* w,
+                     float* y);
+int ucr_fp16_backward(const float* x, const float* gy, size_t rows, size_t in, size_t out,
+                      const uint16_t* w, float* g_x, float* g_w);
+
+/* a15: CMix pieces */
+int ucr_time_shift_delta(const float* x, size_t batch, size_t time, size_t ch, float* xx);
+int ucr_lerp_shift_backward(const float* xx, const uint16_t* mix, const float* g_shifted,
+                            size_t batch, size_t time, size_t ch, float* g_x, float* g_mix);
+
+/* a16: ROSA output expansion and e gradient */
+int ucr_rosa_y_from_idx(const uint8_t* idx, const uint16_t* e, size_t rows, size_t ch, float* y);
+int ucr_rosa_e_grad(const float* g_y, const uint8_t* idx, size_t rows, size_t ch, float* g_e);
+
+/* a17: one Heron train step on the parameter arena, embedding excluded */
+typedef struct ucr_step_stats {
+  float mean_loss;
+  uint64_t n_valid;
+  uint64_t flips_head;
+  uint64_t flips_cmix;
+  uint64_t flips_rosa_o;
+} ucr_step_stats;
+
+int ucr_heron_train_step(const ullis_heron_dims* dims, uint8_t* arena, const float* x_emb,
+                         const uint32_t* labels, uint32_t ignore_id, size_t batch, size_t time,
+                         float learning_rate, const uint8_t* rosa_idx, float* g_emb,
+                         float* row_loss, uint32_t* qkv_bits, ucr_step_stats* stats);
+
+/* Embedding gather and sequential scatter SGD (src/model.rs:2866-2873, 2986-2993). */
+int ucr_embedding_gather(const uint16_t* table, size_t d, const uint32_t* tokens, size_t rows,
+                         float* x);
+int ucr_embedding_scatter_sgd(uint16_t* table, float* residual, size_t d,
+                              const uint32_t* tokens, size_t rows, const float* g_x,
+                              float learning_rate);
+
+/* Exported copy of the arena layout for ctypes callers. */
+size_t ucr_heron_layout(const ullis_heron_dims* dims, ullis_tensor_desc* out, size_t cap,
+                        uint64_t* bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ULLIS_CPU_REF_H */

@@ -1,0 +1,290 @@
+"""GPU parity of the unit operations against the CPU oracle, through the C ABI.
+
+Tolerances: bit-exact for sign packing and
+the FP16 / BinaryConnect SGD updates on identical inputs; relative error
+max|gpu - ref| / max|ref| <= 1e-3 per tensor for fp16 linear / LayerNorm
+outputs and gradients (the GPU feeds fp16 operands to MFMA with fp32
+accumulation; the oracle computes in fp32 on the same fp16-rounded inputs).
+"""
+import numpy as np
+import pytest
+
+from oracle import cpu_ref as o
+from ullis_amd.synth import f16, pack_bits
+
+pytestmark = pytest.mark.gpu
+
+REL = 1e-3
+
+
+def rel(a, r):
+    a = np.asarray(a, np.float64)
+    r = np.asarray(r, np.float64)
+    assert a.shape == r.shape
+    assert np.isfinite(a).all()
+    denom = max(float(np.max(np.abs(r))), 1e-30)
+    return float(np.max(np.abs(a - r))) / denom
+
+
+def h2f32(bits):
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float32)
+
+
+def rand_case(rng, rows, in_f, out_f, bias=True):
+    x16 = f16(rng.standard_normal(rows * in_f))
+    lat = rng.uniform(-0.01, 0.01, out_f * in_f)
+    bits = pack_bits(lat >= 0)
+    scale = f16(rng.uniform(0.005, 0.02, out_f))
+    b = f16(rng.normal(0, 0.01, out_f)) if bias else None
+    return x16, bits, scale, b
+
+
+# ------------------------------------------------------------ packed linear
+def test_binary_linear_metal_fixture(rt):
+    # binary_linear_matches_packed_cpu_forward_and_ste, src/metal.rs:3806-3844
+    signs = [1, -1, -1, 1, 1, 1]
+    bits = pack_bits(np.array(signs) >= 0)
+    x = np.array([0.5, -1.0, 2.0, 1.0, 0.0, -0.5], np.float32)
+    scale, bias = f16([0.5, 0.5]), f16([0.0, 0.0])
+    y = rt.binary_linear(x, bits, scale, bias, 2, 3, 2)
+    want = o.packed_forward(x, 2, 3, 2, bits, scale, bias)
+    np.testing.assert_allclose(y, want, atol=2e-3)
+    gy = np.array([1.0, -0.5, 0.25, 0.75], np.float32)
+    g = rt.binary_linear_backward(f16(x), gy, bits, scale, True, 2, 3, 2)
+    w = o.packed_backward_ste(x, gy, 2, 3, 2, bits, scale)
+    for k in ["input_gradient", "weight_gradient", "scale_gradient", "bias_gradient"]:
+        np.testing.assert_allclose(g[k], w[k], atol=2e-3, err_msg=k)
+
+
+def test_binary_linear_tiled_fixture_past_tile_boundary(rt):
+    # tiled_linears_match_cpu_past_tile_boundary, src/metal.rs:3908-3974 (rows 17, in 19, out 18)
+    rows, inn, out = 17, 19, 18
+    signs = np.array([[1 if (a + i) % 2 == 0 else -1 for i in range(inn)] for a in range(out)])
+    x = np.array([[((r * 5 + i) % 11) * 0.125 - 0.5 for i in range(inn)] for r in range(rows)],
+                 np.float32).ravel()
+    gy = np.array([[((r + a) % 5) * 0.2 - 0.4 for a in range(out)] for r in range(rows)],
+                  np.float32).ravel()
+    bits = pack_bits((signs >= 0).ravel())
+    scale, bias = f16([0.5] * out), f16([0.0] * out)
+    y = rt.binary_linear(x, bits, scale, bias, rows, inn, out)
+    np.testing.assert_allclose(y, o.packed_forward(x, rows, inn, out, bits, scale, bias), atol=3e-3)
+    g = rt.binary_linear_backward(f16(x), gy, bits, scale, True, rows, inn, out)
+    w = o.packed_backward_ste(x, gy, rows, inn, out, bits, scale)
+    for k in ["input_gradient", "weight_gradient", "scale_gradient", "bias_gradient"]:
+        np.testing.assert_allclose(g[k], w[k], atol=4e-3, err_msg=k)
+    weight = f16(np.array([[((a * 3 + i) % 7) * 0.25 - 0.5 for i in range(inn)]
+                           for a in range(out)]).ravel())
+    np.testing.assert_allclose(rt.fp16_linear(x, weight, rows, inn, out),
+                               o.fp16_forward(x, rows, inn, out, weight), atol=3e-3)
+    gx, gw = rt.fp16_linear_backward(f16(x), gy, weight, rows, inn, out)
+    wgx, wgw = o.fp16_backward(x, gy, rows, inn, out, weight)
+    np.testing.assert_allclose(gx, wgx, atol=4e-3)
+    np.testing.assert_allclose(gw, wgw, atol=4e-3)
+
+
+SHAPES = [
+    (2048, 256, 256),   # config 1 (TrainConfig::default layer)
+    (2048, 512, 512),   # heron QKVO
+    (2048, 512, 2048),  # heron CMix key
+    (100, 96, 70),      # ragged, multi-tile
+    (64, 40, 96),       # in not a multiple of 32 (unaligned sign rows)
+]
+
+
+@pytest.mark.parametrize("rows,in_f,out_f", SHAPES)
+def test_binary_linear_forward_parity(rt, rows, in_f, out_f):
+    rng = np.random.default_rng(rows + in_f + out_f)
+    x16, bits, scale, bias = rand_case(rng, rows, in_f, out_f)
+    want = o.packed_forward(h2f32(x16), rows, in_f, out_f, bits, scale, bias)
+    y32 = rt.binary_linear(x16, bits, scale, bias, rows, in_f, out_f)
+    assert rel(y32, want) <= REL
+    y16 = rt.binary_linear(x16, bits, scale, bias, rows, in_f, out_f, out_dtype=np.float16)
+    assert rel(h2f32(y16), want) <= REL
+    # fp32 activations accepted too (converted on load)
+    yf = rt.binary_linear(h2f32(x16), bits, scale, None, rows, in_f, out_f, x_dtype=2)
+    assert rel(yf, o.packed_forward(h2f32(x16), rows, in_f, out_f, bits, scale, None)) <= REL
+
+
+@pytest.mark.parametrize("rows,in_f,out_f", SHAPES)
+def test_binary_linear_backward_parity(rt, rows, in_f, out_f):
+    rng = np.random.default_rng(7 + rows + in_f + out_f)
+    x16, bits, scale, _ = rand_case(rng, rows, in_f, out_f)
+    gy = rng.normal(0, 1e-2, rows * out_f).astype(np.float32)
+    g = rt.binary_linear_backward(x16, gy, bits, scale, True, rows, in_f, out_f)
+    w = o.packed_backward_ste(h2f32(x16), gy, rows, in_f, out_f, bits, scale)
+    for k in ["input_gradient", "weight_gradient", "scale_gradient", "bias_gradient"]:
+        assert rel(g[k], w[k]) <= REL, k
+
+
+@pytest.mark.parametrize("rows,in_f,out_f", [(2048, 2048, 512), (2048, 512, 2048), (50, 24, 40)])
+def test_fp16_linear_parity(rt, rows, in_f, out_f):
+    rng = np.random.default_rng(11 + rows + in_f)
+    x16 = f16(np.maximum(rng.standard_normal(rows * in_f), 0) ** 2)
+    w = f16(rng.normal(0, 0.02, out_f * in_f))
+    want = o.fp16_forward(h2f32(x16), rows, in_f, out_f, w)
+    assert rel(rt.fp16_linear(x16, w, rows, in_f, out_f), want) <= REL
+    gy = rng.normal(0, 1e-2, rows * out_f).astype(np.float32)
+    gx, gw = rt.fp16_linear_backward(x16, gy, w, rows, in_f, out_f)
+    wgx, wgw = o.fp16_backward(h2f32(x16), gy, rows, in_f, out_f, w)
+    assert rel(gx, wgx) <= REL
+    assert rel(gw, wgw) <= REL
+
+
+# -------------------------------------------------------------- LayerNorm
+def test_layer_norm_metal_fixtures(rt):
+    # src/metal.rs:3773-3803
+    w, b = f16([1.25, 0.75, 1.0, 0.5]), f16([0.1, -0.2, 0.0, 0.05])
+    x = np.array([1.0, 2.0, 3.0, 4.0, 0.5, -1.0, 0.0, 2.5], np.float32)
+    np.testing.assert_allclose(rt.layer_norm(x, w, b, 2, 4), o.layer_norm_forward(x, 2, 4, w, b),
+                               atol=2e-3)
+    x = np.array([1.0, 2.0, 0.0, -1.0, 4.0, 1.0, -2.0, 0.5], np.float32)
+    gy = np.array([0.2, -0.1, 0.3, 0.0, -0.4, 0.15, 0.05, -0.2], np.float32)
+    wt = f16([1.0, 0.5, 1.5, 0.75])
+    got = rt.layer_norm_backward(x, gy, wt, 2, 4)
+    want = o.layer_norm_backward(x, gy, 2, 4, wt)
+    for a, r in zip(got, want):
+        np.testing.assert_allclose(a, r, atol=3e-3)
+
+
+@pytest.mark.parametrize("rows,ch", [(2048, 256), (2048, 512), (4096, 1024), (37, 19), (5, 2000)])
+def test_layer_norm_parity(rt, rows, ch):
+    rng = np.random.default_rng(rows * 3 + ch)
+    x = (rng.standard_normal(rows * ch) * 3 + 0.5).astype(np.float32)
+    w, b = f16(rng.uniform(0.5, 1.5, ch)), f16(rng.normal(0, 0.1, ch))
+    want = o.layer_norm_forward(x, rows, ch, w, b)
+    assert rel(rt.layer_norm(x, w, b, rows, ch), want) <= REL
+    assert rel(h2f32(rt.layer_norm(x, w, b, rows, ch, out_dtype=np.float16)), want) <= REL
+    gy = rng.normal(0, 1e-2, rows * ch).astype(np.float32)
+    got = rt.layer_norm_backward(x, gy, w, rows, ch)
+    ref = o.layer_norm_backward(x, gy, rows, ch, w)
+    for a, r, name in zip(got, ref, ["gx", "gw", "gb"]):
+        assert rel(a, r) <= REL, name
+
+
+# ---------------------------------------------------------- bit-exact ops
+def test_sgd_metal_fixtures_bit_exact(rt):
+    # src/metal.rs:4007-4042
+    p, r = rt.clipped_sgd_fp16(f16([0.25, -1.0, 2.0]), np.zeros(3, np.float32),
+                               np.array([0.001, 0.5, -0.25], np.float32), 0.01)
+    wp, wr = o.clipped_sgd(f16([0.25, -1.0, 2.0]), np.zeros(3), [0.001, 0.5, -0.25], 0.01)
+    np.testing.assert_array_equal(p, wp)
+    np.testing.assert_array_equal(r.view(np.uint32), wr.view(np.uint32))
+    p, r = rt.binaryconnect_sgd_fp16(f16([0.0625, -0.0625, 0.9]), np.zeros(3, np.float32),
+                                     np.array([1e-5, -1e-6, 2.0], np.float32), 0.1)
+    wp, wr = o.binaryconnect_sgd(f16([0.0625, -0.0625, 0.9]), np.zeros(3), [1e-5, -1e-6, 2.0], 0.1)
+    np.testing.assert_array_equal(p, wp)
+    np.testing.assert_array_equal(r.view(np.uint32), wr.view(np.uint32))
+
+
+@pytest.mark.parametrize("lr", [0.01, 0.1])
+def test_sgd_random_bit_exact(rt, lr):
+    rng = np.random.default_rng(int(lr * 1000))
+    n = 1 << 20
+    p = f16(rng.uniform(-1.2, 1.2, n) * (10.0 ** rng.integers(-6, 1, n)))
+    res = (rng.standard_normal(n) * 1e-5).astype(np.float32)
+    g = (rng.standard_normal(n) * (10.0 ** rng.integers(-7, 2, n))).astype(np.float32)
+    g[::97] = 0.0
+    g[::101] = np.inf
+    g[::103] = np.nan
+    gc = np.nan_to_num(g, posinf=3.0, nan=0.5)
+    a, b = rt.clipped_sgd_fp16(p, res, gc, lr)
+    wa, wb = o.clipped_sgd(p, res, gc, lr)
+    np.testing.assert_array_equal(a, wa)
+    np.testing.assert_array_equal(b.view(np.uint32), wb.view(np.uint32))
+    a, b = rt.binaryconnect_sgd_fp16(p, res, g, lr)
+    wa, wb = o.binaryconnect_sgd(p, res, g, lr)
+    np.testing.assert_array_equal(a, wa)
+    np.testing.assert_array_equal(b.view(np.uint32), wb.view(np.uint32))
+
+
+@pytest.mark.parametrize("out_f,in_f", [(512, 512), (2048, 512), (18, 19), (8192, 512)])
+def test_apply_latent_sgd_bit_exact(rt, out_f, in_f):
+    rng = np.random.default_rng(out_f + in_f)
+    n = out_f * in_f
+    lat = f16(rng.uniform(-0.01, 0.01, n))
+    lat[:4] = [0x0000, 0x8000, 0x0001, 0x8001]
+    res = np.zeros(n, np.float32)
+    g = (rng.standard_normal(n) * 1e-5).astype(np.float32)
+    g[5::7] = 0.0
+    gl, gr, bits, bits_t = rt.apply_latent_sgd(lat, res, g, out_f, in_f, 0.01, 2047.0)
+    wl, wr = o.binaryconnect_sgd(lat, res, g, 0.01, 2047.0)
+    np.testing.assert_array_equal(gl, wl)
+    np.testing.assert_array_equal(gr.view(np.uint32), wr.view(np.uint32))
+    wbits = o.pack_latent_bits(wl)
+    np.testing.assert_array_equal(bits, wbits)
+    np.testing.assert_array_equal(bits_t, o.transpose_bits(wbits, out_f, in_f))
+
+
+@pytest.mark.parametrize("n", [1, 31, 32, 33, 1000, 2048 * 512])
+def test_sign_pack_bits_bit_exact(rt, n):
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal(n).astype(np.float32)
+    x[::13] = 0.0
+    x[1::17] = -0.0
+    np.testing.assert_array_equal(rt.sign_pack_bits(x), o.sign_pack_bits(x))
+
+
+@pytest.mark.parametrize("out_f,in_f", [(512, 512), (8192, 512), (18, 19), (96, 40)])
+def test_transpose_bits_bit_exact(rt, out_f, in_f):
+    bits = pack_bits(np.random.default_rng(out_f).integers(0, 2, out_f * in_f).astype(bool))
+    np.testing.assert_array_equal(rt.transpose_bits(bits, out_f, in_f),
+                                  o.transpose_bits(bits, out_f, in_f))
+
+
+# -------------------------------------------------------------- head + CE
+def test_head_ce_metal_fixture(rt):
+    # streamed_cross_entropy_matches_cpu_oracle_without_materializing_on_gpu, src/metal.rs:4045-4085
+    signs = [1, -1, 1, -1, -1, 1, 1, 1]
+    bits = pack_bits(np.array(signs) >= 0)
+    hidden = np.array([0.5, -0.25, 1.0, 0.0, -0.5, 0.75], np.float32)
+    tokens = np.array([1, 3, 0], np.uint32)
+    scale = f16([0.5] * 4)
+    lat = f16(np.where(np.array(signs) >= 0, 0.5, -0.5))
+    got = rt.packed_head_train_sgd(f16(hidden), bits, scale, None, lat, np.zeros(8, np.float32),
+                                   np.zeros(4, np.float32), None, tokens, 3, 3, 2, 4,
+                                   0xFFFFFFFF, 0.0, 1.0, want_g_w=True)
+    want = o.head_ce(hidden, 3, 3, 2, 4, bits, scale, None, tokens, 0xFFFFFFFF)
+    assert abs(got["mean_loss"] - want["mean_loss"]) < 3e-3
+    assert got["row_loss"][2] == 0.0
+    np.testing.assert_allclose(got["hidden_gradient"], want["hidden_gradient"], atol=5e-3)
+    np.testing.assert_allclose(got["scale_gradient"], want["scale_gradient"], atol=5e-3)
+    np.testing.assert_allclose(got["weight_gradient"], want["weight_gradient"], atol=5e-3)
+
+
+@pytest.mark.parametrize("rows,time,d,vocab,ignore", [
+    (256, 64, 64, 1000, 0xFFFFFFFF),
+    (512, 128, 128, 2500, 7),
+    (256, 256, 512, 8192, 0xFFFFFFFF),  # config 3 widths (d 512, vocab 8192), 256 rows
+])
+def test_head_ce_parity_and_update(rt, rows, time, d, vocab, ignore):
+    rng = np.random.default_rng(rows + d + vocab)
+    hidden16 = f16(rng.standard_normal(rows * d))
+    lat = f16(rng.uniform(-0.01, 0.01, vocab * d))
+    bits = pack_bits(h2f32(lat) >= 0)
+    scale = f16(rng.uniform(0.005, 0.02, vocab))
+    bias = f16(rng.normal(0, 0.01, vocab))
+    targets = rng.integers(0, vocab, rows).astype(np.uint32)
+    if ignore != 0xFFFFFFFF:
+        targets[::5] = ignore
+    lr, ste = 0.01, float(time - 1)
+    got = rt.packed_head_train_sgd(hidden16, bits, scale, bias, lat, np.zeros(vocab * d, np.float32),
+                                   np.zeros(vocab, np.float32), np.zeros(vocab, np.float32),
+                                   targets, rows, time, d, vocab, ignore, lr, ste, want_g_w=True)
+    want = o.head_ce(h2f32(hidden16), rows, time, d, vocab, bits, scale, bias, targets, ignore)
+    assert got["n_valid"] == want["n_valid"]
+    assert abs(got["mean_loss"] - want["mean_loss"]) <= 1e-4
+    assert np.max(np.abs(got["row_loss"] - want["row_loss"])) <= 1e-4
+    for k in ["hidden_gradient", "scale_gradient", "bias_gradient", "weight_gradient"]:
+        assert rel(got[k], want[k]) <= REL, k
+    # The update applied to the GPU's own gradients is bit-exact with the oracle's
+    # update rules (head: latent step, scale at lr, bias at 8 lr; src/model.rs:3118-3193).
+    wl, wlr = o.binaryconnect_sgd(lat, np.zeros(vocab * d), got["weight_gradient"], lr, ste)
+    np.testing.assert_array_equal(got["next_latent"], wl)
+    np.testing.assert_array_equal(got["next_residual"].view(np.uint32), wlr.view(np.uint32))
+    ws, _ = o.clipped_sgd(scale, np.zeros(vocab), got["scale_gradient"], lr)
+    np.testing.assert_array_equal(got["next_scale"], ws)
+    wb, _ = o.clipped_sgd(bias, np.zeros(vocab), got["bias_gradient"], lr * 8.0)
+    np.testing.assert_array_equal(got["next_bias"], wb)
+    wbits = o.pack_latent_bits(wl)
+    np.testing.assert_array_equal(got["next_bits"], wbits)
+    np.testing.assert_array_equal(got["next_bits_t"], o.transpose_bits(wbits, vocab, d))

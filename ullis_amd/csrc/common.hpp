@@ -1,0 +1,128 @@
+// Shared device helpers for the gfx950 kernels of libullis_hip.
+//
+// Numeric contract (matches the reference CPU backend, src/precision.rs):
+//  - f32 -> f16 conversion is IEEE round-to-nearest-even with subnormals
+//    (v_cvt_f16_f32 in the default RNE mode; f16 denormals are not flushed);
+//  - SGD updates evaluate (current - lr*clamp(g)) + residual with two
+//    roundings, never an FMA: every translation unit is built with
+//    -ffp-contract=off.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ullis {
+
+typedef _Float16 half_t;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLayerNormEps = 1e-5f;  // src/model.rs:132
+constexpr float kHeadBiasLrMult = 8.0f;  // src/model.rs:97
+
+// Dynamic power-of-two scaling of fp32 gradients that feed fp16 MFMA operands:
+// amax * scale lands in [2^(kGradTargetExp-1), 2^kGradTargetExp). The scale is
+// exact, so dividing it back out in an epilogue is exact.
+constexpr int kGradTargetExp = 6;
+
+__device__ __forceinline__ float grad_scale_from_amax(float amax) {
+  if (!(amax > 0.0f) || !__builtin_isfinite(amax)) return 1.0f;
+  int e;
+  (void)__builtin_frexpf(amax, &e);  // amax = m * 2^e, m in [0.5, 1)
+  return __builtin_ldexpf(1.0f, kGradTargetExp - e);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
+  half_t h = (half_t)v;
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
+  return (float)__builtin_bit_cast(half_t, b);
+}
+
+// Saturating conversion for scaled gradients: never produces inf.
+__device__ __forceinline__ half_t f32_to_f16_sat(float v) {
+  v = __builtin_fminf(__builtin_fmaxf(v, -65504.0f), 65504.0f);
+  return (half_t)v;
+}
+
+__device__ __forceinline__ float clampf(float v, float lo, float hi) {
+  // f32::clamp semantics: NaN passes through.
+  return v < lo ? lo : (v > hi ? hi : v);
+}
+
+// Fp16Storage::apply_clipped_sgd, src/precision.rs:106-113.
+__device__ __forceinline__ void clipped_sgd_one(uint16_t& value, float& residual, float gradient,
+                                                float lr) {
+  const float current = f16_bits_to_f32(value);
+  const float update = lr * clampf(gradient, -1.0f, 1.0f);
+  const float desired = current - update + residual;
+  const uint16_t rounded = f32_to_f16_bits(desired);
+  residual = desired - f16_bits_to_f32(rounded);
+  value = rounded;
+}
+
+// Fp16Storage::apply_binaryconnect_sgd, src/precision.rs:124-134.
+// Returns false when the gradient was skipped (zero or non-finite).
+__device__ __forceinline__ bool binaryconnect_sgd_one(uint16_t& value, float& residual,
+                                                      float gradient, float lr) {
+  if (!__builtin_isfinite(gradient) || gradient == 0.0f) return false;
+  const float current = f16_bits_to_f32(value);
+  const float update = lr * clampf(gradient, -1.0f, 1.0f);
+  const float desired = clampf(current - update + residual, -1.0f, 1.0f);
+  const uint16_t rounded = f32_to_f16_bits(desired);
+  residual = desired - f16_bits_to_f32(rounded);
+  value = rounded;
+  return true;
+}
+
+// rebinarize (src/model.rs:878-884): latent >= 0.0, so -0.0 packs as +1.
+__device__ __forceinline__ bool latent_is_plus(uint16_t latent_bits) {
+  return f16_bits_to_f32(latent_bits) >= 0.0f;
+}
+
+// Wave64 reductions (no LDS).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Max over the 32 lanes of each half-wave (lanes 0-31 and 32-63 separately).
+__device__ __forceinline__ float halfwave_max(float v) {
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+__device__ __forceinline__ float halfwave_sum(float v) {
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Non-negative floats order like their bit patterns, so a u32 atomicMax on the
+// bits is an exact, order-independent max.
+__device__ __forceinline__ void atomic_amax(float* slot, float v) {
+  v = __builtin_fabsf(v);
+  if (!(v >= 0.0f)) v = __builtin_inff();  // NaN: poison the scale deliberately
+  atomicMax(reinterpret_cast<unsigned int*>(slot), __float_as_uint(v));
+}
+
+// Row/column of accumulator register r of a 32x32x16 MFMA tile held by `lane`:
+// column = lane % 32, row = 8*(r/4) + 4*(lane/32) + r%4.
+__device__ __forceinline__ int mfma32_row(int r, int lane) {
+  return ((r >> 2) << 3) + ((lane >> 5) << 2) + (r & 3);
+}
+
+}  // namespace ullis

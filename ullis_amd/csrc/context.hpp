@@ -1,0 +1,76 @@
+// Host-side context shared by the C ABI translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "ops.hpp"
+
+struct ullis_hip_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string err;
+  void* scratch = nullptr;
+  size_t scratch_bytes = 0;
+  hipEvent_t events[16] = {};
+
+  int fail(int code, const std::string& msg) {
+    err = msg;
+    return code;
+  }
+  int hip(hipError_t e, const char* what) {
+    if (e == hipSuccess) return 0;
+    err = std::string(what) + ": " + hipGetErrorString(e);
+    return -3;
+  }
+  // Grow-only scratch; waits for the stream before replacing the buffer.
+  int ensure_scratch(size_t bytes, void** out) {
+    if (bytes > scratch_bytes) {
+      if (scratch) {
+        if (int rc = hip(hipStreamSynchronize(stream), "scratch sync")) return rc;
+        if (int rc = hip(hipFree(scratch), "scratch free")) return rc;
+        scratch = nullptr;
+        scratch_bytes = 0;
+      }
+      const size_t want = (bytes + (1u << 20) - 1) / (1u << 20) * (1u << 20);
+      if (hipMalloc(&scratch, want) != hipSuccess) {
+        scratch = nullptr;
+        return fail(-4, "scratch allocation of " + std::to_string(want) + " bytes failed");
+      }
+      scratch_bytes = want;
+    }
+    *out = scratch;
+    return 0;
+  }
+};
+
+namespace ullis {
+
+// Carves 256-byte aligned sub-buffers from one allocation.
+struct Carver {
+  char* p;
+  size_t used = 0;
+  explicit Carver(void* base) : p(static_cast<char*>(base)) {}
+  template <class T>
+  T* take(size_t count) {
+    T* r = reinterpret_cast<T*>(p + used);
+    used += (count * sizeof(T) + 255) / 256 * 256;
+    return r;
+  }
+  static size_t bytes_for(size_t bytes) { return (bytes + 255) / 256 * 256; }
+};
+
+// Split-K factor for a weight-gradient GEMM [out, in] over `rows`.
+inline int dw_splits(long out, long in, long rows) {
+  long tiles = cdiv(out, 128) * cdiv(in, 128);
+  if (tiles < 240) tiles = cdiv(out, 64) * cdiv(in, 64);
+  long s = 256 / (tiles > 0 ? tiles : 1);
+  const long by_rows = rows / 256;
+  if (s > by_rows) s = by_rows;
+  if (s > 8) s = 8;
+  if (s < 1) s = 1;
+  return (int)s;
+}
+
+}  // namespace ullis

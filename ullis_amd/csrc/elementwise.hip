@@ -1,0 +1,234 @@
+// Element-wise and reduction kernels around the GEMMs (HBM-bound).
+//
+// Reference semantics:
+//   clipped SGD          Fp16Storage::apply_clipped_sgd   src/precision.rs:106-113
+//   BinaryConnect SGD    apply_binaryconnect_sgd          src/precision.rs:124-134
+//   sign bit-planes      bit_from_activation + pack_bitplane src/rosa.rs:372-374, 400-411
+//   time-shift mix       time_shift_delta + lerp          src/model.rs:186-212, 1049-1057, 1385-1396
+//   its backward         lerp_shift_backward              src/model.rs:1207-1240
+//   ROSA output          (2*idx-1)*e                      src/rosa.rs:614-639
+//   ROSA e gradient      rosa_e_grad                      src/model.rs:1608-1634
+// Column reductions (g_mix, g_e, g_bias) are two-stage with fixed-order
+// partial sums: deterministic, unlike the Metal float CAS atomics
+// (rwkv8.metal:12-25, :295-323).
+#include "common.hpp"
+#include "ops.hpp"
+
+namespace ullis {
+
+namespace {
+
+constexpr int kColChunkRows = 64;
+
+__global__ void fill_kernel(float* p, long n, float v) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+__global__ void clipped_sgd_kernel(uint16_t* values, float* residual, const float* grad, long n,
+                                   float lr) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) clipped_sgd_one(values[i], residual[i], grad[i], lr);
+}
+
+__global__ void binaryconnect_sgd_kernel(uint16_t* values, float* residual, const float* grad,
+                                         long n, float lr, float grad_scale) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) binaryconnect_sgd_one(values[i], residual[i], grad[i] * grad_scale, lr);
+}
+
+__global__ void sign_pack_kernel(const float* x, long n, uint32_t* bits) {
+  const long w = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long base = w * 32;
+  if (base >= n) return;
+  uint32_t packed = 0;
+  for (int j = 0; j < 32; ++j) {
+    const long i = base + j;
+    if (i < n && x[i] > 0.0f) packed |= 1u << j;
+  }
+  bits[w] = packed;
+}
+
+__global__ __launch_bounds__(256) void amax_kernel(const float* x, long n, float* slot) {
+  float m = 0.0f;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (long)gridDim.x * blockDim.x)
+    m = __builtin_fmaxf(m, __builtin_fabsf(x[i]));
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) atomic_amax(slot, m);
+}
+
+// One thread per (row, 8-channel group) when ch % 8 == 0, else per element.
+__global__ void time_shift_mix_kernel(const uint16_t* x16, long rows, long time, long ch,
+                                      const uint16_t* mix0, uint16_t* out0,
+                                      const uint16_t* mix1, uint16_t* out1,
+                                      const uint16_t* mix2, uint16_t* out2, int group) {
+  const long gi = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long groups_per_row = ch / group;
+  const long row = gi / groups_per_row;
+  if (row >= rows) return;
+  const long c0 = (gi % groups_per_row) * group;
+  const long t = row % time;
+  for (int j = 0; j < group; ++j) {
+    const long idx = row * ch + c0 + j;
+    const float xt = f16_bits_to_f32(x16[idx]);
+    const float xx = t == 0 ? -xt : f16_bits_to_f32(x16[idx - ch]) - xt;
+    const long c = c0 + j;
+    if (out0) out0[idx] = f32_to_f16_bits(xt + xx * f16_bits_to_f32(mix0[c]));
+    if (out1) out1[idx] = f32_to_f16_bits(xt + xx * f16_bits_to_f32(mix1[c]));
+    if (out2) out2[idx] = f32_to_f16_bits(xt + xx * f16_bits_to_f32(mix2[c]));
+  }
+}
+
+// grid (ceil(ch/256), ceil(rows/64)); thread = one channel over a 64-row chunk.
+__global__ void time_shift_mix_bwd_kernel(const float* g_s, const uint16_t* x16,
+                                          const uint16_t* mix, long rows, long time, long ch,
+                                          float* g_x, float* part) {
+  const long c = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= ch) return;
+  const long r0 = (long)blockIdx.y * kColChunkRows;
+  const long r1 = r0 + kColChunkRows < rows ? r0 + kColChunkRows : rows;
+  const float m = f16_bits_to_f32(mix[c]);
+  float gm = 0.0f;
+  for (long row = r0; row < r1; ++row) {
+    const long idx = row * ch + c;
+    const long t = row % time;
+    const float gs = g_s[idx];
+    const float xt = f16_bits_to_f32(x16[idx]);
+    const float xx = t == 0 ? -xt : f16_bits_to_f32(x16[idx - ch]) - xt;
+    gm += gs * xx;
+    float gx = gs - gs * m;
+    if (t + 1 < time) gx = gx + g_s[idx + ch] * m;
+    g_x[idx] = gx;
+  }
+  part[(long)blockIdx.y * ch + c] = gm;
+}
+
+__global__ void column_sum_kernel(const float* v, const uint8_t* idx, long rows, long ch,
+                                  float* part) {
+  const long c = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= ch) return;
+  const long r0 = (long)blockIdx.y * kColChunkRows;
+  const long r1 = r0 + kColChunkRows < rows ? r0 + kColChunkRows : rows;
+  float s = 0.0f;
+  for (long row = r0; row < r1; ++row) {
+    const long i = row * ch + c;
+    const float x = v[i];
+    s += idx ? x * (2.0f * (float)idx[i] - 1.0f) : x;
+  }
+  part[(long)blockIdx.y * ch + c] = s;
+}
+
+__global__ void vector_finish_kernel(const float* part, int nblk, long ch, float* out, float lr,
+                                     uint16_t* values, float* residual) {
+  const long c = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= ch) return;
+  float s = 0.0f;
+  for (int k = 0; k < nblk; ++k) s += part[(long)k * ch + c];
+  if (out) out[c] = s;
+  if (values && lr > 0.0f) clipped_sgd_one(values[c], residual[c], s, lr);
+}
+
+__global__ void rosa_expand_kernel(const uint8_t* idx_cm, const uint16_t* e, long batch, long time,
+                                   long ch, uint16_t* y16, uint8_t* idx_rm) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long n = batch * time * ch;
+  if (i >= n) return;
+  const long c = i % ch;
+  const long row = i / ch;
+  const long b = row / time, t = row % time;
+  const uint8_t bit = idx_cm[(b * ch + c) * time + t];
+  const float y = (2.0f * (float)bit - 1.0f) * f16_bits_to_f32(e[c]);
+  y16[i] = f32_to_f16_bits(y);
+  if (idx_rm) idx_rm[i] = bit;
+}
+
+inline dim3 grid1d(long n, int threads = 256) { return dim3((unsigned)cdiv(n, threads)); }
+
+}  // namespace
+
+hipError_t fill_f32(hipStream_t s, float* p, long n, float v) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_kernel, grid1d(n), dim3(256), 0, s, p, n, v);
+  return hipGetLastError();
+}
+
+hipError_t clipped_sgd(hipStream_t s, uint16_t* values, float* residual, const float* grad, long n,
+                       float lr) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(clipped_sgd_kernel, grid1d(n), dim3(256), 0, s, values, residual, grad, n, lr);
+  return hipGetLastError();
+}
+
+hipError_t binaryconnect_sgd(hipStream_t s, uint16_t* values, float* residual, const float* grad,
+                             long n, float lr, float grad_scale) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(binaryconnect_sgd_kernel, grid1d(n), dim3(256), 0, s, values, residual, grad,
+                     n, lr, grad_scale);
+  return hipGetLastError();
+}
+
+hipError_t sign_pack_bits(hipStream_t s, const float* x, long n, uint32_t* bits) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(sign_pack_kernel, grid1d(cdiv(n, 32)), dim3(256), 0, s, x, n, bits);
+  return hipGetLastError();
+}
+
+hipError_t amax_f32(hipStream_t s, const float* x, long n, float* slot) {
+  if (n <= 0) return hipSuccess;
+  long blocks = cdiv(n, 256 * 8);
+  if (blocks > 1024) blocks = 1024;
+  hipLaunchKernelGGL(amax_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, n, slot);
+  return hipGetLastError();
+}
+
+hipError_t time_shift_mix(hipStream_t s, const uint16_t* x16, long rows, long time, long ch,
+                          const uint16_t* mix0, uint16_t* out0, const uint16_t* mix1,
+                          uint16_t* out1, const uint16_t* mix2, uint16_t* out2) {
+  if (rows <= 0 || ch <= 0 || time <= 0) return hipSuccess;
+  const int group = ch % 8 == 0 ? 8 : 1;
+  const long n = rows * (ch / group);
+  hipLaunchKernelGGL(time_shift_mix_kernel, grid1d(n), dim3(256), 0, s, x16, rows, time, ch, mix0,
+                     out0, mix1, out1, mix2, out2, group);
+  return hipGetLastError();
+}
+
+hipError_t time_shift_mix_backward(hipStream_t s, const float* g_shifted, const uint16_t* x16,
+                                   const uint16_t* mix, long rows, long time, long ch, float* g_x,
+                                   float* part, int* nblk_out) {
+  const long nblk = cdiv(rows, kColChunkRows);
+  if (nblk_out) *nblk_out = (int)nblk;
+  if (rows <= 0 || ch <= 0) return hipSuccess;
+  hipLaunchKernelGGL(time_shift_mix_bwd_kernel, dim3((unsigned)cdiv(ch, 256), (unsigned)nblk),
+                     dim3(256), 0, s, g_shifted, x16, mix, rows, time, ch, g_x, part);
+  return hipGetLastError();
+}
+
+hipError_t column_sum_partials(hipStream_t s, const float* v, const uint8_t* idx, long rows,
+                               long ch, float* part, int* nblk_out) {
+  const long nblk = cdiv(rows, kColChunkRows);
+  if (nblk_out) *nblk_out = (int)nblk;
+  if (rows <= 0 || ch <= 0) return hipSuccess;
+  hipLaunchKernelGGL(column_sum_kernel, dim3((unsigned)cdiv(ch, 256), (unsigned)nblk), dim3(256), 0,
+                     s, v, idx, rows, ch, part);
+  return hipGetLastError();
+}
+
+hipError_t vector_finish(hipStream_t s, const float* part, int nblk, long ch, float* out,
+                         float lr, uint16_t* values, float* residual) {
+  if (ch <= 0) return hipSuccess;
+  hipLaunchKernelGGL(vector_finish_kernel, grid1d(ch), dim3(256), 0, s, part, nblk, ch, out, lr,
+                     values, residual);
+  return hipGetLastError();
+}
+
+hipError_t rosa_expand(hipStream_t s, const uint8_t* idx_cm, const uint16_t* e, long batch,
+                       long time, long ch, uint16_t* y16, uint8_t* idx_rm) {
+  const long n = batch * time * ch;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rosa_expand_kernel, grid1d(n), dim3(256), 0, s, idx_cm, e, batch, time, ch,
+                     y16, idx_rm);
+  return hipGetLastError();
+}
+
+}  // namespace ullis

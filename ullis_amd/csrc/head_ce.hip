@@ -1,0 +1,340 @@
+// Packed vocab head fused with streamed next-token cross-entropy.
+//
+// Reference: the CPU branch of UllisHeron::apply_head_ce (src/model.rs:3132-3274)
+// with causal_ce_row_valid / causal_ce_gradient_scale (src/model.rs:27-55):
+// per valid row, ce = max + ln sum exp(l - max) - l[target], gy = gscale *
+// (softmax - onehot), gscale = 1/(T-1); then the head's backward_ste, the
+// BinaryConnect latent step with ste = T-1 and scale SGD, and the head bias
+// step at 8x the learning rate (src/model.rs:3118-3130). The Metal path it
+// replaces (packed_head_train_sgd, src/metal.rs:3300-3510) materialises
+// [rows, vocab] fp32 logits and their gradient.
+//
+// Here the [rows, vocab] logits are never stored:
+//  1. logits GEMM with an online log-sum-exp epilogue: per (row, 32-column
+//     block) max and sum-exp, plus the target logit;
+//  2. a per-row combine gives lse, row loss, n_valid, mean loss and gscale on
+//     the device (no host round trip);
+//  3. the vocabulary is streamed in chunks of Vc columns: the logits of the
+//     chunk are recomputed, turned into the unscaled fp16 gradient p - onehot
+//     (a [rows, Vc] scratch, never [rows, vocab]), and consumed by the input
+//     gradient GEMM (accumulated into g_hidden, times gscale) and the
+//     weight-gradient GEMM of those Vc head rows, whose finish kernel applies
+//     the latent step and g_scale = sum_i sign * G;
+//  4. g_bias, the scale / bias steps and the bit repack run after the last
+//     chunk, so every GEMM above reads the pre-update bits and scales.
+#include <math.h>
+
+#include "gemm.hpp"
+#include "ops.hpp"
+
+namespace ullis {
+
+hipError_t packed_backward_input_ex(hipStream_t s, const uint16_t* gy16, long ldgy, long rows,
+                                    long in, long k_len, const uint32_t* bits_t, long ldb,
+                                    long kofs, const uint16_t* scale, float* gx,
+                                    const float* out_mul, int accumulate);
+
+namespace {
+
+__device__ __forceinline__ bool ce_row_valid(long row, long rows, long time,
+                                             const uint32_t* targets, uint32_t ignore_id) {
+  // causal_ce_row_valid(row, time, horizon = 1, ...), src/model.rs:27-39
+  if (time == 0 || row % time + 1 >= time) return false;
+  return row + 1 < rows && targets[row + 1] != ignore_id;
+}
+
+struct EpiCeStats {
+  const uint16_t* scale;
+  const uint16_t* bias;
+  const uint32_t* targets;
+  uint32_t ignore_id;
+  long time;
+  float* part_m;  // [nb32][M]
+  float* part_s;
+  float* tgt;     // [M]
+  template <int TM, int TN>
+  __device__ void run(floatx16 (&acc)[TM][TN], int row0, int col0, int lane, int M, int N) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int cbase = col0 + j * 32;
+        const int col = cbase + (lane & 31);
+        const bool colok = col < N;
+        const float sc = colok ? f16_bits_to_f32(scale[col]) : 0.0f;
+        const float bi = (bias && colok) ? f16_bits_to_f32(bias[col]) : 0.0f;
+        const long cb = cbase / 32;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = row0 + i * 32 + mfma32_row(r, lane);
+          const float logit = colok ? bi + sc * acc[i][j][r] : -INFINITY;
+          const float m = halfwave_max(logit);
+          const float e = (colok && m > -INFINITY) ? expf(logit - m) : 0.0f;
+          const float ssum = halfwave_sum(e);
+          if (row < M && cbase < N) {
+            if ((lane & 31) == 0) {
+              part_m[cb * M + row] = m;
+              part_s[cb * M + row] = ssum;
+            }
+            if (colok && ce_row_valid(row, M, time, targets, ignore_id) &&
+                (long)targets[row + 1] == (long)col)
+              tgt[row] = logit;
+          }
+        }
+      }
+  }
+};
+
+struct EpiCeGrad {
+  const uint16_t* scale;  // chunk-offset
+  const uint16_t* bias;   // chunk-offset or null
+  const uint32_t* targets;
+  uint32_t ignore_id;
+  long time;
+  long col_base;          // global vocab index of chunk column 0
+  long vocab;
+  const float* lse;
+  uint16_t* gy16;         // [M][N] chunk scratch
+  float* part_bias;       // [ceil(M/32)][vocab]
+  template <int TM, int TN>
+  __device__ void run(floatx16 (&acc)[TM][TN], int row0, int col0, int lane, int M, int N) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = col0 + j * 32 + (lane & 31);
+        const bool colok = col < N;
+        const float sc = colok ? f16_bits_to_f32(scale[col]) : 0.0f;
+        const float bi = (bias && colok) ? f16_bits_to_f32(bias[col]) : 0.0f;
+        const long vcol = col_base + col;
+        float csum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = row0 + i * 32 + mfma32_row(r, lane);
+          if (row < M && colok) {
+            float g = 0.0f;
+            if (ce_row_valid(row, M, time, targets, ignore_id)) {
+              const float logit = bi + sc * acc[i][j][r];
+              const float p = expf(logit - lse[row]);
+              g = (long)targets[row + 1] == vcol ? p - 1.0f : p;
+            }
+            gy16[(long)row * N + col] = __builtin_bit_cast(uint16_t, (half_t)g);
+            csum += g;
+          }
+        }
+        csum += __shfl_xor(csum, 32, 64);
+        const int tile_row = row0 + i * 32;
+        if (lane < 32 && colok && tile_row < M) part_bias[(long)(tile_row / 32) * vocab + vcol] = csum;
+      }
+  }
+};
+
+// One wave per row: merge the per-block (max, sum-exp) pairs.
+__global__ __launch_bounds__(256) void ce_combine_kernel(const float* part_m, const float* part_s,
+                                                         long nb, long rows, long time,
+                                                         const uint32_t* targets,
+                                                         uint32_t ignore_id, const float* tgt,
+                                                         float* lse, float* row_loss) {
+  const int lane = threadIdx.x & 63;
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  float m = -INFINITY;
+  for (long b = lane; b < nb; b += 64) m = __builtin_fmaxf(m, part_m[b * rows + row]);
+  m = wave_max(m);
+  float s = 0.0f;
+  for (long b = lane; b < nb; b += 64) {
+    const float mb = part_m[b * rows + row];
+    if (mb > -INFINITY) s += part_s[b * rows + row] * expf(mb - m);
+  }
+  s = wave_sum(s);
+  if (lane == 0) {
+    const float l = m + logf(s);
+    lse[row] = l;
+    row_loss[row] = ce_row_valid(row, rows, time, targets, ignore_id) ? l - tgt[row] : 0.0f;
+  }
+}
+
+// Single block: n_valid, loss sum (fixed-order tree), mean and gscale.
+__global__ __launch_bounds__(1024) void ce_mean_kernel(const float* row_loss, long rows, long time,
+                                                       const uint32_t* targets,
+                                                       uint32_t ignore_id, float* stats) {
+  __shared__ float ls[1024];
+  __shared__ float nv[1024];
+  float a = 0.0f, n = 0.0f;
+  for (long r = threadIdx.x; r < rows; r += blockDim.x) {
+    if (ce_row_valid(r, rows, time, targets, ignore_id)) {
+      a += row_loss[r];
+      n += 1.0f;
+    }
+  }
+  ls[threadIdx.x] = a;
+  nv[threadIdx.x] = n;
+  __syncthreads();
+  for (int st = 512; st > 0; st >>= 1) {
+    if ((int)threadIdx.x < st) {
+      ls[threadIdx.x] += ls[threadIdx.x + st];
+      nv[threadIdx.x] += nv[threadIdx.x + st];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const float count = nv[0];
+    stats[0] = count > 0.0f ? ls[0] / count : 0.0f;
+    stats[1] = count;
+    stats[2] = (count > 0.0f && time >= 2) ? 1.0f / (float)(time - 1) : 0.0f;  // :49-55
+    stats[3] = ls[0];
+  }
+}
+
+// g_bias[v] = gscale * sum_b part[b][v]; optional bias step at lr_bias;
+// optional scale step at lr with g_scale.
+__global__ void head_vector_finish_kernel(const float* part, int nb, long vocab,
+                                          const float* stats, float* g_bias, float lr,
+                                          uint16_t* bias, float* bias_res, const float* g_scale,
+                                          uint16_t* scale, float* scale_res) {
+  const long v = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (v >= vocab) return;
+  float s = 0.0f;
+  for (int b = 0; b < nb; ++b) s += part[(long)b * vocab + v];
+  s *= stats[2];
+  if (g_bias) g_bias[v] = s;
+  if (lr > 0.0f) {
+    if (scale) clipped_sgd_one(scale[v], scale_res[v], g_scale[v], lr);
+    if (bias) clipped_sgd_one(bias[v], bias_res[v], s, lr * kHeadBiasLrMult);
+  }
+}
+
+long chunk_cols(long vocab, long d) {
+  // Enough weight-gradient tiles (Vc x d, 64x64) to fill the GPU, multiple of 32.
+  long vc = 2048;
+  if (d < 512) vc = 4096;
+  if (vc > vocab) vc = vocab;
+  vc = cdiv(vc, 32) * 32;
+  return vc;
+}
+
+struct Ws {
+  float *part_m, *part_s, *tgt, *lse, *part_bias, *gpart, *g_scale, *g_bias;
+  uint16_t* gy16;
+};
+
+Ws carve(void* base, long rows, long d, long vocab) {
+  const long nb32 = cdiv(vocab, 32);
+  const long vc = chunk_cols(vocab, d);
+  char* p = static_cast<char*>(base);
+  auto take = [&](size_t bytes) {
+    char* r = p;
+    p += (bytes + 255) / 256 * 256;
+    return r;
+  };
+  Ws w;
+  w.part_m = reinterpret_cast<float*>(take(sizeof(float) * nb32 * rows));
+  w.part_s = reinterpret_cast<float*>(take(sizeof(float) * nb32 * rows));
+  w.tgt = reinterpret_cast<float*>(take(sizeof(float) * rows));
+  w.lse = reinterpret_cast<float*>(take(sizeof(float) * rows));
+  w.part_bias = reinterpret_cast<float*>(take(sizeof(float) * cdiv(rows, 32) * vocab));
+  w.gpart = reinterpret_cast<float*>(take(sizeof(float) * vc * d));
+  w.g_scale = reinterpret_cast<float*>(take(sizeof(float) * vocab));
+  w.g_bias = reinterpret_cast<float*>(take(sizeof(float) * vocab));
+  w.gy16 = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * rows * vc));
+  return w;
+}
+
+template <class Epi>
+hipError_t logits_gemm(hipStream_t s, const uint16_t* hidden16, long rows, long d,
+                       const uint32_t* bits_rows, long ncols, const Epi& epi) {
+  // C[rows][ncols] = hidden . S^T ; S rows start at bits_rows (word aligned).
+  const bool vec = (reinterpret_cast<uintptr_t>(hidden16) & 15u) == 0 && d % 8 == 0;
+  if (cdiv(rows, 128) * cdiv(ncols, 128) >= 240) {
+    LoadF16K<128> la{reinterpret_cast<const half_t*>(hidden16), d, vec};
+    LoadBits<128> lb{bits_rows, d, 0, nullptr, d % 8 == 0};
+    hipLaunchKernelGGL((gemm_kernel<128, 128, LoadF16K<128>, LoadBits<128>, Epi>),
+                       dim3((unsigned)(cdiv(rows, 128) * cdiv(ncols, 128))), dim3(kThreads), 0, s,
+                       la, lb, epi, (int)rows, (int)ncols, (int)d, (int)(cdiv(d, kBK) * kBK));
+  } else {
+    LoadF16K<64> la{reinterpret_cast<const half_t*>(hidden16), d, vec};
+    LoadBits<64> lb{bits_rows, d, 0, nullptr, d % 8 == 0};
+    hipLaunchKernelGGL((gemm_kernel<64, 64, LoadF16K<64>, LoadBits<64>, Epi>),
+                       dim3((unsigned)(cdiv(rows, 64) * cdiv(ncols, 64))), dim3(kThreads), 0, s,
+                       la, lb, epi, (int)rows, (int)ncols, (int)d, (int)(cdiv(d, kBK) * kBK));
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+size_t head_ce_workspace_bytes(long rows, long d, long vocab) {
+  const long nb32 = cdiv(vocab, 32);
+  const long vc = chunk_cols(vocab, d);
+  auto al = [](size_t b) { return (b + 255) / 256 * 256; };
+  return al(4 * nb32 * rows) * 2 + al(4 * rows) * 2 + al(4 * cdiv(rows, 32) * vocab) +
+         al(4 * vc * d) + al(4 * vocab) * 2 + al(2 * rows * vc) + 256;
+}
+
+hipError_t head_ce(hipStream_t s, const HeadCe& h, void* workspace) {
+  const long rows = h.rows, d = h.d, V = h.vocab;
+  if (rows <= 0 || d <= 0 || V <= 0) return hipErrorInvalidValue;
+  Ws w = carve(workspace, rows, d, V);
+  const long nb32 = cdiv(V, 32);
+  hipError_t e;
+
+  // 1. forward statistics (fills every part_m/part_s entry and tgt of valid rows)
+  EpiCeStats st{h.scale, h.bias, h.targets, h.ignore_id, h.time, w.part_m, w.part_s, w.tgt};
+  if ((e = logits_gemm(s, h.hidden16, rows, d, h.bits, V, st)) != hipSuccess) return e;
+  // 2. combine
+  hipLaunchKernelGGL(ce_combine_kernel, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, w.part_m,
+                     w.part_s, nb32, rows, h.time, h.targets, h.ignore_id, w.tgt, w.lse,
+                     h.row_loss);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(ce_mean_kernel, dim3(1), dim3(1024), 0, s, h.row_loss, rows, h.time,
+                     h.targets, h.ignore_id, h.stats);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+
+  // 3. stream the vocabulary in chunks
+  const long vc = chunk_cols(V, d);
+  const float* gscale = h.stats + 2;
+  float* g_scale = h.g_scale ? h.g_scale : w.g_scale;
+  for (long c0 = 0, ci = 0; c0 < V; c0 += vc, ++ci) {
+    const long n = V - c0 < vc ? V - c0 : vc;
+    const uint32_t* bits_rows = h.bits + (c0 * d) / 32;
+    EpiCeGrad gr{h.scale + c0, h.bias ? h.bias + c0 : nullptr, h.targets, h.ignore_id, h.time, c0,
+                 V, w.lse, w.gy16, w.part_bias};
+    if ((e = logits_gemm(s, h.hidden16, rows, d, bits_rows, n, gr)) != hipSuccess) return e;
+    // g_hidden (+)= gscale * gy_chunk . (scale * S)_chunk
+    if ((e = packed_backward_input_ex(s, w.gy16, n, rows, d, n, h.bits_t, V, c0, h.scale,
+                                      h.g_hidden, gscale, ci > 0)) != hipSuccess)
+      return e;
+    // G_chunk = gy_chunk^T . hidden, then the latent step for these head rows
+    if ((e = packed_weight_grad_partials(s, GradIn{nullptr, nullptr}, w.gy16, h.hidden16, rows, d,
+                                         n, 1, w.gpart)) != hipSuccess)
+      return e;
+    PackedFinish f;
+    f.part = w.gpart;
+    f.splits = 1;
+    f.out = n;
+    f.in = d;
+    f.scale = h.scale + c0;
+    f.bits_old = h.bits + (c0 * d) / 32;
+    f.amax = nullptr;
+    f.extra_mul = gscale;
+    f.ste = h.ste;
+    f.lr = h.lr;
+    f.latent = h.lr > 0.0f ? h.latent + c0 * d : nullptr;
+    f.latent_res = h.lr > 0.0f ? h.latent_res + c0 * d : nullptr;
+    f.g_scale = g_scale + c0;
+    f.g_w = h.g_w ? h.g_w + c0 * d : nullptr;
+    if ((e = packed_weight_finish(s, f)) != hipSuccess) return e;
+  }
+
+  // 4. bias gradient, vector steps, repack
+  const bool upd = h.lr > 0.0f;
+  hipLaunchKernelGGL(head_vector_finish_kernel, dim3((unsigned)cdiv(V, 256)), dim3(256), 0, s,
+                     w.part_bias, (int)cdiv(rows, 32), V, h.stats, h.g_bias ? h.g_bias : w.g_bias,
+                     upd ? h.lr : 0.0f, upd ? h.bias_upd : nullptr, h.bias_res, g_scale,
+                     upd ? h.scale_upd : nullptr, h.scale_res);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  if (upd && h.bits_new) return pack_latent_bits(s, h.latent, V, d, h.bits_new, h.bits_t_new);
+  return hipSuccess;
+}
+
+}  // namespace ullis

@@ -1,0 +1,388 @@
+// Packed +-1 BinaryConnect linear and FP16 linear on gfx950 MFMA.
+//
+// Reference semantics (Vladislav-Kalinkin/ullis 0.10.0):
+//   forward      y[r,o]  = bias[o] + scale[o] * sum_i sign[o,i] x[r,i]   src/model.rs:724-742
+//   input grad   gx[r,i] = sum_o gy[r,o] scale[o] sign[o,i]             src/model.rs:783
+//   weight grad  gw[o,i] = sum_r gy[r,o] scale[o] x[r,i]                src/model.rs:782
+//   scale grad   gs[o]   = sum_r gy[r,o] sum_i sign[o,i] x[r,i]         src/model.rs:787
+//                        = sum_i sign[o,i] G[o,i],  G = gy^T x  (computed that way here)
+//   latent SGD   BinaryConnect step on g = gw * ste, then rebinarize    src/model.rs:808-884
+//   FP16 linear  y = x W^T, gx = gy W, gW = gy^T x, clipped SGD          src/model.rs:419-470
+// The Metal kernels these replace are ullis_binary_linear*, ullis_fp16_linear*
+// (src/metal/rwkv8.metal:370-841).
+#include "gemm.hpp"
+#include "ops.hpp"
+
+namespace ullis {
+
+namespace {
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline int vec_ok_f16(const void* p, long ld) { return aligned16(p) && ld % 8 == 0; }
+inline int vec_ok_f32(const void* p, long ld) { return aligned16(p) && ld % 4 == 0; }
+
+template <int BM_, int BN_>
+struct Tile {
+  static constexpr int bm = BM_, bn = BN_;
+};
+
+// 128x128 tiles when they alone give ~one block per CU, else 64x64.
+template <class F>
+hipError_t with_tile(long M, long N, F&& f) {
+  if (cdiv(M, 128) * cdiv(N, 128) >= 240) return f(Tile<128, 128>{});
+  return f(Tile<64, 64>{});
+}
+
+template <int BM, int BN, class LA, class LB, class Epi>
+hipError_t launch_gemm(hipStream_t s, const LA& la, const LB& lb, const Epi& epi, long M, long N,
+                       long K, int splits) {
+  if (M <= 0 || N <= 0) return hipSuccess;
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return hipErrorInvalidValue;
+  if (splits < 1) splits = 1;
+  const long tiles = cdiv(M, BM) * cdiv(N, BN);
+  const int ks = (int)(cdiv(cdiv(K, splits), kBK) * kBK);
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, LA, LB, Epi>), dim3((unsigned)tiles, 1, splits),
+                     dim3(kThreads), 0, s, la, lb, epi, (int)M, (int)N, (int)K, ks > 0 ? ks : kBK);
+  return hipGetLastError();
+}
+
+__device__ __forceinline__ float unscale_of(const float* amax) {
+  return amax ? 1.0f / grad_scale_from_amax(*amax) : 1.0f;
+}
+
+// ---------------------------------------------------------------- epilogues
+
+struct EpiPackedFwd {
+  const uint16_t* scale;
+  const uint16_t* bias;
+  PackedFwdOut o;
+  template <int TM, int TN>
+  __device__ void run(floatx16 (&acc)[TM][TN], int row0, int col0, int lane, int M, int N) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = col0 + j * 32 + (lane & 31);
+        const bool colok = col < N;
+        const float sc = colok ? f16_bits_to_f32(scale[col]) : 0.0f;
+        const float bi = (bias && colok) ? f16_bits_to_f32(bias[col]) : 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = row0 + i * 32 + mfma32_row(r, lane);
+          const bool ok = colok && row < M;
+          const float y = bi + sc * acc[i][j][r];
+          const long idx = (long)row * N + col;
+          if (ok) {
+            if (o.y32) o.y32[idx] = o.resid ? o.resid[idx] + y : y;
+            if (o.y16) o.y16[idx] = __builtin_bit_cast(uint16_t, (half_t)y);
+            if (o.relu2_16) {
+              const float k = y > 0.0f ? y : 0.0f;
+              o.relu2_16[idx] = __builtin_bit_cast(uint16_t, (half_t)(k * k));
+            }
+          }
+          if (o.sign_bits) {
+            const unsigned long long m = __ballot(ok && y > 0.0f);
+            if ((lane & 31) == 0 && row < M && col0 + j * 32 < N) {
+              const long word = ((long)row * N + col0 + j * 32) >> 5;
+              o.sign_bits[word] = (lane < 32) ? (uint32_t)m : (uint32_t)(m >> 32);
+            }
+          }
+        }
+      }
+  }
+};
+
+struct EpiStoreF32 {
+  float* out;
+  const float* amax;  // operand scale to divide out
+  const float* mul;   // extra device scalar
+  int accumulate;
+  template <int TM, int TN>
+  __device__ void run(floatx16 (&acc)[TM][TN], int row0, int col0, int lane, int M, int N) {
+    float m = unscale_of(amax);
+    if (mul) m *= *mul;
+    for_each_acc(acc, row0, col0, lane, M, N, [&](int row, int col, float v) {
+      const long idx = (long)row * N + col;
+      const float g = v * m;
+      out[idx] = accumulate ? out[idx] + g : g;
+    });
+  }
+};
+
+struct EpiF16Fwd {
+  float* y32;
+  const float* resid;
+  uint16_t* y16;
+  template <int TM, int TN>
+  __device__ void run(floatx16 (&acc)[TM][TN], int row0, int col0, int lane, int M, int N) {
+    for_each_acc(acc, row0, col0, lane, M, N, [&](int row, int col, float y) {
+      const long idx = (long)row * N + col;
+      if (y32) y32[idx] = resid ? resid[idx] + y : y;
+      if (y16) y16[idx] = __builtin_bit_cast(uint16_t, (half_t)y);
+    });
+  }
+};
+
+// ReLU^2 backward fused into the value input-gradient: gk = 2 k g (k > 0),
+// src/model.rs:1191-1205, stored in the scaled fp16 domain of g.
+struct EpiRelu2Bwd {
+  const uint16_t* key16;
+  uint16_t* gk16;
+  template <int TM, int TN>
+  __device__ void run(floatx16 (&acc)[TM][TN], int row0, int col0, int lane, int M, int N) {
+    for_each_acc(acc, row0, col0, lane, M, N, [&](int row, int col, float g) {
+      const long idx = (long)row * N + col;
+      const float k = f16_bits_to_f32(key16[idx]);
+      const float gk = k > 0.0f ? 2.0f * k * g : 0.0f;
+      gk16[idx] = __builtin_bit_cast(uint16_t, f32_to_f16_sat(gk));
+    });
+  }
+};
+
+// ------------------------------------------------------------ finish kernels
+
+__global__ __launch_bounds__(256) void packed_finish_kernel(PackedFinish f) {
+  const long o = blockIdx.x;
+  if (o >= f.out) return;
+  __shared__ float red[256];
+  float gmul = f.amax ? 1.0f / grad_scale_from_amax(*f.amax) : 1.0f;
+  if (f.extra_mul) gmul *= *f.extra_mul;
+  const float sc = f16_bits_to_f32(f.scale[o]);
+  const long wn = f.out * f.in;
+  float gs = 0.0f;
+  for (long i = threadIdx.x; i < f.in; i += blockDim.x) {
+    const long w = o * f.in + i;
+    float G = 0.0f;
+    for (int z = 0; z < f.splits; ++z) G += f.part[(long)z * wn + w];
+    G *= gmul;
+    const bool plus = (f.bits_old[w >> 5] >> (w & 31)) & 1u;
+    gs += plus ? G : -G;
+    const float gw = sc * G;
+    if (f.g_w) f.g_w[w] = gw;
+    if (f.latent) binaryconnect_sgd_one(f.latent[w], f.latent_res[w], gw * f.ste, f.lr);
+  }
+  red[threadIdx.x] = gs;
+  __syncthreads();
+  for (int st = 128; st > 0; st >>= 1) {
+    if ((int)threadIdx.x < st) red[threadIdx.x] += red[threadIdx.x + st];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0 && f.g_scale) f.g_scale[o] = red[0];
+}
+
+__global__ void fp16_finish_kernel(const float* part, int splits, long n, const float* amax,
+                                   float lr, uint16_t* w, float* w_res, float* g_w) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float m = amax ? 1.0f / grad_scale_from_amax(*amax) : 1.0f;
+  float G = 0.0f;
+  for (int z = 0; z < splits; ++z) G += part[(long)z * n + i];
+  G *= m;
+  if (g_w) g_w[i] = G;
+  if (w) clipped_sgd_one(w[i], w_res[i], G, lr);
+}
+
+// One thread per word: bit j of word w is latent[32w + j] >= 0 (ullis_pack_latent_bits).
+__global__ void pack_bits_kernel(const uint16_t* latent, long n, uint32_t* bits) {
+  const long w = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long base = w * 32;
+  if (base >= n) return;
+  uint32_t packed = 0;
+  for (int j = 0; j < 32; ++j) {
+    const long i = base + j;
+    if (i < n && latent_is_plus(latent[i])) packed |= 1u << j;
+  }
+  bits[w] = packed;
+}
+
+// bits_t[i*out + o] = bits[o*in + i]. Aligned path: one half-wave transposes a
+// 32x32 bit block with 32 ballots.
+__global__ void transpose_bits_aligned_kernel(const uint32_t* bits, long out, long in,
+                                              uint32_t* bits_t) {
+  const int lane = threadIdx.x & 63;
+  const long blk = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 5;  // one block per half-wave
+  const long ob = out / 32, ib = in / 32;
+  const bool active = blk < ob * ib;
+  const long bo = active ? blk / ib : 0, bi = active ? blk % ib : 0;
+  const long o = bo * 32 + (lane & 31);
+  const uint32_t word = active ? bits[(o * in + bi * 32) >> 5] : 0u;
+  for (int b = 0; b < 32; ++b) {
+    const unsigned long long m = __ballot((word >> b) & 1u);
+    if ((lane & 31) == 0 && active) {
+      const long i = bi * 32 + b;
+      bits_t[(i * out + bo * 32) >> 5] = (lane < 32) ? (uint32_t)m : (uint32_t)(m >> 32);
+    }
+  }
+}
+
+__global__ void transpose_bits_generic_kernel(const uint32_t* bits, long out, long in,
+                                              uint32_t* bits_t) {
+  const long w = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long n = out * in;
+  const long base = w * 32;
+  if (base >= n) return;
+  uint32_t packed = 0;
+  for (int j = 0; j < 32; ++j) {
+    const long t = base + j;
+    if (t >= n) break;
+    const long i = t / out, o = t % out;
+    const long src = o * in + i;
+    if ((bits[src >> 5] >> (src & 31)) & 1u) packed |= 1u << j;
+  }
+  bits_t[w] = packed;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ packed
+
+hipError_t packed_forward(hipStream_t s, const void* x, int x_dtype, long rows, long in, long out,
+                          const uint32_t* bits, const uint16_t* scale, const uint16_t* bias,
+                          const PackedFwdOut& o) {
+  if (o.sign_bits && out % 32 != 0) return hipErrorInvalidValue;
+  EpiPackedFwd epi{scale, bias, o};
+  return with_tile(rows, out, [&](auto t) {
+    using T = decltype(t);
+    LoadBits<T::bn> lb{bits, in, 0, nullptr, in % 8 == 0};
+    if (x_dtype == kF16) {
+      LoadF16K<T::bm> la{static_cast<const half_t*>(x), in, vec_ok_f16(x, in)};
+      return launch_gemm<T::bm, T::bn>(s, la, lb, epi, rows, out, in, 1);
+    }
+    LoadF32K<T::bm> la{static_cast<const float*>(x), in, vec_ok_f32(x, in), nullptr, 1.0f};
+    return launch_gemm<T::bm, T::bn>(s, la, lb, epi, rows, out, in, 1);
+  });
+}
+
+hipError_t packed_backward_input(hipStream_t s, GradIn gy32, const uint16_t* gy16, long rows,
+                                 long in, long out, const uint32_t* bits_t, const uint16_t* scale,
+                                 float* gx, const float* out_mul, int accumulate) {
+  EpiStoreF32 epi{gx, gy32.amax, out_mul, accumulate};
+  return with_tile(rows, in, [&](auto t) {
+    using T = decltype(t);
+    LoadBits<T::bn> lb{bits_t, out, 0, scale, out % 8 == 0};
+    if (gy16) {
+      LoadF16K<T::bm> la{reinterpret_cast<const half_t*>(gy16), out, vec_ok_f16(gy16, out)};
+      return launch_gemm<T::bm, T::bn>(s, la, lb, epi, rows, in, out, 1);
+    }
+    LoadF32K<T::bm> la{gy32.p, out, vec_ok_f32(gy32.p, out), gy32.amax, 1.0f};
+    return launch_gemm<T::bm, T::bn>(s, la, lb, epi, rows, in, out, 1);
+  });
+}
+
+// Input gradient over a column window of the output features: contraction
+// over k in [kofs, kofs + k_len) of a bits_t matrix with ldb bits per row, gy
+// fp16 [rows][ldgy] holding only that window (unscaled), scale indexed kofs + k.
+hipError_t packed_backward_input_ex(hipStream_t s, const uint16_t* gy16, long ldgy, long rows,
+                                    long in, long k_len, const uint32_t* bits_t, long ldb,
+                                    long kofs, const uint16_t* scale, float* gx,
+                                    const float* out_mul, int accumulate) {
+  EpiStoreF32 epi{gx, nullptr, out_mul, accumulate};
+  return with_tile(rows, in, [&](auto t) {
+    using T = decltype(t);
+    LoadBits<T::bn> lb{bits_t, ldb, kofs, scale, ldb % 8 == 0 && kofs % 8 == 0};
+    LoadF16K<T::bm> la{reinterpret_cast<const half_t*>(gy16), ldgy, vec_ok_f16(gy16, ldgy)};
+    return launch_gemm<T::bm, T::bn>(s, la, lb, epi, rows, in, k_len, 1);
+  });
+}
+
+hipError_t packed_weight_grad_partials(hipStream_t s, GradIn gy32, const uint16_t* gy16,
+                                       const uint16_t* x16, long rows, long in, long out,
+                                       int splits, float* part) {
+  EpiPartial epi{part};
+  // G[out][in]: M = out, N = in, K = rows; both operands are row-contiguous.
+  return with_tile(out, in, [&](auto t) {
+    using T = decltype(t);
+    LoadF16T<T::bn> lb{reinterpret_cast<const half_t*>(x16), in, vec_ok_f16(x16, in)};
+    if (gy16) {
+      LoadF16T<T::bm> la{reinterpret_cast<const half_t*>(gy16), out, vec_ok_f16(gy16, out)};
+      return launch_gemm<T::bm, T::bn>(s, la, lb, epi, out, in, rows, splits);
+    }
+    LoadF32T<T::bm> la{gy32.p, out, vec_ok_f32(gy32.p, out), gy32.amax, 1.0f};
+    return launch_gemm<T::bm, T::bn>(s, la, lb, epi, out, in, rows, splits);
+  });
+}
+
+hipError_t packed_weight_finish(hipStream_t s, const PackedFinish& f) {
+  if (f.out <= 0 || f.in <= 0) return hipSuccess;
+  hipLaunchKernelGGL(packed_finish_kernel, dim3((unsigned)f.out), dim3(256), 0, s, f);
+  return hipGetLastError();
+}
+
+hipError_t pack_latent_bits(hipStream_t s, const uint16_t* latent, long out, long in,
+                            uint32_t* bits, uint32_t* bits_t) {
+  const long n = out * in;
+  if (n <= 0) return hipSuccess;
+  const long words = cdiv(n, 32);
+  hipLaunchKernelGGL(pack_bits_kernel, dim3((unsigned)cdiv(words, 256)), dim3(256), 0, s, latent,
+                     n, bits);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !bits_t) return e;
+  return transpose_bits(s, bits, out, in, bits_t);
+}
+
+hipError_t transpose_bits(hipStream_t s, const uint32_t* bits, long out, long in,
+                          uint32_t* bits_t) {
+  const long n = out * in;
+  if (n <= 0) return hipSuccess;
+  if (out % 32 == 0 && in % 32 == 0) {
+    const long blocks32 = (out / 32) * (in / 32);
+    const long threads = blocks32 * 32;
+    hipLaunchKernelGGL(transpose_bits_aligned_kernel, dim3((unsigned)cdiv(threads, 256)),
+                       dim3(256), 0, s, bits, out, in, bits_t);
+  } else {
+    hipLaunchKernelGGL(transpose_bits_generic_kernel, dim3((unsigned)cdiv(cdiv(n, 32), 256)),
+                       dim3(256), 0, s, bits, out, in, bits_t);
+  }
+  return hipGetLastError();
+}
+
+// -------------------------------------------------------------------- fp16
+
+hipError_t fp16_forward(hipStream_t s, const void* x, int x_dtype, long rows, long in, long out,
+                        const uint16_t* w, float* y32, const float* resid, uint16_t* y16) {
+  EpiF16Fwd epi{y32, resid, y16};
+  return with_tile(rows, out, [&](auto t) {
+    using T = decltype(t);
+    LoadF16K<T::bn> lb{reinterpret_cast<const half_t*>(w), in, vec_ok_f16(w, in)};
+    if (x_dtype == kF16) {
+      LoadF16K<T::bm> la{static_cast<const half_t*>(x), in, vec_ok_f16(x, in)};
+      return launch_gemm<T::bm, T::bn>(s, la, lb, epi, rows, out, in, 1);
+    }
+    LoadF32K<T::bm> la{static_cast<const float*>(x), in, vec_ok_f32(x, in), nullptr, 1.0f};
+    return launch_gemm<T::bm, T::bn>(s, la, lb, epi, rows, out, in, 1);
+  });
+}
+
+hipError_t fp16_backward_input(hipStream_t s, GradIn gy32, long rows, long in, long out,
+                               const uint16_t* w, float* gx, const uint16_t* key16,
+                               uint16_t* gk16) {
+  // gX[rows][in] = gY[rows][out] . W[out][in]: B(n = i, k = o) = W[o*in + i].
+  return with_tile(rows, in, [&](auto t) {
+    using T = decltype(t);
+    LoadF32K<T::bm> la{gy32.p, out, vec_ok_f32(gy32.p, out), gy32.amax, 1.0f};
+    LoadF16T<T::bn> lb{reinterpret_cast<const half_t*>(w), in, vec_ok_f16(w, in)};
+    if (gk16) {
+      EpiRelu2Bwd epi{key16, gk16};
+      return launch_gemm<T::bm, T::bn>(s, la, lb, epi, rows, in, out, 1);
+    }
+    EpiStoreF32 epi{gx, gy32.amax, nullptr, 0};
+    return launch_gemm<T::bm, T::bn>(s, la, lb, epi, rows, in, out, 1);
+  });
+}
+
+hipError_t fp16_weight_grad_partials(hipStream_t s, GradIn gy32, const uint16_t* x16, long rows,
+                                     long in, long out, int splits, float* part) {
+  return packed_weight_grad_partials(s, gy32, nullptr, x16, rows, in, out, splits, part);
+}
+
+hipError_t fp16_weight_finish(hipStream_t s, const float* part, int splits, long out, long in,
+                              const float* amax, float lr, uint16_t* w, float* w_res,
+                              float* g_w) {
+  const long n = out * in;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(fp16_finish_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, s, part,
+                     splits, n, amax, lr, w, w_res, g_w);
+  return hipGetLastError();
+}
+
+}  // namespace ullis

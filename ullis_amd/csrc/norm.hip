@@ -1,0 +1,359 @@
+// LayerNorm forward / backward (HBM-bound), one wave64 per row.
+//
+// Reference: LayerNorm::forward / backward, src/model.rs:259-316 (affine,
+// population variance, eps = 1e-5, inv = 1/sqrt(var + eps)); the Metal kernels
+// replaced are ullis_layer_norm, ullis_layer_norm_backward and
+// ullis_layer_norm_param_bwd (src/metal/rwkv8.metal:154-269), which run one
+// thread per row. Here a row is spread over the 64 lanes of a wave: each lane
+// keeps its float4 chunks in registers and row sums are wave (DPP) reductions.
+// gamma/beta gradients are column sums written as per-block partials and
+// reduced in a fixed order by layer_norm_param_finish, so results do not
+// depend on scheduling.
+#include <type_traits>
+
+#include "common.hpp"
+#include "ops.hpp"
+
+namespace ullis {
+
+namespace {
+
+constexpr int kRowsPerBlock = 4;
+
+// NV = float4 chunks per lane (ch <= 256 * NV, ch % 4 == 0).
+template <int NV>
+__global__ __launch_bounds__(256) void ln_fwd_vec_kernel(const float* __restrict__ x, long rows,
+                                                         int ch, const uint16_t* __restrict__ w,
+                                                         const uint16_t* __restrict__ b,
+                                                         float* __restrict__ y32,
+                                                         uint16_t* __restrict__ y16) {
+  const int lane = threadIdx.x & 63;
+  const long row = (long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* xr = x + row * ch;
+  floatx4 v[NV];
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 4;
+    v[j] = c < ch ? *reinterpret_cast<const floatx4*>(xr + c) : (floatx4){};
+    s += (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]);
+  }
+  const float mean = wave_sum(s) / (float)ch;
+  float q = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 4;
+    if (c < ch) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float d = v[j][e] - mean;
+        q += d * d;
+      }
+    }
+  }
+  const float var = wave_sum(q) / (float)ch;
+  const float inv = 1.0f / __builtin_sqrtf(var + kLayerNormEps);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 4;
+    if (c < ch) {
+      floatx4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = (v[j][e] - mean) * inv * f16_bits_to_f32(w[c + e]) + f16_bits_to_f32(b[c + e]);
+      if (y32) *reinterpret_cast<floatx4*>(y32 + row * ch + c) = o;
+      if (y16) {
+        half4 h;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = (half_t)o[e];
+        *reinterpret_cast<half4*>(y16 + row * ch + c) = h;
+      }
+    }
+  }
+}
+
+// Any ch: two passes over global memory, lane-strided.
+__global__ __launch_bounds__(256) void ln_fwd_any_kernel(const float* x, long rows, int ch,
+                                                         const uint16_t* w, const uint16_t* b,
+                                                         float* y32, uint16_t* y16) {
+  const int lane = threadIdx.x & 63;
+  const long row = (long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* xr = x + row * ch;
+  float s = 0.0f;
+  for (int c = lane; c < ch; c += 64) s += xr[c];
+  const float mean = wave_sum(s) / (float)ch;
+  float q = 0.0f;
+  for (int c = lane; c < ch; c += 64) {
+    const float d = xr[c] - mean;
+    q += d * d;
+  }
+  const float var = wave_sum(q) / (float)ch;
+  const float inv = 1.0f / __builtin_sqrtf(var + kLayerNormEps);
+  for (int c = lane; c < ch; c += 64) {
+    const float o = (xr[c] - mean) * inv * f16_bits_to_f32(w[c]) + f16_bits_to_f32(b[c]);
+    if (y32) y32[row * ch + c] = o;
+    if (y16) y16[row * ch + c] = f32_to_f16_bits(o);
+  }
+}
+
+// Backward, ch % 4 == 0 and ch <= 1024 (block LDS reduction of the column
+// partials). Rows are distributed wave-strided over a fixed grid.
+template <int NV>
+__global__ __launch_bounds__(256) void ln_bwd_vec_kernel(const float* __restrict__ x,
+                                                         const float* __restrict__ gy, long rows,
+                                                         int ch, const uint16_t* __restrict__ w,
+                                                         float* gx, int accumulate, float* amax,
+                                                         float* __restrict__ part) {
+  __shared__ float red[kRowsPerBlock][2][1024];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  floatx4 pw[NV], pb[NV], wv[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    pw[j] = (floatx4){};
+    pb[j] = (floatx4){};
+    const int c = (lane + 64 * j) * 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) wv[j][e] = c < ch ? f16_bits_to_f32(w[c + e]) : 0.0f;
+  }
+  float local_max = 0.0f;
+  for (long row = (long)blockIdx.x * kRowsPerBlock + wave; row < rows;
+       row += (long)gridDim.x * kRowsPerBlock) {
+    const float* xr = x + row * ch;
+    const float* gr = gy + row * ch;
+    floatx4 v[NV], g[NV];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int c = (lane + 64 * j) * 4;
+      v[j] = c < ch ? *reinterpret_cast<const floatx4*>(xr + c) : (floatx4){};
+      g[j] = c < ch ? *reinterpret_cast<const floatx4*>(gr + c) : (floatx4){};
+      s += (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]);
+    }
+    const float mean = wave_sum(s) / (float)ch;
+    float q = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int c = (lane + 64 * j) * 4;
+      if (c < ch) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float d = v[j][e] - mean;
+          q += d * d;
+        }
+      }
+    }
+    const float var = wave_sum(q) / (float)ch;
+    const float inv = 1.0f / __builtin_sqrtf(var + kLayerNormEps);
+    float sd = 0.0f, sdx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float xhat = (v[j][e] - mean) * inv;
+        const float dxhat = g[j][e] * wv[j][e];
+        v[j][e] = xhat;  // keep xhat
+        sd += dxhat;
+        sdx += dxhat * xhat;
+        pw[j][e] += g[j][e] * xhat;
+        pb[j][e] += g[j][e];
+      }
+    }
+    const float sum_dxhat = wave_sum(sd);
+    const float sum_dxhat_xhat = wave_sum(sdx);
+    const float inv_n = inv / (float)ch;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int c = (lane + 64 * j) * 4;
+      if (c < ch) {
+        floatx4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float dxhat = g[j][e] * wv[j][e];
+          o[e] = inv_n * ((float)ch * dxhat - sum_dxhat - v[j][e] * sum_dxhat_xhat);
+        }
+        floatx4* dst = reinterpret_cast<floatx4*>(gx + row * ch + c);
+        if (accumulate) {
+          const floatx4 old = *dst;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = old[e] + o[e];
+        }
+        *dst = o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) local_max = __builtin_fmaxf(local_max, __builtin_fabsf(o[e]));
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 4;
+    if (c < ch) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        red[wave][0][c + e] = pw[j][e];
+        red[wave][1][c + e] = pb[j][e];
+      }
+    }
+  }
+  if (amax) {
+    const float m = wave_max(local_max);
+    if (lane == 0) atomic_amax(amax, m);
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < ch; c += blockDim.x) {
+    float a = 0.0f, bsum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kRowsPerBlock; ++k) {
+      a += red[k][0][c];
+      bsum += red[k][1][c];
+    }
+    part[((long)blockIdx.x * 2 + 0) * ch + c] = a;
+    part[((long)blockIdx.x * 2 + 1) * ch + c] = bsum;
+  }
+}
+
+// Any ch: one wave per (block, row slot); per-wave partials (block = 1 wave).
+__global__ __launch_bounds__(64) void ln_bwd_any_kernel(const float* x, const float* gy, long rows,
+                                                        int ch, const uint16_t* w, float* gx,
+                                                        int accumulate, float* amax, float* part) {
+  const int lane = threadIdx.x & 63;
+  float local_max = 0.0f;
+  float* pw = part + ((long)blockIdx.x * 2 + 0) * ch;
+  float* pb = part + ((long)blockIdx.x * 2 + 1) * ch;
+  for (int c = lane; c < ch; c += 64) {
+    pw[c] = 0.0f;
+    pb[c] = 0.0f;
+  }
+  for (long row = blockIdx.x; row < rows; row += gridDim.x) {
+    const float* xr = x + row * ch;
+    const float* gr = gy + row * ch;
+    float s = 0.0f;
+    for (int c = lane; c < ch; c += 64) s += xr[c];
+    const float mean = wave_sum(s) / (float)ch;
+    float q = 0.0f;
+    for (int c = lane; c < ch; c += 64) {
+      const float d = xr[c] - mean;
+      q += d * d;
+    }
+    const float var = wave_sum(q) / (float)ch;
+    const float inv = 1.0f / __builtin_sqrtf(var + kLayerNormEps);
+    float sd = 0.0f, sdx = 0.0f;
+    for (int c = lane; c < ch; c += 64) {
+      const float xhat = (xr[c] - mean) * inv;
+      const float dxhat = gr[c] * f16_bits_to_f32(w[c]);
+      sd += dxhat;
+      sdx += dxhat * xhat;
+      pw[c] += gr[c] * xhat;
+      pb[c] += gr[c];
+    }
+    const float sum_dxhat = wave_sum(sd);
+    const float sum_dxhat_xhat = wave_sum(sdx);
+    const float inv_n = inv / (float)ch;
+    for (int c = lane; c < ch; c += 64) {
+      const float xhat = (xr[c] - mean) * inv;
+      const float dxhat = gr[c] * f16_bits_to_f32(w[c]);
+      float o = inv_n * ((float)ch * dxhat - sum_dxhat - xhat * sum_dxhat_xhat);
+      if (accumulate) o = gx[row * ch + c] + o;
+      gx[row * ch + c] = o;
+      local_max = __builtin_fmaxf(local_max, __builtin_fabsf(o));
+    }
+  }
+  if (amax) {
+    const float m = wave_max(local_max);
+    if (lane == 0) atomic_amax(amax, m);
+  }
+}
+
+__global__ void ln_param_finish_kernel(const float* part, int nblk, long ch, float* gw, float* gb,
+                                       float lr, uint16_t* w, float* w_res, uint16_t* b,
+                                       float* b_res) {
+  const long c = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= ch) return;
+  float a = 0.0f, s = 0.0f;
+  for (int k = 0; k < nblk; ++k) {
+    a += part[((long)k * 2 + 0) * ch + c];
+    s += part[((long)k * 2 + 1) * ch + c];
+  }
+  if (gw) gw[c] = a;
+  if (gb) gb[c] = s;
+  if (lr > 0.0f && w) {
+    // LayerNorm::apply_clipped_sgd, src/model.rs:318-332
+    clipped_sgd_one(w[c], w_res[c], a, lr);
+    clipped_sgd_one(b[c], b_res[c], s, lr);
+  }
+}
+
+template <class F>
+hipError_t by_nv(long ch, F&& f) {
+  const long nv = cdiv(ch, 256);
+  if (nv <= 1) return f(std::integral_constant<int, 1>{});
+  if (nv <= 2) return f(std::integral_constant<int, 2>{});
+  if (nv <= 4) return f(std::integral_constant<int, 4>{});
+  if (nv <= 8) return f(std::integral_constant<int, 8>{});
+  return f(std::integral_constant<int, 16>{});
+}
+
+inline bool vec_ok(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+hipError_t layer_norm_forward(hipStream_t s, const float* x, long rows, long ch,
+                              const uint16_t* w, const uint16_t* b, float* y32, uint16_t* y16) {
+  if (rows <= 0 || ch <= 0) return hipSuccess;
+  const dim3 grid((unsigned)cdiv(rows, kRowsPerBlock));
+  const bool vec = ch % 4 == 0 && ch <= 4096 && vec_ok(x) && (!y32 || vec_ok(y32)) &&
+                   (!y16 || (reinterpret_cast<uintptr_t>(y16) & 7u) == 0);
+  if (vec) {
+    return by_nv(ch, [&](auto nv) {
+      hipLaunchKernelGGL(ln_fwd_vec_kernel<decltype(nv)::value>, grid, dim3(256), 0, s, x, rows,
+                         (int)ch, w, b, y32, y16);
+      return hipGetLastError();
+    });
+  }
+  hipLaunchKernelGGL(ln_fwd_any_kernel, grid, dim3(256), 0, s, x, rows, (int)ch, w, b, y32, y16);
+  return hipGetLastError();
+}
+
+static bool ln_bwd_vec_path(long ch) { return ch % 4 == 0 && ch <= 1024; }
+
+int layer_norm_backward_blocks(long rows) {
+  // Two rows per wave at the heron shape; never more blocks than row slots.
+  long nblk = cdiv(rows, 2 * kRowsPerBlock);
+  if (nblk > 256) nblk = 256;
+  if (nblk < 1) nblk = 1;
+  return (int)nblk;
+}
+
+hipError_t layer_norm_backward_rows(hipStream_t s, const float* x, const float* gy, long rows,
+                                    long ch, const uint16_t* w, float* gx, int accumulate,
+                                    float* amax, float* part, int* nblk_out) {
+  if (rows <= 0 || ch <= 0) {
+    if (nblk_out) *nblk_out = 0;
+    return hipSuccess;
+  }
+  const int nblk = layer_norm_backward_blocks(rows);
+  if (nblk_out) *nblk_out = nblk;
+  if (ln_bwd_vec_path(ch) && vec_ok(x) && vec_ok(gy) && vec_ok(gx)) {
+    return by_nv(ch, [&](auto nv) {
+      hipLaunchKernelGGL(ln_bwd_vec_kernel<decltype(nv)::value>, dim3(nblk), dim3(256), 0, s, x,
+                         gy, rows, (int)ch, w, gx, accumulate, amax, part);
+      return hipGetLastError();
+    });
+  }
+  hipLaunchKernelGGL(ln_bwd_any_kernel, dim3(nblk), dim3(64), 0, s, x, gy, rows, (int)ch, w, gx,
+                     accumulate, amax, part);
+  return hipGetLastError();
+}
+
+hipError_t layer_norm_param_finish(hipStream_t s, const float* part, int nblk, long ch, float* gw,
+                                   float* gb, float lr, uint16_t* w, float* w_res, uint16_t* b,
+                                   float* b_res) {
+  if (ch <= 0) return hipSuccess;
+  hipLaunchKernelGGL(ln_param_finish_kernel, dim3((unsigned)cdiv(ch, 256)), dim3(256), 0, s, part,
+                     nblk, ch, gw, gb, lr, w, w_res, b, b_res);
+  return hipGetLastError();
+}
+
+}  // namespace ullis

@@ -1,0 +1,187 @@
+// Internal launchers of libullis_hip (stream-ordered, device pointers, no
+// host synchronisation). The C ABI in capi.hip validates arguments and calls
+// these; the Heron step in heron.hip composes them.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ullis {
+
+enum ActDtype : int { kF16 = 1, kF32 = 2 };
+
+inline long cdiv(long a, long b) { return (a + b - 1) / b; }
+
+// Scaled-gradient operand: values are multiplied by a power of two derived from
+// *amax (or by 1 when amax is null) before the fp16 conversion.
+struct GradIn {
+  const float* p;
+  const float* amax;
+};
+
+// ------------------------------------------------------------ packed linear
+
+// Output of a packed forward y = bias + scale * (x . S^T).
+struct PackedFwdOut {
+  float* y32 = nullptr;          // fp32 y, or resid + y when resid is set
+  const float* resid = nullptr;  // residual stream input for fused x += y
+  uint16_t* y16 = nullptr;       // fp16 y
+  uint32_t* sign_bits = nullptr; // bit (row*out + o) = y > 0 (requires out % 32 == 0)
+  uint16_t* relu2_16 = nullptr;  // fp16 max(y,0)^2 (CMix key)
+};
+
+hipError_t packed_forward(hipStream_t s, const void* x, int x_dtype, long rows, long in, long out,
+                          const uint32_t* bits, const uint16_t* scale, const uint16_t* bias,
+                          const PackedFwdOut& o);
+
+// gX = (gY * scale) . S  via bits_t ([in, out] transpose bits) -> fp32 gx.
+// gy is fp32 (scaled by amax) or fp16 (already scaled by 1/unscale); result is
+// multiplied by out_mul (device scalar, may be null) and 1/gy-scale.
+// accumulate: gx += result.
+hipError_t packed_backward_input(hipStream_t s, GradIn gy32, const uint16_t* gy16, long rows,
+                                 long in, long out, const uint32_t* bits_t, const uint16_t* scale,
+                                 float* gx, const float* out_mul, int accumulate);
+
+// Raw G = gY^T . X partials: part[z][out][in], z < splits. x is fp16 [rows, in];
+// gy is fp32 scaled (GradIn) or fp16 [rows, out].
+hipError_t packed_weight_grad_partials(hipStream_t s, GradIn gy32, const uint16_t* gy16,
+                                       const uint16_t* x16, long rows, long in, long out,
+                                       int splits, float* part);
+
+// Reduces the partials and applies, per weight, the BinaryConnect latent step
+// with g = scale[o] * G * gmul * ste, gmul = (1/gy-scale) * (*extra_mul);
+// g_scale[o] = sum_i sign_old[o,i] * G * gmul. Optionally writes g_w.
+struct PackedFinish {
+  const float* part;
+  int splits;
+  long out, in;
+  const uint16_t* scale;
+  const uint32_t* bits_old;
+  const float* amax;       // gy scale source (null: unscaled)
+  const float* extra_mul;  // device scalar or null
+  float ste;
+  float lr;
+  uint16_t* latent;        // null: no update
+  float* latent_res;
+  float* g_scale;          // may be null
+  float* g_w;              // may be null
+};
+hipError_t packed_weight_finish(hipStream_t s, const PackedFinish& f);
+
+// Latent -> bits (row-major) and, if bits_t is non-null, the transposed bits.
+hipError_t pack_latent_bits(hipStream_t s, const uint16_t* latent, long out, long in,
+                            uint32_t* bits, uint32_t* bits_t);
+hipError_t transpose_bits(hipStream_t s, const uint32_t* bits, long out, long in,
+                          uint32_t* bits_t);
+
+// -------------------------------------------------------------- fp16 linear
+
+// y = x . W^T (W f16 [out, in]); same output options as packed_forward (no
+// bias/scale) plus the fused residual add.
+hipError_t fp16_forward(hipStream_t s, const void* x, int x_dtype, long rows, long in, long out,
+                        const uint16_t* w, float* y32, const float* resid, uint16_t* y16);
+
+// gX = gY . W -> fp32, or with key16 set: fp16 2*k*gX for k > 0 (CMix ReLU^2
+// backward, kept in the gy-scaled domain) written to gk16.
+hipError_t fp16_backward_input(hipStream_t s, GradIn gy32, long rows, long in, long out,
+                               const uint16_t* w, float* gx, const uint16_t* key16,
+                               uint16_t* gk16);
+
+// G = gY^T . X partials [z][out][in]; x fp16 [rows, in].
+hipError_t fp16_weight_grad_partials(hipStream_t s, GradIn gy32, const uint16_t* x16, long rows,
+                                     long in, long out, int splits, float* part);
+
+// W clipped SGD from the reduced partials (g = G / gy-scale); optional g_w out.
+hipError_t fp16_weight_finish(hipStream_t s, const float* part, int splits, long out, long in,
+                              const float* amax, float lr, uint16_t* w, float* w_res,
+                              float* g_w);
+
+// ---------------------------------------------------------------- LayerNorm
+
+hipError_t layer_norm_forward(hipStream_t s, const float* x, long rows, long ch,
+                              const uint16_t* w, const uint16_t* b, float* y32, uint16_t* y16);
+
+// gx = LN backward; mode 0 store, 1 accumulate (gx += ...). amax (optional)
+// receives max |gx result|. Column partials go to part[nblk][2][ch];
+// returns nblk through *nblk_out.
+hipError_t layer_norm_backward_rows(hipStream_t s, const float* x, const float* gy, long rows,
+                                    long ch, const uint16_t* w, float* gx, int accumulate,
+                                    float* amax, float* part, int* nblk_out);
+int layer_norm_backward_blocks(long rows);
+
+// Sums part[nblk][2][ch] -> gw, gb (optional outputs) and, when lr > 0,
+// clipped SGD on (w, b) with their carries.
+hipError_t layer_norm_param_finish(hipStream_t s, const float* part, int nblk, long ch, float* gw,
+                                   float* gb, float lr, uint16_t* w, float* w_res, uint16_t* b,
+                                   float* b_res);
+
+// ---------------------------------------------------------------- elementwise
+
+hipError_t fill_f32(hipStream_t s, float* p, long n, float v);
+hipError_t clipped_sgd(hipStream_t s, uint16_t* values, float* residual, const float* grad, long n,
+                       float lr);
+hipError_t binaryconnect_sgd(hipStream_t s, uint16_t* values, float* residual, const float* grad,
+                             long n, float lr, float grad_scale);
+hipError_t sign_pack_bits(hipStream_t s, const float* x, long n, uint32_t* bits);
+hipError_t amax_f32(hipStream_t s, const float* x, long n, float* slot);
+
+// shifted_j = x + (x[t-1] - x) * mix_j for up to 3 mixes (time shift per
+// sequence of length `time`; t == 0 uses -x). x fp16 [rows, ch].
+hipError_t time_shift_mix(hipStream_t s, const uint16_t* x16, long rows, long time, long ch,
+                          const uint16_t* mix0, uint16_t* out0, const uint16_t* mix1,
+                          uint16_t* out1, const uint16_t* mix2, uint16_t* out2);
+
+// lerp_shift_backward: g_x = g_s - g_s*mix + g_s[t+1]*mix (stored), and
+// g_mix[c] = sum g_s * xx with xx recomputed from x16. g_mix column partials
+// go to part[nblk][ch]; *nblk_out receives nblk.
+hipError_t time_shift_mix_backward(hipStream_t s, const float* g_shifted, const uint16_t* x16,
+                                   const uint16_t* mix, long rows, long time, long ch, float* g_x,
+                                   float* part, int* nblk_out);
+
+// Column sums of v[rows][ch] (times +-1 from idx when idx != null, i.e.
+// sum g_y * (2*idx - 1)) into part[nblk][ch].
+hipError_t column_sum_partials(hipStream_t s, const float* v, const uint8_t* idx, long rows,
+                               long ch, float* part, int* nblk_out);
+// Sums part[nblk][ch] -> out (optional) and optional clipped SGD with lr.
+hipError_t vector_finish(hipStream_t s, const float* part, int nblk, long ch, float* out,
+                         float lr, uint16_t* values, float* residual);
+
+// ROSA: idx channel-major [batch][ch][time] u8 -> y16 row-major (2*idx-1)*e
+// and the row-major idx tape.
+hipError_t rosa_expand(hipStream_t s, const uint8_t* idx_cm, const uint16_t* e, long batch,
+                       long time, long ch, uint16_t* y16, uint8_t* idx_rm);
+
+// --------------------------------------------------------------- head + CE
+
+struct HeadCe {
+  long rows, time, d, vocab;
+  const uint16_t* hidden16;  // [rows, d]
+  const uint32_t* bits;      // [vocab, d]
+  const uint32_t* bits_t;    // [d, vocab]
+  const uint16_t* scale;     // [vocab]
+  const uint16_t* bias;      // [vocab] or null
+  const uint32_t* targets;   // [rows]
+  uint32_t ignore_id;
+  // outputs
+  float* row_loss;      // [rows]
+  float* stats;         // [4]: mean_loss, n_valid, gscale, loss_sum
+  float* g_hidden;      // [rows, d] fp32
+  float* g_scale;       // [vocab] or null
+  float* g_bias;        // [vocab] or null
+  float* g_w;           // [vocab, d] or null (tests)
+  // update (lr > 0): latent step + scale clipped SGD (lr) + bias (8 lr)
+  float lr;
+  float ste;
+  uint16_t* latent;
+  float* latent_res;
+  uint16_t* scale_upd;  // scale tensor to update (same as scale) or null
+  float* scale_res;
+  uint16_t* bias_upd;
+  float* bias_res;
+  uint32_t* bits_new;   // repacked bits (may alias bits only after all reads)
+  uint32_t* bits_t_new;
+};
+size_t head_ce_workspace_bytes(long rows, long d, long vocab);
+hipError_t head_ce(hipStream_t s, const HeadCe& h, void* workspace);
+
+}  // namespace ullis

@@ -1,0 +1,371 @@
+"""Python convenience layer over the C ABI (tests, bench, smoke).
+
+`HipRuntime` mirrors the host-slice methods of the reference's `MetalRuntime`
+(src/metal.rs): numpy arrays in, numpy arrays out, one synchronous round trip
+per call. It exists for parity tests and scripts; the device-resident API is
+the C ABI itself (`DeviceBuffer` + `lib` calls), which is what `HeronTrainer`
+and bench.py use. Shape rules and error texts come from the library.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+
+F16 = _lib.F16
+F32 = _lib.F32
+
+
+class HipError(RuntimeError):
+    pass
+
+
+class DeviceBuffer:
+    """An owned device allocation."""
+
+    def __init__(self, rt: "HipRuntime", nbytes: int):
+        self.rt = rt
+        self.nbytes = int(nbytes)
+        ptr = C.c_void_p()
+        rt._check(rt.lib.ullis_hip_malloc(rt.ctx, max(self.nbytes, 4), C.byref(ptr)), "malloc")
+        self.ptr = ptr.value
+
+    def upload(self, arr: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(arr)
+        if a.nbytes > self.nbytes:
+            raise ValueError("upload larger than buffer")
+        self.rt._check(
+            self.rt.lib.ullis_hip_upload(self.rt.ctx, self.ptr, a.ctypes.data, a.nbytes), "upload")
+        return self
+
+    def download(self, dtype, count: int | None = None, offset: int = 0) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dtype.itemsize
+        out = np.empty(count, dtype=dtype)
+        if out.nbytes:
+            self.rt._check(self.rt.lib.ullis_hip_download(
+                self.rt.ctx, out.ctypes.data, self.ptr + offset, out.nbytes), "download")
+        return out
+
+    def free(self):
+        if self.ptr:
+            self.rt.lib.ullis_hip_free(self.rt.ctx, self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def f16_bits(x) -> np.ndarray:
+    return np.asarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def f16_values(bits) -> np.ndarray:
+    return np.asarray(bits, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+class HipRuntime:
+    """MetalRuntime-shaped host API over libullis_hip (src/metal.rs:466-3510)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = _lib.load()
+        ctx = C.c_void_p()
+        rc = self.lib.ullis_hip_create(device, C.byref(ctx))
+        if rc != 0:
+            raise HipError(f"ullis_hip_create failed ({rc}): no usable HIP device {device}")
+        self.ctx = ctx.value
+
+    def close(self):
+        if self.ctx:
+            self.lib.ullis_hip_destroy(self.ctx)
+            self.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc: int, what: str):
+        if rc != 0:
+            msg = self.lib.ullis_hip_last_error(self.ctx)
+            raise HipError(f"{what}: {msg.decode() if msg else ''} (status {rc})")
+
+    def sync(self):
+        self._check(self.lib.ullis_hip_sync(self.ctx), "sync")
+
+    def buffer(self, nbytes: int) -> DeviceBuffer:
+        return DeviceBuffer(self, nbytes)
+
+    def put(self, arr) -> DeviceBuffer:
+        a = np.ascontiguousarray(arr)
+        return DeviceBuffer(self, a.nbytes).upload(a)
+
+    def zeros(self, dtype, count: int) -> DeviceBuffer:
+        return self.put(np.zeros(count, dtype=dtype))
+
+    # ------------------------------------------------------------ unit ops
+    def layer_norm(self, x, weight_bits, bias_bits, rows, channels, out_dtype=np.float32):
+        dx = self.put(np.asarray(x, np.float32))
+        dw = self.put(np.asarray(weight_bits, np.uint16))
+        db = self.put(np.asarray(bias_bits, np.uint16))
+        n = rows * channels
+        if out_dtype == np.float16:
+            y = self.buffer(2 * n)
+            self._check(self.lib.ullis_hip_layer_norm(self.ctx, dx.ptr, dw.ptr, db.ptr, rows,
+                                                      channels, None, y.ptr), "layer_norm")
+            return y.download(np.uint16, n)
+        y = self.buffer(4 * n)
+        self._check(self.lib.ullis_hip_layer_norm(self.ctx, dx.ptr, dw.ptr, db.ptr, rows,
+                                                  channels, y.ptr, None), "layer_norm")
+        return y.download(np.float32, n)
+
+    def layer_norm_backward(self, x, gy, weight_bits, rows, channels):
+        dx = self.put(np.asarray(x, np.float32))
+        dg = self.put(np.asarray(gy, np.float32))
+        dw = self.put(np.asarray(weight_bits, np.uint16))
+        gx, gw, gb = self.buffer(4 * rows * channels), self.buffer(4 * channels), self.buffer(4 * channels)
+        self._check(self.lib.ullis_hip_layer_norm_backward(
+            self.ctx, dx.ptr, dg.ptr, dw.ptr, rows, channels, gx.ptr, gw.ptr, gb.ptr),
+            "layer_norm_backward")
+        return (gx.download(np.float32, rows * channels), gw.download(np.float32, channels),
+                gb.download(np.float32, channels))
+
+    def binary_linear(self, x, bits, scale_bits, bias_bits, rows, in_f, out_f, x_dtype=F16,
+                      out_dtype=np.float32):
+        xa = np.asarray(x)
+        if x_dtype == F16:
+            dx = self.put(xa.astype(np.uint16) if xa.dtype == np.uint16 else f16_bits(xa))
+        else:
+            dx = self.put(xa.astype(np.float32))
+        db = self.put(np.asarray(bits, np.uint32))
+        ds = self.put(np.asarray(scale_bits, np.uint16))
+        dbias = self.put(np.asarray(bias_bits, np.uint16)) if bias_bits is not None else None
+        n = rows * out_f
+        y = self.buffer((2 if out_dtype == np.float16 else 4) * n)
+        self._check(self.lib.ullis_hip_binary_linear(
+            self.ctx, dx.ptr, x_dtype, db.ptr, ds.ptr, dbias.ptr if dbias else None, rows, in_f,
+            out_f, None if out_dtype == np.float16 else y.ptr,
+            y.ptr if out_dtype == np.float16 else None), "binary_linear")
+        return y.download(np.uint16 if out_dtype == np.float16 else np.float32, n)
+
+    def binary_linear_backward(self, x16_bits, gy, bits, scale_bits, has_bias, rows, in_f, out_f):
+        dx = self.put(np.asarray(x16_bits, np.uint16))
+        dg = self.put(np.asarray(gy, np.float32))
+        db = self.put(np.asarray(bits, np.uint32))
+        ds = self.put(np.asarray(scale_bits, np.uint16))
+        gx = self.buffer(4 * rows * in_f)
+        gw = self.buffer(4 * out_f * in_f)
+        gs = self.buffer(4 * out_f)
+        gb = self.buffer(4 * out_f)
+        self._check(self.lib.ullis_hip_binary_linear_backward(
+            self.ctx, dx.ptr, dg.ptr, db.ptr, ds.ptr, int(has_bias), rows, in_f, out_f, gx.ptr,
+            gw.ptr, gs.ptr, gb.ptr), "binary_linear_backward")
+        return {
+            "input_gradient": gx.download(np.float32, rows * in_f),
+            "weight_gradient": gw.download(np.float32, out_f * in_f),
+            "scale_gradient": gs.download(np.float32, out_f),
+            "bias_gradient": gb.download(np.float32, out_f) if has_bias else None,
+        }
+
+    def apply_latent_sgd(self, latent_bits, residual, gradient, out_f, in_f, lr, ste):
+        dl = self.put(np.asarray(latent_bits, np.uint16))
+        dr = self.put(np.asarray(residual, np.float32))
+        dg = self.put(np.asarray(gradient, np.float32))
+        words = (out_f * in_f + 31) // 32
+        bits = self.buffer(4 * words)
+        bits_t = self.buffer(4 * words)
+        self._check(self.lib.ullis_hip_apply_latent_sgd(
+            self.ctx, dl.ptr, dr.ptr, dg.ptr, out_f, in_f, lr, ste, bits.ptr, bits_t.ptr),
+            "apply_latent_sgd")
+        n = out_f * in_f
+        return (dl.download(np.uint16, n), dr.download(np.float32, n),
+                bits.download(np.uint32, words), bits_t.download(np.uint32, words))
+
+    def fp16_linear(self, x, w_bits, rows, in_f, out_f, x_dtype=F16):
+        xa = np.asarray(x)
+        dx = self.put(f16_bits(xa) if x_dtype == F16 and xa.dtype != np.uint16 else
+                      (xa if x_dtype == F16 else xa.astype(np.float32)))
+        dw = self.put(np.asarray(w_bits, np.uint16))
+        y = self.buffer(4 * rows * out_f)
+        self._check(self.lib.ullis_hip_fp16_linear(self.ctx, dx.ptr, x_dtype, dw.ptr, rows, in_f,
+                                                   out_f, y.ptr, None), "fp16_linear")
+        return y.download(np.float32, rows * out_f)
+
+    def fp16_linear_backward(self, x16_bits, gy, w_bits, rows, in_f, out_f):
+        dx = self.put(np.asarray(x16_bits, np.uint16))
+        dg = self.put(np.asarray(gy, np.float32))
+        dw = self.put(np.asarray(w_bits, np.uint16))
+        gx = self.buffer(4 * rows * in_f)
+        gw = self.buffer(4 * out_f * in_f)
+        self._check(self.lib.ullis_hip_fp16_linear_backward(
+            self.ctx, dx.ptr, dg.ptr, dw.ptr, rows, in_f, out_f, gx.ptr, gw.ptr),
+            "fp16_linear_backward")
+        return gx.download(np.float32, rows * in_f), gw.download(np.float32, out_f * in_f)
+
+    def clipped_sgd_fp16(self, params, residual, gradient, lr):
+        p, r, g = self.put(np.asarray(params, np.uint16)), self.put(np.asarray(residual, np.float32)), \
+            self.put(np.asarray(gradient, np.float32))
+        n = len(params)
+        self._check(self.lib.ullis_hip_clipped_sgd_fp16(self.ctx, p.ptr, r.ptr, g.ptr, n, lr),
+                    "clipped_sgd_fp16")
+        return p.download(np.uint16, n), r.download(np.float32, n)
+
+    def binaryconnect_sgd_fp16(self, params, residual, gradient, lr):
+        p, r, g = self.put(np.asarray(params, np.uint16)), self.put(np.asarray(residual, np.float32)), \
+            self.put(np.asarray(gradient, np.float32))
+        n = len(params)
+        self._check(self.lib.ullis_hip_binaryconnect_sgd_fp16(self.ctx, p.ptr, r.ptr, g.ptr, n, lr),
+                    "binaryconnect_sgd_fp16")
+        return p.download(np.uint16, n), r.download(np.float32, n)
+
+    def sign_pack_bits(self, x):
+        xa = np.asarray(x, np.float32)
+        dx = self.put(xa)
+        words = (xa.size + 31) // 32
+        b = self.buffer(4 * words)
+        self._check(self.lib.ullis_hip_sign_pack_bits(self.ctx, dx.ptr, xa.size, b.ptr),
+                    "sign_pack_bits")
+        return b.download(np.uint32, words)
+
+    def transpose_bits(self, bits, out_f, in_f):
+        db = self.put(np.asarray(bits, np.uint32))
+        words = (out_f * in_f + 31) // 32
+        bt = self.buffer(4 * words)
+        self._check(self.lib.ullis_hip_transpose_bits(self.ctx, db.ptr, out_f, in_f, bt.ptr),
+                    "transpose_bits")
+        return bt.download(np.uint32, words)
+
+    def packed_head_train_sgd(self, hidden16_bits, bits, scale_bits, bias_bits, latent_bits,
+                              latent_res, scale_res, bias_res, targets, rows, time, d, vocab,
+                              ignore_id, lr, ste, want_g_w=False):
+        """Head + streamed CE (+ update when lr > 0). Returns a dict of host arrays."""
+        words = (vocab * d + 31) // 32
+        dh = self.put(np.asarray(hidden16_bits, np.uint16))
+        db = self.put(np.asarray(bits, np.uint32))
+        dbt = self.buffer(4 * words)
+        self._check(self.lib.ullis_hip_transpose_bits(self.ctx, db.ptr, vocab, d, dbt.ptr),
+                    "transpose_bits")
+        ds = self.put(np.asarray(scale_bits, np.uint16))
+        dbias = self.put(np.asarray(bias_bits, np.uint16)) if bias_bits is not None else None
+        dl = self.put(np.asarray(latent_bits, np.uint16))
+        dlr = self.put(np.asarray(latent_res, np.float32))
+        dsr = self.put(np.asarray(scale_res, np.float32))
+        dbr = self.put(np.asarray(bias_res, np.float32)) if bias_bits is not None else None
+        dt = self.put(np.asarray(targets, np.uint32))
+        row_loss = self.buffer(4 * rows)
+        stats = self.buffer(16)
+        g_hidden = self.buffer(4 * rows * d)
+        g_scale = self.buffer(4 * vocab)
+        g_bias = self.buffer(4 * vocab)
+        g_w = self.buffer(4 * vocab * d) if want_g_w else None
+        self._check(self.lib.ullis_hip_packed_head_train_sgd(
+            self.ctx, dh.ptr, db.ptr, dbt.ptr, ds.ptr, dbias.ptr if dbias else None, dl.ptr,
+            dlr.ptr, dsr.ptr, dbr.ptr if dbr else None, dt.ptr, rows, time, d, vocab, ignore_id,
+            lr, ste, row_loss.ptr, stats.ptr, g_hidden.ptr, g_scale.ptr, g_bias.ptr,
+            g_w.ptr if g_w else None), "packed_head_train_sgd")
+        st = stats.download(np.float32, 4)
+        out = {
+            "mean_loss": float(st[0]), "n_valid": int(st[1]), "gradient_scale": float(st[2]),
+            "row_loss": row_loss.download(np.float32, rows),
+            "hidden_gradient": g_hidden.download(np.float32, rows * d),
+            "scale_gradient": g_scale.download(np.float32, vocab),
+            "bias_gradient": g_bias.download(np.float32, vocab),
+            "next_bits": db.download(np.uint32, words),
+            "next_bits_t": dbt.download(np.uint32, words),
+            "next_latent": dl.download(np.uint16, vocab * d),
+            "next_residual": dlr.download(np.float32, vocab * d),
+            "next_scale": ds.download(np.uint16, vocab),
+            "next_scale_residual": dsr.download(np.float32, vocab),
+        }
+        if dbias is not None:
+            out["next_bias"] = dbias.download(np.uint16, vocab)
+            out["next_bias_residual"] = dbr.download(np.float32, vocab)
+        if g_w is not None:
+            out["weight_gradient"] = g_w.download(np.float32, vocab * d)
+        return out
+
+
+@dataclass
+class HeronShape:
+    d_model: int
+    n_layers: int
+    dim_ffn: int
+    vocab: int
+    batch: int
+    time: int
+
+    @property
+    def rows(self) -> int:
+        return self.batch * self.time
+
+    def dims(self) -> _lib.HeronDims:
+        return _lib.HeronDims(self.d_model, self.n_layers, self.dim_ffn, self.vocab)
+
+
+def heron_layout(dims: _lib.HeronDims, lib=None):
+    """[(name, dtype, count, offset, derived)], total bytes - via the library export."""
+    lib = lib or _lib.load()
+    total = C.c_uint64()
+    n = lib.ullis_hip_heron_layout(C.byref(dims), None, 0, C.byref(total))
+    arr = (_lib.TensorDesc * n)()
+    lib.ullis_hip_heron_layout(C.byref(dims), arr, n, C.byref(total))
+    out = [(d.name.decode(), d.dtype, d.count, d.offset, d.derived) for d in arr]
+    return out, total.value
+
+
+class HeronTrainer:
+    """Device-resident Heron train step (ullis_hip_heron_*)."""
+
+    def __init__(self, rt: HipRuntime, shape: HeronShape):
+        self.rt = rt
+        self.shape = shape
+        self._dims = shape.dims()
+        h = C.c_void_p()
+        rt._check(rt.lib.ullis_hip_heron_create(rt.ctx, C.byref(self._dims), shape.batch,
+                                                shape.time, C.byref(h)), "heron_create")
+        self.h = h.value
+        ptr, nbytes = C.c_void_p(), C.c_uint64()
+        rt._check(rt.lib.ullis_hip_heron_arena(self.h, C.byref(ptr), C.byref(nbytes)), "arena")
+        self.arena_ptr, self.arena_bytes = ptr.value, nbytes.value
+        self.layout, total = heron_layout(self._dims, rt.lib)
+        assert total == self.arena_bytes
+
+    def close(self):
+        if self.h:
+            self.rt.lib.ullis_hip_heron_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def upload_arena(self, arena: np.ndarray):
+        a = np.ascontiguousarray(arena, dtype=np.uint8)
+        assert a.nbytes == self.arena_bytes
+        self.rt._check(self.rt.lib.ullis_hip_upload(self.rt.ctx, self.arena_ptr, a.ctypes.data,
+                                                    a.nbytes), "arena upload")
+        self.rt._check(self.rt.lib.ullis_hip_heron_refresh_derived(self.h), "refresh derived")
+
+    def download_arena(self) -> np.ndarray:
+        out = np.empty(self.arena_bytes, dtype=np.uint8)
+        self.rt._check(self.rt.lib.ullis_hip_download(self.rt.ctx, out.ctypes.data,
+                                                      self.arena_ptr, out.nbytes), "arena download")
+        return out
+
+    def step(self, x_emb: DeviceBuffer, labels: DeviceBuffer, ignore_id: int, lr: float,
+             rosa_idx: DeviceBuffer, g_emb: DeviceBuffer, row_loss: DeviceBuffer | None = None,
+             stats: DeviceBuffer | None = None, qkv_bits: DeviceBuffer | None = None):
+        self.rt._check(self.rt.lib.ullis_hip_heron_step(
+            self.h, x_emb.ptr, labels.ptr, ignore_id, lr, rosa_idx.ptr, g_emb.ptr,
+            row_loss.ptr if row_loss else None, stats.ptr if stats else None,
+            qkv_bits.ptr if qkv_bits else None), "heron_step")
