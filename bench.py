@@ -1,0 +1,163 @@
+#!/usr/bin/env python3
+"""Heron train-step throughput on one MI355X (BASELINE.json metric).
+
+Workload (config 4): one full Heron train step's GPU work, D=512, L=12,
+T=2048, vocab 8192, F=2048, batch 1, rosa_grad = stop_grad_bits, with the
+suffix-automaton output synthesised as Bernoulli(0.5) indices (+-e). Inputs
+are resident in HBM before the timed region; a step is ullis_hip_heron_step
+(forward, head + streamed CE, backward, every parameter update). The timed
+region is bracketed by stream synchronisation; HIP events on the library's
+stream give the step time.
+
+Prints ONE JSON line. `roofline` is for the kernel that dominates the step,
+timed with events around its own launches inside the timed region (see
+ullis_hip_heron_probe). `cpu_baseline` times the CPU oracle (a port of the
+reference's CPU backend) single-threaded on a bounded sample of the same
+workload (fewer rows, same widths and depth), scaled per token.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+CONFIG = dict(d_model=512, n_layers=12, dim_ffn=2048, vocab=8192, batch=1, time=2048)
+LR = 0.01
+NO_IGNORE = 0xFFFFFFFF
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2516.6  # dense fp16 MFMA, MI355X
+
+
+def cpu_baseline(rows: int) -> dict:
+    from oracle import cpu_ref as o
+    from ullis_amd.synth import heron_arena, step_inputs
+
+    c = CONFIG
+    dims = o.HeronDims(c["d_model"], c["n_layers"], c["dim_ffn"], c["vocab"])
+    lay, total = o.heron_layout(dims)
+    arena = heron_arena(lay, total, dims, seed=7)
+    x, labels, idx = step_inputs(rows, c["d_model"], c["vocab"], c["n_layers"], 1, rows, seed=7)
+    t0 = time.perf_counter()
+    o.heron_train_step(dims, arena, x, labels, NO_IGNORE, 1, rows, LR, idx, want_qkv=True)
+    dt = time.perf_counter() - t0
+    return {
+        "value": rows / dt,
+        "unit": "tokens/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"oracle/cpu_ref.c heron step D512 L12 F2048 V8192, one window of T={rows} "
+                   f"tokens (full widths and depth), single thread, {dt:.1f} s; tokens/s scales "
+                   "linearly in T for every op except the per-weight SGD, which this sample "
+                   "charges to fewer tokens"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--cpu-rows", type=int, default=64,
+                    help="rows of the CPU-baseline sample (0 disables it)")
+    ap.add_argument("--probe", default="key_forward",
+                    help="launch class timed for the roofline object")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build measures one MI355X only (no multi-GPU path); "
+              "run with --gpus 1", file=sys.stderr)
+        return 2
+
+    from ullis_amd.runtime import HeronShape, HeronTrainer, HipRuntime
+    from ullis_amd.synth import heron_arena, step_inputs
+
+    c = CONFIG
+    shape = HeronShape(**c)
+    rt = HipRuntime(0)
+    trainer = HeronTrainer(rt, shape)
+    arena = heron_arena(trainer.layout, trainer.arena_bytes, shape.dims(), seed=7)
+    trainer.upload_arena(arena)
+    x, labels, idx = step_inputs(shape.rows, c["d_model"], c["vocab"], c["n_layers"], c["batch"],
+                                 c["time"], seed=7)
+    dx, dl, di = rt.put(x), rt.put(labels), rt.put(idx)
+    g = rt.zeros(np.float32, shape.rows * c["d_model"])
+    rl = rt.zeros(np.float32, shape.rows)
+    st = rt.zeros(np.float32, 4)
+    words = (shape.rows * c["d_model"] + 31) // 32
+    qkv = rt.zeros(np.uint32, c["n_layers"] * 3 * words)
+
+    def step():
+        trainer.step(dx, dl, NO_IGNORE, LR, di, g, rl, st, qkv)
+
+    for _ in range(args.warmup):
+        step()
+    rt.sync()
+    probe = trainer.probe_begin(args.probe)
+    lib, ctx = rt.lib, rt.ctx
+    rt._check(lib.ullis_hip_event_record(ctx, 0), "event")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    rt._check(lib.ullis_hip_event_record(ctx, 1), "event")
+    rt.sync()
+    wall = time.perf_counter() - t0
+    import ctypes as C
+
+    ms = C.c_float()
+    rt._check(lib.ullis_hip_event_elapsed_ms(ctx, 0, 1, C.byref(ms)), "elapsed")
+    ms_per_step = ms.value / args.steps
+    tokens = shape.rows * args.steps
+    value = tokens / (ms.value / 1e3)
+    kernel = trainer.probe_end(probe)
+    loss = float(st.download(np.float32, 4)[0])
+
+    roofline = None
+    if kernel and kernel["count"]:
+        avg_s = kernel["total_ms"] / kernel["count"] / 1e3
+        achieved = kernel["work"] / avg_s / (1e12 if kernel["bound"] == "mfma" else 1e9)
+        peak = FP16_PEAK_TFLOPS if kernel["bound"] == "mfma" else HBM_PEAK_GBS
+        roofline = {
+            "bound": kernel["bound"], "achieved": round(achieved, 2), "peak": peak,
+            "unit": "TFLOP/s" if kernel["bound"] == "mfma" else "GB/s",
+            "frac": round(achieved / peak, 4), "traffic": kernel.get("traffic"),
+            "kernel": kernel["name"], "avg_us": round(avg_s * 1e6, 2),
+            "launches": kernel["count"],
+        }
+
+    baseline = cpu_baseline(args.cpu_rows) if args.cpu_rows > 0 else None
+    line = {
+        "metric": "train tokens/s (heron D512 L12 T2048)",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded; random-init heron parameters, ROSA indices Bernoulli(0.5))",
+        "config": {"workload": "heron train step (config 4): D512 L12 F2048 V8192 T2048 B1, "
+                               "stop_grad_bits, lr 0.01",
+                   "global_batch": c["batch"], "seq_len": c["time"], "parallelism": "none (1 GPU)"},
+        "wall_s": round(wall, 3),
+        "loss_last_step": round(loss, 5),
+        "roofline": roofline,
+        "cpu_baseline": baseline,
+    }
+    print(json.dumps(line), flush=True)
+    trainer.close()
+    rt.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

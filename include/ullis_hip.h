@@ -168,6 +168,27 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
                          uint32_t ignore_id, float learning_rate, const uint8_t* rosa_idx,
                          float* g_emb, float* row_loss, float* stats4, uint32_t* qkv_bits);
 
+/*
+ * Kernel probe, the device-side counterpart of the reference's per-phase
+ * TrainStepProfile (src/model.rs:101-124): while a probe id is set, every
+ * launch of that class inside ullis_hip_heron_step is bracketed by HIP events
+ * on the step's stream (at most 512 launches are recorded). probe_read waits
+ * for the recorded events and returns the summed kernel time and the number
+ * of launches, then restarts the count.
+ */
+#define ULLIS_HIP_PROBE_NONE 0
+#define ULLIS_HIP_PROBE_KEY_FORWARD 1       /* CMix key packed GEMM + ReLU^2, per layer */
+#define ULLIS_HIP_PROBE_VALUE_FORWARD 2     /* CMix value fp16 GEMM + residual add */
+#define ULLIS_HIP_PROBE_HEAD_CE 3           /* whole head + streamed CE (several kernels) */
+#define ULLIS_HIP_PROBE_VALUE_INPUT_GRAD 4  /* value dX GEMM + ReLU^2 backward */
+#define ULLIS_HIP_PROBE_KEY_INPUT_GRAD 5    /* key dX packed GEMM */
+#define ULLIS_HIP_PROBE_KEY_WEIGHT_GRAD 6   /* key dW GEMM (partials) */
+#define ULLIS_HIP_PROBE_LN_FORWARD 7        /* ln2 forward */
+#define ULLIS_HIP_PROBE_LN_BACKWARD 8       /* ln2 backward rows */
+#define ULLIS_HIP_PROBE_COUNT 9
+int ullis_hip_heron_probe(ullis_hip_heron* h, int probe_id);
+int ullis_hip_heron_probe_read(ullis_hip_heron* h, float* total_ms, int* launches);
+
 #ifdef __cplusplus
 }
 #endif

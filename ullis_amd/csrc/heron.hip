@@ -75,6 +75,10 @@ struct ullis_hip_heron {
   uint32_t* qkv = nullptr;
   void* head_ws = nullptr;
   int splits_o = 1, splits_key = 1, splits_value = 1;
+  // kernel probe: events around every launch of one launch class
+  int probe = 0;
+  int probe_used = 0;
+  std::vector<hipEvent_t> probe_events;
 
   template <class T>
   T* tensor(const std::string& name) {
@@ -115,6 +119,20 @@ bool bind_packed(ullis_hip_heron* h, const std::string& p, long out, long in, bo
 #define STEP(expr, what)                              \
   do {                                                \
     if (int rc_ = c->hip((expr), (what))) return rc_; \
+  } while (0)
+
+constexpr int kProbeMax = 512;
+
+// Brackets one launch with events when `id` is the probed launch class.
+#define PROBED(id, expr, what)                                                       \
+  do {                                                                               \
+    const bool on_ = h->probe == (id) && h->probe_used < kProbeMax;                  \
+    if (on_) STEP(hipEventRecord(h->probe_events[2 * h->probe_used], s), "probe");   \
+    STEP(expr, what);                                                                \
+    if (on_) {                                                                       \
+      STEP(hipEventRecord(h->probe_events[2 * h->probe_used + 1], s), "probe");      \
+      ++h->probe_used;                                                               \
+    }                                                                                \
   } while (0)
 
 }  // namespace
@@ -249,6 +267,14 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
   h->row_loss = cv.take<float>(R);
   h->qkv = cv.take<uint32_t>(words * 3 * L);
   h->head_ws = cv.take<char>(head_ws);
+  h->probe_events.resize(2 * kProbeMax);
+  for (auto& e : h->probe_events) {
+    if (hipEventCreate(&e) != hipSuccess) {
+      e = nullptr;
+      ullis_hip_heron_destroy(h);
+      return c->fail(ULLIS_HIP_ERR_RUNTIME, "probe event creation failed");
+    }
+  }
   if (int rc = c->hip(hipStreamSynchronize(c->stream), "heron create")) {
     ullis_hip_heron_destroy(h);
     return rc;
@@ -260,6 +286,7 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
 void ullis_hip_heron_destroy(ullis_hip_heron* h) {
   if (!h) return;
   if (h->ctx) (void)hipStreamSynchronize(h->ctx->stream);
+  for (auto& e : h->probe_events) (void)hipEventDestroy(e);
   if (h->arena) (void)hipFree(h->arena);
   if (h->act) (void)hipFree(h->act);
   delete h;
@@ -269,6 +296,30 @@ int ullis_hip_heron_arena(ullis_hip_heron* h, void** device_ptr, uint64_t* bytes
   if (!h || !device_ptr || !bytes) return ULLIS_HIP_ERR_INVALID;
   *device_ptr = h->arena;
   *bytes = h->arena_bytes;
+  return 0;
+}
+
+int ullis_hip_heron_probe(ullis_hip_heron* h, int probe_id) {
+  if (!h || probe_id < 0 || probe_id >= ULLIS_HIP_PROBE_COUNT) return ULLIS_HIP_ERR_INVALID;
+  h->probe = probe_id;
+  h->probe_used = 0;
+  return 0;
+}
+
+int ullis_hip_heron_probe_read(ullis_hip_heron* h, float* total_ms, int* launches) {
+  if (!h || !total_ms || !launches) return ULLIS_HIP_ERR_INVALID;
+  ullis_hip_ctx* c = h->ctx;
+  double sum = 0.0;
+  for (int i = 0; i < h->probe_used; ++i) {
+    float ms = 0.0f;
+    STEP(hipEventSynchronize(h->probe_events[2 * i + 1]), "probe sync");
+    STEP(hipEventElapsedTime(&ms, h->probe_events[2 * i], h->probe_events[2 * i + 1]),
+         "probe elapsed");
+    sum += ms;
+  }
+  *total_ms = (float)sum;
+  *launches = h->probe_used;
+  h->probe_used = 0;
   return 0;
 }
 
@@ -341,16 +392,19 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
     uint16_t* sh = h->shifted16 + l * nd;
     uint16_t* key = h->key16 + l * nf;
     uint16_t* r2 = h->relu2_16 + l * nf;
-    STEP(layer_norm_forward(s, ar, R, D, b.ln2.w, b.ln2.b, nullptr, ln2), "ln2");
+    PROBED(ULLIS_HIP_PROBE_LN_FORWARD,
+           layer_norm_forward(s, ar, R, D, b.ln2.w, b.ln2.b, nullptr, ln2), "ln2");
     STEP(time_shift_mix(s, ln2, R, T, D, b.cx_k, sh, nullptr, nullptr, nullptr, nullptr), "mix");
     {
       PackedFwdOut o;
       o.y16 = key;
       o.relu2_16 = r2;
-      STEP(packed_forward(s, sh, kF16, R, D, F, b.key.bits, b.key.scale, nullptr, o), "key");
+      PROBED(ULLIS_HIP_PROBE_KEY_FORWARD,
+             packed_forward(s, sh, kF16, R, D, F, b.key.bits, b.key.scale, nullptr, o), "key");
     }
-    STEP(fp16_forward(s, r2, kF16, R, F, D, b.value, h->resid + (l + 1) * nd, ar, nullptr),
-         "value");
+    PROBED(ULLIS_HIP_PROBE_VALUE_FORWARD,
+           fp16_forward(s, r2, kF16, R, F, D, b.value, h->resid + (l + 1) * nd, ar, nullptr),
+           "value");
   }
   float* x_last = h->resid + L * nd;
   STEP(layer_norm_forward(s, x_last, R, D, h->ln_out.w, h->ln_out.b, nullptr, h->ln16), "ln_out");
@@ -383,7 +437,7 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
     hc.bias_res = h->head.bias_res;
     hc.bits_new = h->head.bits;
     hc.bits_t_new = h->head.bits_t;
-    STEP(head_ce(s, hc, h->head_ws), "head ce");
+    PROBED(ULLIS_HIP_PROBE_HEAD_CE, head_ce(s, hc, h->head_ws), "head ce");
   }
   // LN_out backward + step (src/model.rs:2932-2937)
   STEP(layer_norm_backward_rows(s, x_last, h->g_a, R, D, h->ln_out.w, h->g_x, 0, h->slots + L,
@@ -405,20 +459,23 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
     const float* ar = h->after_rosa + l * nd;
 
     // CMix backward_update (src/model.rs:1145-1177)
-    STEP(fp16_backward_input(s, GradIn{h->g_x, slot_in}, R, F, D, b.value, nullptr, key, h->gk16),
-         "value input grad + relu2 bwd");
+    PROBED(ULLIS_HIP_PROBE_VALUE_INPUT_GRAD,
+           fp16_backward_input(s, GradIn{h->g_x, slot_in}, R, F, D, b.value, nullptr, key, h->gk16),
+           "value input grad + relu2 bwd");
     STEP(fp16_weight_grad_partials(s, GradIn{h->g_x, slot_in}, r2, R, F, D, h->splits_value,
                                    h->gpart),
          "value weight grad");
     STEP(fp16_weight_finish(s, h->gpart, h->splits_value, D, F, slot_in, lr, b.value, b.value_res,
                             nullptr),
          "value step");
-    STEP(packed_backward_input(s, GradIn{nullptr, slot_in}, h->gk16, R, D, F, b.key.bits_t,
-                               b.key.scale, h->g_a, nullptr, 0),
-         "key input grad");
-    STEP(packed_weight_grad_partials(s, GradIn{nullptr, slot_in}, h->gk16, sh, R, D, F,
-                                     h->splits_key, h->gpart),
-         "key weight grad");
+    PROBED(ULLIS_HIP_PROBE_KEY_INPUT_GRAD,
+           packed_backward_input(s, GradIn{nullptr, slot_in}, h->gk16, R, D, F, b.key.bits_t,
+                                 b.key.scale, h->g_a, nullptr, 0),
+           "key input grad");
+    PROBED(ULLIS_HIP_PROBE_KEY_WEIGHT_GRAD,
+           packed_weight_grad_partials(s, GradIn{nullptr, slot_in}, h->gk16, sh, R, D, F,
+                                       h->splits_key, h->gpart),
+           "key weight grad");
     {
       PackedFinish f;
       f.part = h->gpart;
@@ -444,8 +501,10 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
     STEP(vector_finish(s, h->part, nb, D, nullptr, lr, b.cx_k, b.cx_k_res), "x_k step");
 
     // LN2 backward, += into g_x (src/model.rs:2958-2963)
-    STEP(layer_norm_backward_rows(s, ar, h->g_b, R, D, b.ln2.w, h->g_x, 1, slot_mid, h->part, &nb),
-         "ln2 bwd");
+    PROBED(ULLIS_HIP_PROBE_LN_BACKWARD,
+           layer_norm_backward_rows(s, ar, h->g_b, R, D, b.ln2.w, h->g_x, 1, slot_mid, h->part,
+                                    &nb),
+           "ln2 bwd");
     STEP(layer_norm_param_finish(s, h->part, nb, D, nullptr, nullptr, lr, b.ln2.w, b.ln2.w_res,
                                  b.ln2.b, b.ln2.b_res),
          "ln2 step");

@@ -349,6 +349,35 @@ class HeronTrainer:
         except Exception:
             pass
 
+    # probe name -> (id, roofline bound, algorithmic work per launch, kernel label)
+    def probes(self):
+        s = self.shape
+        r, d, f, v = s.rows, s.d_model, s.dim_ffn, s.vocab
+        return {
+            "key_forward": (1, "mfma", 2.0 * r * d * f, "packed +-1 GEMM: CMix key fwd + ReLU^2"),
+            "value_forward": (2, "mfma", 2.0 * r * f * d, "fp16 GEMM: CMix value fwd + residual"),
+            "head_ce": (3, "mfma", 3 * 2.0 * r * d * v, "head + streamed CE (whole op)"),
+            "value_input_grad": (4, "mfma", 2.0 * r * d * f, "fp16 GEMM: value dX + ReLU^2 bwd"),
+            "key_input_grad": (5, "mfma", 2.0 * r * f * d, "packed +-1 GEMM: key dX"),
+            "key_weight_grad": (6, "mfma", 2.0 * r * f * d, "key dW GEMM"),
+            "ln_forward": (7, "hbm", r * d * (4 + 2) + 4.0 * d, "LayerNorm fwd (ln2)"),
+            "ln_backward": (8, "hbm", r * d * 16 + 2.0 * d, "LayerNorm bwd rows (ln2, += g_x)"),
+        }
+
+    def probe_begin(self, name: str = "key_forward") -> str:
+        pid = self.probes()[name][0]
+        self.rt._check(self.rt.lib.ullis_hip_heron_probe(self.h, pid), "probe")
+        return name
+
+    def probe_end(self, name: str) -> dict:
+        total, count = C.c_float(), C.c_int()
+        self.rt._check(self.rt.lib.ullis_hip_heron_probe_read(self.h, C.byref(total),
+                                                              C.byref(count)), "probe read")
+        self.rt._check(self.rt.lib.ullis_hip_heron_probe(self.h, 0), "probe off")
+        pid, bound, work, label = self.probes()[name]
+        return {"name": label, "probe": name, "bound": bound, "work": work,
+                "total_ms": total.value, "count": count.value}
+
     def upload_arena(self, arena: np.ndarray):
         a = np.ascontiguousarray(arena, dtype=np.uint8)
         assert a.nbytes == self.arena_bytes
