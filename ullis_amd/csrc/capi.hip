@@ -233,7 +233,7 @@ int ullis_hip_binary_linear_backward(ullis_hip_ctx* c, const uint16_t* x16, cons
   const long R = (long)rows, I = (long)in, O = (long)out;
   const int splits = dw_splits(O, I, R);
   const long words = cdiv(I * O, 32);
-  const long nb = cdiv(R, 64);
+  const long nb = column_partial_blocks(R);
   const size_t need = Carver::bytes_for(4 * words) + Carver::bytes_for(4ul * splits * O * I) +
                       Carver::bytes_for(4) + Carver::bytes_for(4ul * nb * O);
   void* ws = nullptr;

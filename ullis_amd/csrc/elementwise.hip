@@ -18,7 +18,7 @@ namespace ullis {
 
 namespace {
 
-constexpr int kColChunkRows = 64;
+constexpr int kColChunkRows = 16;
 
 __global__ void fill_kernel(float* p, long n, float v) {
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -119,14 +119,33 @@ __global__ void column_sum_kernel(const float* v, const uint8_t* idx, long rows,
   part[(long)blockIdx.y * ch + c] = s;
 }
 
-__global__ void vector_finish_kernel(const float* part, int nblk, long ch, float* out, float lr,
-                                     uint16_t* values, float* residual) {
-  const long c = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= ch) return;
+// Sums part[nblk][ncols] over nblk: 64 columns per block, 16 partial subsets
+// per column summed in a fixed order (strided, then an LDS tree), so the result
+// does not depend on scheduling. Columns < split go to target a, the rest to b.
+__global__ __launch_bounds__(1024) void partial_reduce_kernel(const float* part, int nblk,
+                                                              long ncols, long split, VecTarget a,
+                                                              VecTarget b) {
+  __shared__ float red[16][64];
+  const int lc = threadIdx.x & 63, sub = threadIdx.x >> 6;
+  const long col = (long)blockIdx.x * 64 + lc;
   float s = 0.0f;
-  for (int k = 0; k < nblk; ++k) s += part[(long)k * ch + c];
-  if (out) out[c] = s;
-  if (values && lr > 0.0f) clipped_sgd_one(values[c], residual[c], s, lr);
+  if (col < ncols)
+    for (int k = sub; k < nblk; k += 16) s += part[(long)k * ncols + col];
+  red[sub][lc] = s;
+  __syncthreads();
+  for (int st = 8; st > 0; st >>= 1) {
+    if (sub < st) red[sub][lc] += red[sub + st][lc];
+    __syncthreads();
+  }
+  if (sub == 0 && col < ncols) {
+    const bool first = col < split;
+    const VecTarget& t = first ? a : b;
+    const long i = first ? col : col - split;
+    float v = red[0][lc];
+    if (t.mul) v *= *t.mul;
+    if (t.out) t.out[i] = v;
+    if (t.values && t.lr > 0.0f) clipped_sgd_one(t.values[i], t.residual[i], v, t.lr);
+  }
 }
 
 __global__ void rosa_expand_kernel(const uint8_t* idx_cm, const uint16_t* e, long batch, long time,
@@ -214,12 +233,18 @@ hipError_t column_sum_partials(hipStream_t s, const float* v, const uint8_t* idx
   return hipGetLastError();
 }
 
+hipError_t partial_reduce(hipStream_t s, const float* part, int nblk, long ncols, long split,
+                          const VecTarget& a, const VecTarget& b) {
+  if (ncols <= 0) return hipSuccess;
+  hipLaunchKernelGGL(partial_reduce_kernel, dim3((unsigned)cdiv(ncols, 64)), dim3(1024), 0, s,
+                     part, nblk, ncols, split, a, b);
+  return hipGetLastError();
+}
+
 hipError_t vector_finish(hipStream_t s, const float* part, int nblk, long ch, float* out,
                          float lr, uint16_t* values, float* residual) {
-  if (ch <= 0) return hipSuccess;
-  hipLaunchKernelGGL(vector_finish_kernel, grid1d(ch), dim3(256), 0, s, part, nblk, ch, out, lr,
-                     values, residual);
-  return hipGetLastError();
+  VecTarget a{out, values, residual, lr, nullptr};
+  return partial_reduce(s, part, nblk, ch, ch, a, a);
 }
 
 hipError_t rosa_expand(hipStream_t s, const uint8_t* idx_cm, const uint16_t* e, long batch,

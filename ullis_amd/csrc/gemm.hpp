@@ -2,21 +2,28 @@
 //
 // One block = 256 threads = 4 wave64s in a 2x2 grid; each wave owns a
 // (BM/2) x (BN/2) sub-tile made of 32x32 v_mfma_f32_32x32x16_f16 tiles with
-// fp32 accumulation. The K loop steps BK = 32 with two LDS buffers: global
-// loads for step k+1 are issued before the MFMAs of step k and stored to the
-// other LDS buffer afterwards, so one barrier per step suffices.
+// fp32 accumulation. The K loop steps BK (32 or 64) with two LDS buffers and a
+// ring of S register stages: at step t the loads of tile t+S are issued, the
+// MFMAs of tile t run from LDS, then tile t+1 (loaded S-1 steps earlier) is
+// written to the other LDS buffer. S-1 steps of global-load latency are hidden
+// behind MFMA work, which matters because the heron grids give one block per
+// CU. One barrier per step (it waits for LDS traffic only).
+//
+// Each loader has a checked path (zero fill outside M / N / K, scalar
+// fallbacks for unaligned rows) and a fast path for full, aligned tiles with
+// straight-line vector loads. The fast path is chosen once per block, so the
+// loads it issues stay in flight across steps; per-element branches would make
+// the compiler wait for every load at the branch join.
 //
 // Operands reach LDS as fp16 in a [row][k] layout (k contiguous, rows padded
-// to 40 halves = 80 B so the ds_read_b128 fragment reads of 16 lanes hit 16
-// distinct bank quads). Loaders convert on the way in:
+// by 8 halves: 80 B rows for BK 32, 144 B for BK 64, so the ds_read_b128
+// fragment reads of 16 lanes hit 16 distinct bank quads). Loaders:
 //   LoadF16K   fp16 source, k contiguous            (activations [rows][k])
 //   LoadF32K   fp32 source, k contiguous, x scale   (fp32 gradients)
 //   LoadF16T   fp16 source, row contiguous          ([k][rows]: transposed)
 //   LoadF32T   fp32 source, row contiguous, x scale
 //   LoadBits   packed sign bits, LSB-first u32; each bit becomes +-1 (or
 //              +-scale[k] when a per-k scale vector is given) in fp16.
-// Out-of-range elements are zero, so any M, N, K works; the vector fast paths
-// need 16-byte aligned rows and are selected per launch by the host.
 //
 // The epilogue functor receives the accumulators with their tile origin.
 #pragma once
@@ -25,39 +32,51 @@
 
 namespace ullis {
 
-constexpr int kBK = 32;
-constexpr int kLDK = kBK + 8;  // padded LDS row, in halves
 constexpr int kThreads = 256;
+
+template <int BK>
+struct Lds {
+  static constexpr int ldk = BK + 8;  // padded LDS row, in halves
+};
+
+constexpr int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 // ------------------------------------------------------------------ loaders
 
 // Element (row, k) at p[row * ld + k].
-template <int ROWS>
+template <int ROWS, int BK>
 struct LoadF16K {
   const half_t* p;
   long ld;
   int vec_ok;  // ld % 8 == 0 and p 16-byte aligned
-  static constexpr int U = (ROWS * kBK / 8 + kThreads - 1) / kThreads;
+  static constexpr int CPR = BK / 8;
+  static constexpr int ITEMS = ROWS * CPR;
+  static constexpr int U = ceil_div(ITEMS, kThreads);
   struct Regs {
     half8 v[U];
   };
   __device__ void prepare() {}
+  __device__ bool fast(int row0, int rows) const { return vec_ok && row0 + ROWS <= rows; }
+  __device__ __forceinline__ void load_fast(Regs& r, int row0, int k0) const {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = threadIdx.x + u * kThreads;
+      if (ITEMS % kThreads == 0 || c < ITEMS)
+        r.v[u] = *reinterpret_cast<const half8*>(p + (long)(row0 + c / CPR) * ld + k0 + (c % CPR) * 8);
+    }
+  }
   __device__ __forceinline__ void load(Regs& r, int row0, int k0, int rows, int kend) const {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = threadIdx.x + u * kThreads;
       half8 v = {};
-      if (c < ROWS * kBK / 8) {
-        const int row = row0 + (c >> 2);
-        const int k = k0 + (c & 3) * 8;
+      if (c < ITEMS) {
+        const int row = row0 + c / CPR;
+        const int k = k0 + (c % CPR) * 8;
         if (row < rows) {
           const half_t* src = p + (long)row * ld + k;
-          if (vec_ok && k + 8 <= kend) {
-            v = *reinterpret_cast<const half8*>(src);
-          } else {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = (k + j < kend) ? src[j] : (half_t)0.0f;
-          }
+          for (int j = 0; j < 8; ++j) v[j] = (k + j < kend) ? src[j] : (half_t)0.0f;
         }
       }
       r.v[u] = v;
@@ -67,76 +86,108 @@ struct LoadF16K {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = threadIdx.x + u * kThreads;
-      if (c < ROWS * kBK / 8) *reinterpret_cast<half8*>(&s[(c >> 2) * kLDK + (c & 3) * 8]) = r.v[u];
+      if (ITEMS % kThreads == 0 || c < ITEMS)
+        *reinterpret_cast<half8*>(&s[(c / CPR) * Lds<BK>::ldk + (c % CPR) * 8]) = r.v[u];
     }
   }
 };
 
 // Element (row, k) = p[row * ld + k] * scale (fp32 source).
-template <int ROWS>
+template <int ROWS, int BK>
 struct LoadF32K {
   const float* p;
   long ld;
   int vec_ok;  // ld % 4 == 0 and p 16-byte aligned
   const float* amax;  // optional: scale = grad_scale_from_amax(*amax)
   float scale;
-  static constexpr int U = (ROWS * kBK / 8 + kThreads - 1) / kThreads;
+  static constexpr int CPR = BK / 8;
+  static constexpr int ITEMS = ROWS * CPR;
+  static constexpr int U = ceil_div(ITEMS, kThreads);
   struct Regs {
-    half8 v[U];
+    floatx4 a[U], b[U];
   };
   __device__ void prepare() {
     if (amax) scale = grad_scale_from_amax(*amax);
+  }
+  __device__ bool fast(int row0, int rows) const { return vec_ok && row0 + ROWS <= rows; }
+  __device__ __forceinline__ void load_fast(Regs& r, int row0, int k0) const {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = threadIdx.x + u * kThreads;
+      if (ITEMS % kThreads == 0 || c < ITEMS) {
+        const float* src = p + (long)(row0 + c / CPR) * ld + k0 + (c % CPR) * 8;
+        r.a[u] = *reinterpret_cast<const floatx4*>(src);
+        r.b[u] = *reinterpret_cast<const floatx4*>(src + 4);
+      }
+    }
   }
   __device__ __forceinline__ void load(Regs& r, int row0, int k0, int rows, int kend) const {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = threadIdx.x + u * kThreads;
-      half8 v = {};
-      if (c < ROWS * kBK / 8) {
-        const int row = row0 + (c >> 2);
-        const int k = k0 + (c & 3) * 8;
+      floatx4 a = {}, b = {};
+      if (c < ITEMS) {
+        const int row = row0 + c / CPR;
+        const int k = k0 + (c % CPR) * 8;
         if (row < rows) {
           const float* src = p + (long)row * ld + k;
-          if (vec_ok && k + 8 <= kend) {
-            const floatx4 a = *reinterpret_cast<const floatx4*>(src);
-            const floatx4 b = *reinterpret_cast<const floatx4*>(src + 4);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              v[j] = f32_to_f16_sat(a[j] * scale);
-              v[j + 4] = f32_to_f16_sat(b[j] * scale);
-            }
-          } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-              v[j] = (k + j < kend) ? f32_to_f16_sat(src[j] * scale) : (half_t)0.0f;
+          for (int j = 0; j < 4; ++j) {
+            a[j] = (k + j < kend) ? src[j] : 0.0f;
+            b[j] = (k + 4 + j < kend) ? src[4 + j] : 0.0f;
           }
         }
       }
-      r.v[u] = v;
+      r.a[u] = a;
+      r.b[u] = b;
     }
   }
   __device__ __forceinline__ void store(const Regs& r, half_t* s) const {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = threadIdx.x + u * kThreads;
-      if (c < ROWS * kBK / 8) *reinterpret_cast<half8*>(&s[(c >> 2) * kLDK + (c & 3) * 8]) = r.v[u];
+      if (ITEMS % kThreads == 0 || c < ITEMS) {
+        half8 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[j] = f32_to_f16_sat(r.a[u][j] * scale);
+          v[j + 4] = f32_to_f16_sat(r.b[u][j] * scale);
+        }
+        *reinterpret_cast<half8*>(&s[(c / CPR) * Lds<BK>::ldk + (c % CPR) * 8]) = v;
+      }
     }
   }
 };
 
 // Transposed fp16 source: element (row, k) at p[k * ld + row].
-// Work item = (k pair, 8 consecutive rows); written to LDS as 8 b32 pairs.
-template <int ROWS>
+// Work item = (k pair, 8 consecutive rows), written to LDS as 8 b32 pairs;
+// consecutive lanes take consecutive k pairs of one row block, so each LDS
+// write instruction of 32 lanes covers 128 contiguous bytes.
+template <int ROWS, int BK>
 struct LoadF16T {
   const half_t* p;
   long ld;
   int vec_ok;  // ld % 8 == 0 and p 16-byte aligned
-  static constexpr int ITEMS = (kBK / 2) * (ROWS / 8);
-  static constexpr int U = (ITEMS + kThreads - 1) / kThreads;
+  static constexpr int KP = BK / 2;
+  static constexpr int ITEMS = KP * (ROWS / 8);
+  static constexpr int U = ceil_div(ITEMS, kThreads);
   struct Regs {
-    uint32_t w[U][8];
+    u32x4 lo[U], hi[U];
   };
   __device__ void prepare() {}
+  __device__ bool fast(int row0, int rows) const { return vec_ok && row0 + ROWS <= rows; }
+  __device__ __forceinline__ void load_fast(Regs& r, int row0, int k0) const {
+    const uint16_t* q = reinterpret_cast<const uint16_t*>(p);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = threadIdx.x + u * kThreads;
+      if (ITEMS % kThreads == 0 || c < ITEMS) {
+        const uint16_t* src = q + (long)(k0 + 2 * (c % KP)) * ld + row0 + 8 * (c / KP);
+        r.lo[u] = *reinterpret_cast<const u32x4*>(src);
+        r.hi[u] = *reinterpret_cast<const u32x4*>(src + ld);
+      }
+    }
+  }
   __device__ __forceinline__ void load(Regs& r, int row0, int k0, int rows, int kend) const {
     const uint16_t* q = reinterpret_cast<const uint16_t*>(p);
 #pragma unroll
@@ -144,63 +195,72 @@ struct LoadF16T {
       const int c = threadIdx.x + u * kThreads;
       u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
       if (c < ITEMS) {
-        const int kp = c & 15;
-        const int rc = c >> 4;
-        const int k = k0 + 2 * kp;
-        const int row = row0 + 8 * rc;
-        if (vec_ok && row + 8 <= rows) {
-          if (k < kend) lo = *reinterpret_cast<const u32x4*>(q + (long)k * ld + row);
-          if (k + 1 < kend) hi = *reinterpret_cast<const u32x4*>(q + (long)(k + 1) * ld + row);
-        } else {
+        const int k = k0 + 2 * (c % KP);
+        const int row = row0 + 8 * (c / KP);
 #pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            if (row + j < rows) {
-              const uint32_t sh = (j & 1) * 16;
-              if (k < kend) lo[j >> 1] |= (uint32_t)q[(long)k * ld + row + j] << sh;
-              if (k + 1 < kend) hi[j >> 1] |= (uint32_t)q[(long)(k + 1) * ld + row + j] << sh;
-            }
+        for (int j = 0; j < 8; ++j) {
+          if (row + j < rows) {
+            const uint32_t sh = (j & 1) * 16;
+            if (k < kend) lo[j >> 1] |= (uint32_t)q[(long)k * ld + row + j] << sh;
+            if (k + 1 < kend) hi[j >> 1] |= (uint32_t)q[(long)(k + 1) * ld + row + j] << sh;
           }
         }
       }
-      // dword j = {row + j at k, row + j at k + 1}: low halves of lo/hi for
-      // even j, high halves for odd j (v_perm_b32 byte selects).
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        r.w[u][2 * m] = __builtin_amdgcn_perm(hi[m], lo[m], 0x05040100u);
-        r.w[u][2 * m + 1] = __builtin_amdgcn_perm(hi[m], lo[m], 0x07060302u);
-      }
+      r.lo[u] = lo;
+      r.hi[u] = hi;
     }
   }
   __device__ __forceinline__ void store(const Regs& r, half_t* s) const {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = threadIdx.x + u * kThreads;
-      if (c < ITEMS) {
-        const int kp = c & 15;
-        const int rc = c >> 4;
+      if (ITEMS % kThreads == 0 || c < ITEMS) {
+        const int kp = c % KP;
+        const int rc = c / KP;
+        // dword j = {row + j at k, row + j at k + 1}: low halves of lo/hi for
+        // even j, high halves for odd j (v_perm_b32 byte selects).
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          *reinterpret_cast<uint32_t*>(&s[(8 * rc + j) * kLDK + 2 * kp]) = r.w[u][j];
+        for (int m = 0; m < 4; ++m) {
+          *reinterpret_cast<uint32_t*>(&s[(8 * rc + 2 * m) * Lds<BK>::ldk + 2 * kp]) =
+              __builtin_amdgcn_perm(r.hi[u][m], r.lo[u][m], 0x05040100u);
+          *reinterpret_cast<uint32_t*>(&s[(8 * rc + 2 * m + 1) * Lds<BK>::ldk + 2 * kp]) =
+              __builtin_amdgcn_perm(r.hi[u][m], r.lo[u][m], 0x07060302u);
+        }
       }
     }
   }
 };
 
 // Transposed fp32 source with scale: element (row, k) = p[k * ld + row] * scale.
-template <int ROWS>
+template <int ROWS, int BK>
 struct LoadF32T {
   const float* p;
   long ld;
   int vec_ok;  // ld % 4 == 0 and p 16-byte aligned
   const float* amax;
   float scale;
-  static constexpr int ITEMS = (kBK / 2) * (ROWS / 8);
-  static constexpr int U = (ITEMS + kThreads - 1) / kThreads;
+  static constexpr int KP = BK / 2;
+  static constexpr int ITEMS = KP * (ROWS / 8);
+  static constexpr int U = ceil_div(ITEMS, kThreads);
   struct Regs {
-    uint32_t w[U][8];
+    floatx4 lo0[U], lo1[U], hi0[U], hi1[U];
   };
   __device__ void prepare() {
     if (amax) scale = grad_scale_from_amax(*amax);
+  }
+  __device__ bool fast(int row0, int rows) const { return vec_ok && row0 + ROWS <= rows; }
+  __device__ __forceinline__ void load_fast(Regs& r, int row0, int k0) const {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = threadIdx.x + u * kThreads;
+      if (ITEMS % kThreads == 0 || c < ITEMS) {
+        const float* src = p + (long)(k0 + 2 * (c % KP)) * ld + row0 + 8 * (c / KP);
+        r.lo0[u] = *reinterpret_cast<const floatx4*>(src);
+        r.lo1[u] = *reinterpret_cast<const floatx4*>(src + 4);
+        r.hi0[u] = *reinterpret_cast<const floatx4*>(src + ld);
+        r.hi1[u] = *reinterpret_cast<const floatx4*>(src + ld + 4);
+      }
+    }
   }
   __device__ __forceinline__ void load(Regs& r, int row0, int k0, int rows, int kend) const {
 #pragma unroll
@@ -213,45 +273,22 @@ struct LoadF32T {
         hi[j] = 0.0f;
       }
       if (c < ITEMS) {
-        const int kp = c & 15;
-        const int rc = c >> 4;
-        const int k = k0 + 2 * kp;
-        const int row = row0 + 8 * rc;
-        if (vec_ok && row + 8 <= rows) {
-          if (k < kend) {
-            const floatx4* s0 = reinterpret_cast<const floatx4*>(p + (long)k * ld + row);
-            const floatx4 a = s0[0], b = s0[1];
+        const int k = k0 + 2 * (c % KP);
+        const int row = row0 + 8 * (c / KP);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              lo[j] = a[j];
-              lo[j + 4] = b[j];
-            }
-          }
-          if (k + 1 < kend) {
-            const floatx4* s1 = reinterpret_cast<const floatx4*>(p + (long)(k + 1) * ld + row);
-            const floatx4 a = s1[0], b = s1[1];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              hi[j] = a[j];
-              hi[j + 4] = b[j];
-            }
-          }
-        } else {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            if (row + j < rows) {
-              if (k < kend) lo[j] = p[(long)k * ld + row + j];
-              if (k + 1 < kend) hi[j] = p[(long)(k + 1) * ld + row + j];
-            }
+        for (int j = 0; j < 8; ++j) {
+          if (row + j < rows) {
+            if (k < kend) lo[j] = p[(long)k * ld + row + j];
+            if (k + 1 < kend) hi[j] = p[(long)(k + 1) * ld + row + j];
           }
         }
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const half_t l = f32_to_f16_sat(lo[j] * scale);
-        const half_t h = f32_to_f16_sat(hi[j] * scale);
-        r.w[u][j] = (uint32_t)__builtin_bit_cast(uint16_t, l) |
-                    ((uint32_t)__builtin_bit_cast(uint16_t, h) << 16);
+      for (int j = 0; j < 4; ++j) {
+        r.lo0[u][j] = lo[j];
+        r.lo1[u][j] = lo[j + 4];
+        r.hi0[u][j] = hi[j];
+        r.hi1[u][j] = hi[j + 4];
       }
     }
   }
@@ -259,12 +296,17 @@ struct LoadF32T {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = threadIdx.x + u * kThreads;
-      if (c < ITEMS) {
-        const int kp = c & 15;
-        const int rc = c >> 4;
+      if (ITEMS % kThreads == 0 || c < ITEMS) {
+        const int kp = c % KP;
+        const int rc = c / KP;
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          *reinterpret_cast<uint32_t*>(&s[(8 * rc + j) * kLDK + 2 * kp]) = r.w[u][j];
+        for (int j = 0; j < 8; ++j) {
+          const float lo = j < 4 ? r.lo0[u][j & 3] : r.lo1[u][j & 3];
+          const float hi = j < 4 ? r.hi0[u][j & 3] : r.hi1[u][j & 3];
+          const uint32_t l = __builtin_bit_cast(uint16_t, f32_to_f16_sat(lo * scale));
+          const uint32_t h = __builtin_bit_cast(uint16_t, f32_to_f16_sat(hi * scale));
+          *reinterpret_cast<uint32_t*>(&s[(8 * rc + j) * Lds<BK>::ldk + 2 * kp]) = l | (h << 16);
+        }
       }
     }
   }
@@ -272,75 +314,104 @@ struct LoadF32T {
 
 // Packed sign bits: element (row, k) is bit (row * ldb + kofs + k) of the
 // LSB-first u32 array `bits` (src/model.rs:146-148), 1 => +1, 0 => -1.
-// With `kscale` (f16 bits, indexed kofs + k) the element is +-kscale[k].
-template <int ROWS>
+// With SCALED, `kscale` (f16 bits, indexed kofs + k) is applied: the element is
+// +-kscale[k] (a compile-time choice: a runtime null check would put a branch
+// join after the loads, where the compiler waits for them).
+// Work item = 8 consecutive k of one row: one byte of sign bits -> 8 halves.
+template <int ROWS, int BK, bool SCALED = false>
 struct LoadBits {
   const uint32_t* bits;
   long ldb;   // bits per row
   long kofs;  // bit offset of k = 0 within each row
-  const uint16_t* kscale;
-  int aligned;  // ldb % 8 == 0 and kofs % 8 == 0: each byte lies in one word
-  static constexpr int ITEMS = ROWS * kBK / 8;
-  static constexpr int U = (ITEMS + kThreads - 1) / kThreads;
+  const uint16_t* kscale;  // used iff SCALED
+  int aligned;  // ldb % 8 == 0, kofs % 8 == 0, kscale 16-byte aligned
+  static constexpr int BPR = BK / 8;
+  static constexpr int ITEMS = ROWS * BPR;
+  static constexpr int U = ceil_div(ITEMS, kThreads);
   struct Regs {
-    u32x4 v[U];
+    uint32_t word[U];  // raw sign word; the byte is extracted in store()
+    uint32_t sh[U];    // bit offset of the byte within word
+    u32x4 sc[U];
   };
   __device__ void prepare() {}
+  __device__ bool fast(int row0, int rows) const { return aligned && row0 + ROWS <= rows; }
+  __device__ __forceinline__ void load_fast(Regs& r, int row0, int k0) const {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = threadIdx.x + u * kThreads;
+      if (ITEMS % kThreads == 0 || c < ITEMS) {
+        const int k = k0 + (c % BPR) * 8;
+        const long g = (long)(row0 + c / BPR) * ldb + kofs + k;
+        r.word[u] = bits[g >> 5];
+        r.sh[u] = (uint32_t)(g & 31);
+        if constexpr (SCALED) r.sc[u] = *reinterpret_cast<const u32x4*>(kscale + kofs + k);
+      }
+    }
+  }
   __device__ __forceinline__ void load(Regs& r, int row0, int k0, int rows, int kend) const {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = threadIdx.x + u * kThreads;
-      uint32_t byte = 0, valid = 0;
-      const int row = row0 + (c >> 2);
-      const int k = k0 + (c & 3) * 8;
+      const int row = row0 + c / BPR;
+      const int k = k0 + (c % BPR) * 8;
+      uint32_t byte = 0;
+      u32x4 sc = {0u, 0u, 0u, 0u};
       if (c < ITEMS && row < rows && k < kend) {
         const int nv = kend - k < 8 ? kend - k : 8;
-        valid = nv >= 8 ? 0xffu : ((1u << nv) - 1u);
         const long g = (long)row * ldb + kofs + k;
-        const uint32_t w0 = bits[g >> 5];
         const uint32_t sh = (uint32_t)(g & 31);
-        byte = (w0 >> sh) & 0xffu;
+        byte = bits[g >> 5] >> sh;
         // The next word is read only when valid bits spill into it, so the
         // last word of the array is never overrun.
-        if (!aligned && sh + (uint32_t)nv > 32u) byte = (byte | (bits[(g >> 5) + 1] << (32u - sh))) & 0xffu;
-      }
-      u32x4 out;
-      if (kscale) {
-        uint16_t sc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (valid) {
+        if (sh + (uint32_t)nv > 32u) byte |= bits[(g >> 5) + 1] << (32u - sh);
+        // Out-of-range elements become zero: with a scale, a zero scale; without,
+        // the +-1 expansion is masked in store() through sc = 0x3C00 per valid half.
 #pragma unroll
-          for (int j = 0; j < 8; ++j)
-            if ((valid >> j) & 1u) sc[j] = kscale[kofs + k + j];
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t b0 = (byte >> (2 * j)) & 1u, b1 = (byte >> (2 * j + 1)) & 1u;
-          const uint32_t lo = (uint32_t)sc[2 * j] ^ ((b0 ^ 1u) << 15);
-          const uint32_t hi = (uint32_t)sc[2 * j + 1] ^ ((b1 ^ 1u) << 15);
-          out[j] = (((valid >> (2 * j)) & 1u) ? lo : 0u) |
-                   ((((valid >> (2 * j + 1)) & 1u) ? hi : 0u) << 16);
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t b0 = (byte >> (2 * j)) & 1u, b1 = (byte >> (2 * j + 1)) & 1u;
-          const uint32_t lo = 0xBC00u ^ (b0 << 15);  // 0x3C00 = +1.0, 0xBC00 = -1.0
-          const uint32_t hi = 0xBC00u ^ (b1 << 15);
-          out[j] = (((valid >> (2 * j)) & 1u) ? lo : 0u) |
-                   ((((valid >> (2 * j + 1)) & 1u) ? hi : 0u) << 16);
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t base = (j < nv) ? (SCALED ? (uint32_t)kscale[kofs + k + j] : 0x3C00u) : 0u;
+          sc[j >> 1] |= base << ((j & 1) * 16);
         }
       }
-      r.v[u] = out;
+      r.word[u] = byte;
+      r.sh[u] = 0;
+      r.sc[u] = sc;
     }
   }
-  __device__ __forceinline__ void store(const Regs& r, half_t* s) const {
+  // Expansion: sign bit 15 of each half is set for a 0 bit (-1 / -scale).
+  template <bool FAST>
+  __device__ __forceinline__ void store_t(const Regs& r, half_t* s) const {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = threadIdx.x + u * kThreads;
-      if (c < ITEMS) *reinterpret_cast<u32x4*>(&s[(c >> 2) * kLDK + (c & 3) * 8]) = r.v[u];
+      if (ITEMS % kThreads == 0 || c < ITEMS) {
+        const uint32_t byte = r.word[u] >> r.sh[u];
+        u32x4 out;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t neg = ((~byte >> (2 * j)) & 1u) << 15 | ((~byte >> (2 * j + 1)) & 1u) << 31;
+          // Masked elements have a zero base; flipping its sign leaves a zero.
+          const uint32_t base = (FAST && !SCALED) ? 0x3C003C00u : r.sc[u][j];
+          out[j] = base ^ neg;
+        }
+        *reinterpret_cast<u32x4*>(&s[(c / BPR) * Lds<BK>::ldk + (c % BPR) * 8]) = out;
+      }
     }
   }
+  __device__ __forceinline__ void store(const Regs& r, half_t* s) const { store_t<false>(r, s); }
+  __device__ __forceinline__ void store_fast(const Regs& r, half_t* s) const { store_t<true>(r, s); }
 };
+
+// Loaders other than LoadBits store the same way on both paths.
+template <class L>
+__device__ __forceinline__ auto store_fast_of(const L& l, const typename L::Regs& r, half_t* s,
+                                              int) -> decltype(l.store_fast(r, s)) {
+  return l.store_fast(r, s);
+}
+template <class L>
+__device__ __forceinline__ void store_fast_of(const L& l, const typename L::Regs& r, half_t* s,
+                                              long) {
+  l.store(r, s);
+}
 
 // ------------------------------------------------------------------ kernel
 
@@ -355,14 +426,111 @@ __device__ __forceinline__ void tile_of_block(int bid, int tiles_m, int tiles_n,
   tn = t % tiles_n;
 }
 
-template <int BM, int BN, class LA, class LB, class Epi>
+template <bool FAST, int BM, int BN, int BK, int S, class LA, class LB, int TM, int TN>
+__device__ __forceinline__ void gemm_mainloop(const LA& la, const LB& lb, floatx16 (&acc)[TM][TN],
+                                              half_t (*sA)[BM * Lds<BK>::ldk],
+                                              half_t (*sB)[BN * Lds<BK>::ldk], int m0, int n0,
+                                              int kbeg, int kend, int M, int N) {
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int LDK = Lds<BK>::ldk;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+  typename LA::Regs ra[S];
+  typename LB::Regs rb[S];
+  auto load = [&](typename LA::Regs& a, typename LB::Regs& b, int k0) {
+    if constexpr (FAST) {
+      la.load_fast(a, m0, k0);
+      lb.load_fast(b, n0, k0);
+    } else {
+      la.load(a, m0, k0, M, kend);
+      lb.load(b, n0, k0, N, kend);
+    }
+  };
+  auto store = [&](const typename LA::Regs& a, const typename LB::Regs& b, int buf) {
+    if constexpr (FAST) {
+      store_fast_of(la, a, sA[buf], 0);
+      store_fast_of(lb, b, sB[buf], 0);
+    } else {
+      la.store(a, sA[buf]);
+      lb.store(b, sB[buf]);
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+    if (s < nk) load(ra[s], rb[s], kbeg + s * BK);
+  if (nk > 0) store(ra[0], rb[0], 0);
+  __syncthreads();
+
+  const int frag_row = lane & 31;
+  const int frag_k = (lane >> 5) * 8;
+  auto compute = [&](int cur) {
+    const half_t* a_t = sA[cur];
+    const half_t* b_t = sB[cur];
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      half8 af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        af[i] = *reinterpret_cast<const half8*>(
+            &a_t[(wm * WM + i * 32 + frag_row) * LDK + ks * 16 + frag_k]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        bf[j] = *reinterpret_cast<const half8*>(
+            &b_t[(wn * WN + j * 32 + frag_row) * LDK + ks * 16 + frag_k]);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  int kt = 0;
+  // Steady state: every step issues its loads and stores unconditionally, so
+  // the waits before the LDS stores only cover loads issued S-1 steps earlier.
+  for (; kt + 2 * S <= nk; kt += S) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int t = kt + s;
+      const int cur = t & 1;
+      load(ra[s], rb[s], kbeg + (t + S) * BK);
+      compute(cur);
+      const int nxt = (s + 1) % S;  // constant once the s loop is unrolled
+      store(ra[nxt], rb[nxt], cur ^ 1);
+      __syncthreads();
+    }
+  }
+  // Tail: the last (fewer than 2 S) tiles, with bounds on every action.
+  for (; kt < nk; kt += S) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int t = kt + s;  // tile computed now; register slot s held it
+      if (t < nk) {
+        const int cur = t & 1;
+        if (t + S < nk) load(ra[s], rb[s], kbeg + (t + S) * BK);
+        compute(cur);
+        if (t + 1 < nk) {
+          const int nxt = (s + 1) % S;
+          store(ra[nxt], rb[nxt], cur ^ 1);
+        }
+        __syncthreads();
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int BK, int S, class LA, class LB, class Epi>
 __global__ __launch_bounds__(256) void gemm_kernel(LA la, LB lb, Epi epi, int M, int N, int K,
                                                    int k_split) {
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int LDK = Lds<BK>::ldk;
   static_assert(TM >= 1 && TN >= 1, "tile too small");
-  __shared__ __attribute__((aligned(16))) half_t sA[2][BM * kLDK];
-  __shared__ __attribute__((aligned(16))) half_t sB[2][BN * kLDK];
+  static_assert(S >= 1, "at least one register stage");
+  __shared__ __attribute__((aligned(16))) half_t sA[2][BM * LDK];
+  __shared__ __attribute__((aligned(16))) half_t sB[2][BN * LDK];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -383,49 +551,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(LA la, LB lb, Epi epi, int M,
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = (floatx16){};
 
-  const int nk = kend > kbeg ? (kend - kbeg + kBK - 1) / kBK : 0;
-  typename LA::Regs ra;
-  typename LB::Regs rb;
-  if (nk > 0) {
-    la.load(ra, m0, kbeg, M, kend);
-    lb.load(rb, n0, kbeg, N, kend);
-    la.store(ra, sA[0]);
-    lb.store(rb, sB[0]);
-  }
-  __syncthreads();
-
-  const int frag_row = lane & 31;
-  const int frag_k = (lane >> 5) * 8;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < nk;
-    if (more) {
-      la.load(ra, m0, kbeg + (kt + 1) * kBK, M, kend);
-      lb.load(rb, n0, kbeg + (kt + 1) * kBK, N, kend);
-    }
-#pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      half8 af[TM], bf[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-        af[i] = *reinterpret_cast<const half8*>(
-            &sA[cur][(wm * WM + i * 32 + frag_row) * kLDK + ks * 16 + frag_k]);
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        bf[j] = *reinterpret_cast<const half8*>(
-            &sB[cur][(wn * WN + j * 32 + frag_row) * kLDK + ks * 16 + frag_k]);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-    if (more) {
-      la.store(ra, sA[cur ^ 1]);
-      lb.store(rb, sB[cur ^ 1]);
-    }
-    __syncthreads();
-  }
+  const bool fast = la.fast(m0, M) && lb.fast(n0, N) && (kend - kbeg) % BK == 0;
+  if (fast)
+    gemm_mainloop<true, BM, BN, BK, S>(la, lb, acc, sA, sB, m0, n0, kbeg, kend, M, N);
+  else
+    gemm_mainloop<false, BM, BN, BK, S>(la, lb, acc, sA, sB, m0, n0, kbeg, kend, M, N);
 
   epi.template run<TM, TN>(acc, m0 + wm * WM, n0 + wn * WN, lane, M, N);
 }
@@ -456,6 +586,16 @@ struct EpiPartial {
     for_each_acc(acc, row0, col0, lane, M, N,
                  [&](int row, int col, float v) { dst[(long)row * N + col] = v; });
   }
+};
+
+// Tile configurations: 128x128 tiles (BK 32, 2 register stages: 16 MFMAs per
+// wave per step already cover a load, and a third stage spills) when they
+// alone give about one block per CU, else 64x64 tiles (BK 64, 3 stages).
+struct CfgLarge {
+  static constexpr int bm = 128, bn = 128, bk = 32, stages = 2;
+};
+struct CfgSmall {
+  static constexpr int bm = 64, bn = 64, bk = 64, stages = 3;
 };
 
 }  // namespace ullis

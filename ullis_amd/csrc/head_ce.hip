@@ -186,24 +186,6 @@ __global__ __launch_bounds__(1024) void ce_mean_kernel(const float* row_loss, lo
   }
 }
 
-// g_bias[v] = gscale * sum_b part[b][v]; optional bias step at lr_bias;
-// optional scale step at lr with g_scale.
-__global__ void head_vector_finish_kernel(const float* part, int nb, long vocab,
-                                          const float* stats, float* g_bias, float lr,
-                                          uint16_t* bias, float* bias_res, const float* g_scale,
-                                          uint16_t* scale, float* scale_res) {
-  const long v = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (v >= vocab) return;
-  float s = 0.0f;
-  for (int b = 0; b < nb; ++b) s += part[(long)b * vocab + v];
-  s *= stats[2];
-  if (g_bias) g_bias[v] = s;
-  if (lr > 0.0f) {
-    if (scale) clipped_sgd_one(scale[v], scale_res[v], g_scale[v], lr);
-    if (bias) clipped_sgd_one(bias[v], bias_res[v], s, lr * kHeadBiasLrMult);
-  }
-}
-
 long chunk_cols(long vocab, long d) {
   // Enough weight-gradient tiles (Vc x d, 64x64) to fill the GPU, multiple of 32.
   long vc = 2048;
@@ -245,20 +227,20 @@ hipError_t logits_gemm(hipStream_t s, const uint16_t* hidden16, long rows, long 
                        const uint32_t* bits_rows, long ncols, const Epi& epi) {
   // C[rows][ncols] = hidden . S^T ; S rows start at bits_rows (word aligned).
   const bool vec = (reinterpret_cast<uintptr_t>(hidden16) & 15u) == 0 && d % 8 == 0;
-  if (cdiv(rows, 128) * cdiv(ncols, 128) >= 240) {
-    LoadF16K<128> la{reinterpret_cast<const half_t*>(hidden16), d, vec};
-    LoadBits<128> lb{bits_rows, d, 0, nullptr, d % 8 == 0};
-    hipLaunchKernelGGL((gemm_kernel<128, 128, LoadF16K<128>, LoadBits<128>, Epi>),
-                       dim3((unsigned)(cdiv(rows, 128) * cdiv(ncols, 128))), dim3(kThreads), 0, s,
-                       la, lb, epi, (int)rows, (int)ncols, (int)d, (int)(cdiv(d, kBK) * kBK));
-  } else {
-    LoadF16K<64> la{reinterpret_cast<const half_t*>(hidden16), d, vec};
-    LoadBits<64> lb{bits_rows, d, 0, nullptr, d % 8 == 0};
-    hipLaunchKernelGGL((gemm_kernel<64, 64, LoadF16K<64>, LoadBits<64>, Epi>),
-                       dim3((unsigned)(cdiv(rows, 64) * cdiv(ncols, 64))), dim3(kThreads), 0, s,
-                       la, lb, epi, (int)rows, (int)ncols, (int)d, (int)(cdiv(d, kBK) * kBK));
-  }
-  return hipGetLastError();
+  auto run = [&](auto cfg) {
+    using T = decltype(cfg);
+    using LA = LoadF16K<T::bm, T::bk>;
+    using LB = LoadBits<T::bn, T::bk>;
+    LA la{reinterpret_cast<const half_t*>(hidden16), d, vec};
+    LB lb{bits_rows, d, 0, nullptr, d % 8 == 0};
+    hipLaunchKernelGGL((gemm_kernel<T::bm, T::bn, T::bk, T::stages, LA, LB, Epi>),
+                       dim3((unsigned)(cdiv(rows, T::bm) * cdiv(ncols, T::bn))), dim3(kThreads),
+                       0, s, la, lb, epi, (int)rows, (int)ncols, (int)d,
+                       (int)(cdiv(d, T::bk) * T::bk));
+    return hipGetLastError();
+  };
+  if (cdiv(rows, 128) * cdiv(ncols, 128) >= 240) return run(CfgLarge{});
+  return run(CfgSmall{});
 }
 
 }  // namespace
@@ -328,11 +310,15 @@ hipError_t head_ce(hipStream_t s, const HeadCe& h, void* workspace) {
 
   // 4. bias gradient, vector steps, repack
   const bool upd = h.lr > 0.0f;
-  hipLaunchKernelGGL(head_vector_finish_kernel, dim3((unsigned)cdiv(V, 256)), dim3(256), 0, s,
-                     w.part_bias, (int)cdiv(rows, 32), V, h.stats, h.g_bias ? h.g_bias : w.g_bias,
-                     upd ? h.lr : 0.0f, upd ? h.bias_upd : nullptr, h.bias_res, g_scale,
-                     upd ? h.scale_upd : nullptr, h.scale_res);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
+  // g_bias = gscale * sum over row tiles; head bias step at 8 lr (src/model.rs:3118-3130)
+  VecTarget bias_t{h.g_bias ? h.g_bias : w.g_bias, upd ? h.bias_upd : nullptr, h.bias_res,
+                   h.lr * kHeadBiasLrMult, gscale};
+  if ((e = partial_reduce(s, w.part_bias, (int)cdiv(rows, 32), V, V, bias_t, bias_t)) !=
+      hipSuccess)
+    return e;
+  if (upd && h.scale_upd) {
+    if ((e = clipped_sgd(s, h.scale_upd, h.scale_res, g_scale, V, h.lr)) != hipSuccess) return e;
+  }
   if (upd && h.bits_new) return pack_latent_bits(s, h.latent, V, d, h.bits_new, h.bits_t_new);
   return hipSuccess;
 }

@@ -211,7 +211,7 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
   if ((long)h->splits_key * F * D > gpart) gpart = (long)h->splits_key * F * D;
   if ((long)h->splits_value * D * F > gpart) gpart = (long)h->splits_value * D * F;
   long part = 2L * layer_norm_backward_blocks(R) * D;
-  if (cdiv(R, 64) * D > part) part = cdiv(R, 64) * D;
+  if (column_partial_blocks(R) * D > part) part = column_partial_blocks(R) * D;
   const long vec = F > V ? F : (V > D ? V : D);
   const size_t head_ws = head_ce_workspace_bytes(R, D, V);
 

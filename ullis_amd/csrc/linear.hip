@@ -10,6 +10,8 @@
 //   FP16 linear  y = x W^T, gx = gy W, gW = gy^T x, clipped SGD          src/model.rs:419-470
 // The Metal kernels these replace are ullis_binary_linear*, ullis_fp16_linear*
 // (src/metal/rwkv8.metal:370-841).
+#include <type_traits>
+
 #include "gemm.hpp"
 #include "ops.hpp"
 
@@ -21,28 +23,28 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 inline int vec_ok_f16(const void* p, long ld) { return aligned16(p) && ld % 8 == 0; }
 inline int vec_ok_f32(const void* p, long ld) { return aligned16(p) && ld % 4 == 0; }
 
-template <int BM_, int BN_>
-struct Tile {
-  static constexpr int bm = BM_, bn = BN_;
-};
+inline int bits_aligned(long ldb, long kofs, const void* kscale) {
+  return ldb % 8 == 0 && kofs % 8 == 0 && (!kscale || aligned16(kscale));
+}
 
 // 128x128 tiles when they alone give ~one block per CU, else 64x64.
 template <class F>
 hipError_t with_tile(long M, long N, F&& f) {
-  if (cdiv(M, 128) * cdiv(N, 128) >= 240) return f(Tile<128, 128>{});
-  return f(Tile<64, 64>{});
+  if (cdiv(M, 128) * cdiv(N, 128) >= 240) return f(CfgLarge{});
+  return f(CfgSmall{});
 }
 
-template <int BM, int BN, class LA, class LB, class Epi>
+template <class T, class LA, class LB, class Epi>
 hipError_t launch_gemm(hipStream_t s, const LA& la, const LB& lb, const Epi& epi, long M, long N,
                        long K, int splits) {
   if (M <= 0 || N <= 0) return hipSuccess;
   if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return hipErrorInvalidValue;
   if (splits < 1) splits = 1;
-  const long tiles = cdiv(M, BM) * cdiv(N, BN);
-  const int ks = (int)(cdiv(cdiv(K, splits), kBK) * kBK);
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, LA, LB, Epi>), dim3((unsigned)tiles, 1, splits),
-                     dim3(kThreads), 0, s, la, lb, epi, (int)M, (int)N, (int)K, ks > 0 ? ks : kBK);
+  const long tiles = cdiv(M, T::bm) * cdiv(N, T::bn);
+  const int ks = (int)(cdiv(cdiv(K, splits), T::bk) * T::bk);
+  hipLaunchKernelGGL((gemm_kernel<T::bm, T::bn, T::bk, T::stages, LA, LB, Epi>),
+                     dim3((unsigned)tiles, 1, splits), dim3(kThreads), 0, s, la, lb, epi, (int)M,
+                     (int)N, (int)K, ks > 0 ? ks : T::bk);
   return hipGetLastError();
 }
 
@@ -52,6 +54,12 @@ __device__ __forceinline__ float unscale_of(const float* amax) {
 
 // ---------------------------------------------------------------- epilogues
 
+// Output set of a packed forward, fixed at compile time so each instantiation
+// carries only the stores it makes (a generic epilogue keeps every path live
+// and spills at 128x128 tiles).
+enum : int { kOutY32 = 1, kOutResid = 2, kOutY16 = 4, kOutRelu2 = 8, kOutBits = 16 };
+
+template <int OUT>
 struct EpiPackedFwd {
   const uint16_t* scale;
   const uint16_t* bias;
@@ -73,14 +81,19 @@ struct EpiPackedFwd {
           const float y = bi + sc * acc[i][j][r];
           const long idx = (long)row * N + col;
           if (ok) {
-            if (o.y32) o.y32[idx] = o.resid ? o.resid[idx] + y : y;
-            if (o.y16) o.y16[idx] = __builtin_bit_cast(uint16_t, (half_t)y);
-            if (o.relu2_16) {
+            if constexpr ((OUT & kOutY32) != 0) {
+              if constexpr ((OUT & kOutResid) != 0)
+                o.y32[idx] = o.resid[idx] + y;
+              else
+                o.y32[idx] = y;
+            }
+            if constexpr ((OUT & kOutY16) != 0) o.y16[idx] = __builtin_bit_cast(uint16_t, (half_t)y);
+            if constexpr ((OUT & kOutRelu2) != 0) {
               const float k = y > 0.0f ? y : 0.0f;
               o.relu2_16[idx] = __builtin_bit_cast(uint16_t, (half_t)(k * k));
             }
           }
-          if (o.sign_bits) {
+          if constexpr ((OUT & kOutBits) != 0) {
             const unsigned long long m = __ballot(ok && y > 0.0f);
             if ((lane & 31) == 0 && row < M && col0 + j * 32 < N) {
               const long word = ((long)row * N + col0 + j * 32) >> 5;
@@ -240,17 +253,33 @@ hipError_t packed_forward(hipStream_t s, const void* x, int x_dtype, long rows, 
                           const uint32_t* bits, const uint16_t* scale, const uint16_t* bias,
                           const PackedFwdOut& o) {
   if (o.sign_bits && out % 32 != 0) return hipErrorInvalidValue;
-  EpiPackedFwd epi{scale, bias, o};
-  return with_tile(rows, out, [&](auto t) {
-    using T = decltype(t);
-    LoadBits<T::bn> lb{bits, in, 0, nullptr, in % 8 == 0};
-    if (x_dtype == kF16) {
-      LoadF16K<T::bm> la{static_cast<const half_t*>(x), in, vec_ok_f16(x, in)};
-      return launch_gemm<T::bm, T::bn>(s, la, lb, epi, rows, out, in, 1);
-    }
-    LoadF32K<T::bm> la{static_cast<const float*>(x), in, vec_ok_f32(x, in), nullptr, 1.0f};
-    return launch_gemm<T::bm, T::bn>(s, la, lb, epi, rows, out, in, 1);
-  });
+  const int mask = (o.y32 ? kOutY32 : 0) | (o.y32 && o.resid ? kOutResid : 0) |
+                   (o.y16 ? kOutY16 : 0) | (o.relu2_16 ? kOutRelu2 : 0) |
+                   (o.sign_bits ? kOutBits : 0);
+  auto run = [&](auto out_tag) {
+    constexpr int OUT = decltype(out_tag)::value;
+    EpiPackedFwd<OUT> epi{scale, bias, o};
+    return with_tile(rows, out, [&](auto t) {
+      using T = decltype(t);
+      LoadBits<T::bn, T::bk> lb{bits, in, 0, nullptr, bits_aligned(in, 0, nullptr)};
+      if (x_dtype == kF16) {
+        LoadF16K<T::bm, T::bk> la{static_cast<const half_t*>(x), in, vec_ok_f16(x, in)};
+        return launch_gemm<T>(s, la, lb, epi, rows, out, in, 1);
+      }
+      LoadF32K<T::bm, T::bk> la{static_cast<const float*>(x), in, vec_ok_f32(x, in), nullptr,
+                                1.0f};
+      return launch_gemm<T>(s, la, lb, epi, rows, out, in, 1);
+    });
+  };
+  switch (mask) {
+    case kOutY32: return run(std::integral_constant<int, kOutY32>{});
+    case kOutY16: return run(std::integral_constant<int, kOutY16>{});
+    case kOutY32 | kOutY16: return run(std::integral_constant<int, kOutY32 | kOutY16>{});
+    case kOutY32 | kOutResid: return run(std::integral_constant<int, kOutY32 | kOutResid>{});
+    case kOutY16 | kOutRelu2: return run(std::integral_constant<int, kOutY16 | kOutRelu2>{});
+    case kOutBits: return run(std::integral_constant<int, kOutBits>{});
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t packed_backward_input(hipStream_t s, GradIn gy32, const uint16_t* gy16, long rows,
@@ -259,13 +288,13 @@ hipError_t packed_backward_input(hipStream_t s, GradIn gy32, const uint16_t* gy1
   EpiStoreF32 epi{gx, gy32.amax, out_mul, accumulate};
   return with_tile(rows, in, [&](auto t) {
     using T = decltype(t);
-    LoadBits<T::bn> lb{bits_t, out, 0, scale, out % 8 == 0};
+    LoadBits<T::bn, T::bk, true> lb{bits_t, out, 0, scale, bits_aligned(out, 0, scale)};
     if (gy16) {
-      LoadF16K<T::bm> la{reinterpret_cast<const half_t*>(gy16), out, vec_ok_f16(gy16, out)};
-      return launch_gemm<T::bm, T::bn>(s, la, lb, epi, rows, in, out, 1);
+      LoadF16K<T::bm, T::bk> la{reinterpret_cast<const half_t*>(gy16), out, vec_ok_f16(gy16, out)};
+      return launch_gemm<T>(s, la, lb, epi, rows, in, out, 1);
     }
-    LoadF32K<T::bm> la{gy32.p, out, vec_ok_f32(gy32.p, out), gy32.amax, 1.0f};
-    return launch_gemm<T::bm, T::bn>(s, la, lb, epi, rows, in, out, 1);
+    LoadF32K<T::bm, T::bk> la{gy32.p, out, vec_ok_f32(gy32.p, out), gy32.amax, 1.0f};
+    return launch_gemm<T>(s, la, lb, epi, rows, in, out, 1);
   });
 }
 
@@ -279,9 +308,9 @@ hipError_t packed_backward_input_ex(hipStream_t s, const uint16_t* gy16, long ld
   EpiStoreF32 epi{gx, nullptr, out_mul, accumulate};
   return with_tile(rows, in, [&](auto t) {
     using T = decltype(t);
-    LoadBits<T::bn> lb{bits_t, ldb, kofs, scale, ldb % 8 == 0 && kofs % 8 == 0};
-    LoadF16K<T::bm> la{reinterpret_cast<const half_t*>(gy16), ldgy, vec_ok_f16(gy16, ldgy)};
-    return launch_gemm<T::bm, T::bn>(s, la, lb, epi, rows, in, k_len, 1);
+    LoadBits<T::bn, T::bk, true> lb{bits_t, ldb, kofs, scale, bits_aligned(ldb, kofs, scale)};
+    LoadF16K<T::bm, T::bk> la{reinterpret_cast<const half_t*>(gy16), ldgy, vec_ok_f16(gy16, ldgy)};
+    return launch_gemm<T>(s, la, lb, epi, rows, in, k_len, 1);
   });
 }
 
@@ -292,13 +321,13 @@ hipError_t packed_weight_grad_partials(hipStream_t s, GradIn gy32, const uint16_
   // G[out][in]: M = out, N = in, K = rows; both operands are row-contiguous.
   return with_tile(out, in, [&](auto t) {
     using T = decltype(t);
-    LoadF16T<T::bn> lb{reinterpret_cast<const half_t*>(x16), in, vec_ok_f16(x16, in)};
+    LoadF16T<T::bn, T::bk> lb{reinterpret_cast<const half_t*>(x16), in, vec_ok_f16(x16, in)};
     if (gy16) {
-      LoadF16T<T::bm> la{reinterpret_cast<const half_t*>(gy16), out, vec_ok_f16(gy16, out)};
-      return launch_gemm<T::bm, T::bn>(s, la, lb, epi, out, in, rows, splits);
+      LoadF16T<T::bm, T::bk> la{reinterpret_cast<const half_t*>(gy16), out, vec_ok_f16(gy16, out)};
+      return launch_gemm<T>(s, la, lb, epi, out, in, rows, splits);
     }
-    LoadF32T<T::bm> la{gy32.p, out, vec_ok_f32(gy32.p, out), gy32.amax, 1.0f};
-    return launch_gemm<T::bm, T::bn>(s, la, lb, epi, out, in, rows, splits);
+    LoadF32T<T::bm, T::bk> la{gy32.p, out, vec_ok_f32(gy32.p, out), gy32.amax, 1.0f};
+    return launch_gemm<T>(s, la, lb, epi, out, in, rows, splits);
   });
 }
 
@@ -343,13 +372,13 @@ hipError_t fp16_forward(hipStream_t s, const void* x, int x_dtype, long rows, lo
   EpiF16Fwd epi{y32, resid, y16};
   return with_tile(rows, out, [&](auto t) {
     using T = decltype(t);
-    LoadF16K<T::bn> lb{reinterpret_cast<const half_t*>(w), in, vec_ok_f16(w, in)};
+    LoadF16K<T::bn, T::bk> lb{reinterpret_cast<const half_t*>(w), in, vec_ok_f16(w, in)};
     if (x_dtype == kF16) {
-      LoadF16K<T::bm> la{static_cast<const half_t*>(x), in, vec_ok_f16(x, in)};
-      return launch_gemm<T::bm, T::bn>(s, la, lb, epi, rows, out, in, 1);
+      LoadF16K<T::bm, T::bk> la{static_cast<const half_t*>(x), in, vec_ok_f16(x, in)};
+      return launch_gemm<T>(s, la, lb, epi, rows, out, in, 1);
     }
-    LoadF32K<T::bm> la{static_cast<const float*>(x), in, vec_ok_f32(x, in), nullptr, 1.0f};
-    return launch_gemm<T::bm, T::bn>(s, la, lb, epi, rows, out, in, 1);
+    LoadF32K<T::bm, T::bk> la{static_cast<const float*>(x), in, vec_ok_f32(x, in), nullptr, 1.0f};
+    return launch_gemm<T>(s, la, lb, epi, rows, out, in, 1);
   });
 }
 
@@ -359,14 +388,14 @@ hipError_t fp16_backward_input(hipStream_t s, GradIn gy32, long rows, long in, l
   // gX[rows][in] = gY[rows][out] . W[out][in]: B(n = i, k = o) = W[o*in + i].
   return with_tile(rows, in, [&](auto t) {
     using T = decltype(t);
-    LoadF32K<T::bm> la{gy32.p, out, vec_ok_f32(gy32.p, out), gy32.amax, 1.0f};
-    LoadF16T<T::bn> lb{reinterpret_cast<const half_t*>(w), in, vec_ok_f16(w, in)};
+    LoadF32K<T::bm, T::bk> la{gy32.p, out, vec_ok_f32(gy32.p, out), gy32.amax, 1.0f};
+    LoadF16T<T::bn, T::bk> lb{reinterpret_cast<const half_t*>(w), in, vec_ok_f16(w, in)};
     if (gk16) {
       EpiRelu2Bwd epi{key16, gk16};
-      return launch_gemm<T::bm, T::bn>(s, la, lb, epi, rows, in, out, 1);
+      return launch_gemm<T>(s, la, lb, epi, rows, in, out, 1);
     }
     EpiStoreF32 epi{gx, gy32.amax, nullptr, 0};
-    return launch_gemm<T::bm, T::bn>(s, la, lb, epi, rows, in, out, 1);
+    return launch_gemm<T>(s, la, lb, epi, rows, in, out, 1);
   });
 }
 

@@ -266,25 +266,6 @@ __global__ __launch_bounds__(64) void ln_bwd_any_kernel(const float* x, const fl
   }
 }
 
-__global__ void ln_param_finish_kernel(const float* part, int nblk, long ch, float* gw, float* gb,
-                                       float lr, uint16_t* w, float* w_res, uint16_t* b,
-                                       float* b_res) {
-  const long c = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= ch) return;
-  float a = 0.0f, s = 0.0f;
-  for (int k = 0; k < nblk; ++k) {
-    a += part[((long)k * 2 + 0) * ch + c];
-    s += part[((long)k * 2 + 1) * ch + c];
-  }
-  if (gw) gw[c] = a;
-  if (gb) gb[c] = s;
-  if (lr > 0.0f && w) {
-    // LayerNorm::apply_clipped_sgd, src/model.rs:318-332
-    clipped_sgd_one(w[c], w_res[c], a, lr);
-    clipped_sgd_one(b[c], b_res[c], s, lr);
-  }
-}
-
 template <class F>
 hipError_t by_nv(long ch, F&& f) {
   const long nv = cdiv(ch, 256);
@@ -351,9 +332,11 @@ hipError_t layer_norm_param_finish(hipStream_t s, const float* part, int nblk, l
                                    float* gb, float lr, uint16_t* w, float* w_res, uint16_t* b,
                                    float* b_res) {
   if (ch <= 0) return hipSuccess;
-  hipLaunchKernelGGL(ln_param_finish_kernel, dim3((unsigned)cdiv(ch, 256)), dim3(256), 0, s, part,
-                     nblk, ch, gw, gb, lr, w, w_res, b, b_res);
-  return hipGetLastError();
+  // part is [nblk][2][ch]: columns [0, ch) are gamma sums, [ch, 2 ch) beta sums.
+  // LayerNorm::apply_clipped_sgd, src/model.rs:318-332.
+  VecTarget a{gw, lr > 0.0f ? w : nullptr, w_res, lr, nullptr};
+  VecTarget bt{gb, lr > 0.0f ? b : nullptr, b_res, lr, nullptr};
+  return partial_reduce(s, part, nblk, 2 * ch, ch, a, bt);
 }
 
 }  // namespace ullis

@@ -138,6 +138,9 @@ hipError_t time_shift_mix_backward(hipStream_t s, const float* g_shifted, const 
                                    const uint16_t* mix, long rows, long time, long ch, float* g_x,
                                    float* part, int* nblk_out);
 
+// Number of row chunks (partials) used by the column reductions below.
+inline long column_partial_blocks(long rows) { return cdiv(rows, 16); }
+
 // Column sums of v[rows][ch] (times +-1 from idx when idx != null, i.e.
 // sum g_y * (2*idx - 1)) into part[nblk][ch].
 hipError_t column_sum_partials(hipStream_t s, const float* v, const uint8_t* idx, long rows,
@@ -145,6 +148,20 @@ hipError_t column_sum_partials(hipStream_t s, const float* v, const uint8_t* idx
 // Sums part[nblk][ch] -> out (optional) and optional clipped SGD with lr.
 hipError_t vector_finish(hipStream_t s, const float* part, int nblk, long ch, float* out,
                          float lr, uint16_t* values, float* residual);
+
+// Destination of a reduced vector: optional fp32 copy and optional clipped
+// SGD of an f16 tensor with its carry; the sum is first multiplied by *mul.
+struct VecTarget {
+  float* out;
+  uint16_t* values;
+  float* residual;
+  float lr;
+  const float* mul;
+};
+// Fixed-order sum of part[nblk][ncols] over nblk; columns [0, split) go to a,
+// [split, ncols) to b (index relative to split).
+hipError_t partial_reduce(hipStream_t s, const float* part, int nblk, long ncols, long split,
+                          const VecTarget& a, const VecTarget& b);
 
 // ROSA: idx channel-major [batch][ch][time] u8 -> y16 row-major (2*idx-1)*e
 // and the row-major idx tape.
