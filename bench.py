@@ -34,6 +34,15 @@ NO_IGNORE = 0xFFFFFFFF
 HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2516.6  # dense fp16 MFMA, MI355X
 
+# HBM bytes per launch of the probed kernel, from two rocprofv3 --pmc passes
+# (FETCH_SIZE, WRITE_SIZE; KiB per dispatch) over this script with
+# --copy-mib 256, scaled by what the same counters read for the 256 MiB copy
+# kernel (FETCH_SIZE reads half the bytes copied: x2.0; WRITE_SIZE x1.0).
+# Summary: profiles/key_forward_hbm_traffic.txt. Re-measure when the kernel changes.
+TRAFFIC_BYTES = {
+    "key_forward": (1664.5 * 2.0 + 16384.0 * 1.0) * 1024,
+}
+
 
 def cpu_baseline(rows: int) -> dict:
     from oracle import cpu_ref as o
@@ -59,6 +68,23 @@ def cpu_baseline(rows: int) -> dict:
     }
 
 
+def copy_calibration(rt, mib: int) -> None:
+    """One copy kernel (ullis_hip_copy) that reads `mib` MiB and writes `mib` MiB.
+
+    Under `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE` its counter values give the factor
+    between what the counters report and the bytes a kernel actually moves.
+    """
+    from ullis_amd.runtime import DeviceBuffer
+
+    n = mib * (1 << 20)
+    src = DeviceBuffer(rt, n)
+    dst = DeviceBuffer(rt, n)
+    rt._check(rt.lib.ullis_hip_copy(rt.ctx, dst.ptr, src.ptr, n), "copy")
+    rt.sync()
+    src.free()
+    dst.free()
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -68,6 +94,9 @@ def main() -> int:
                     help="rows of the CPU-baseline sample (0 disables it)")
     ap.add_argument("--probe", default="key_forward",
                     help="launch class timed for the roofline object")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="after the timed region, run one plain device copy kernel of this many "
+                         "MiB (read + write) so HBM counters can be scaled against known bytes")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -117,6 +146,8 @@ def main() -> int:
     value = tokens / (ms.value / 1e3)
     kernel = trainer.probe_end(probe)
     loss = float(st.download(np.float32, 4)[0])
+    if args.copy_mib > 0:
+        copy_calibration(rt, args.copy_mib)
 
     roofline = None
     if kernel and kernel["count"]:
@@ -126,7 +157,7 @@ def main() -> int:
         roofline = {
             "bound": kernel["bound"], "achieved": round(achieved, 2), "peak": peak,
             "unit": "TFLOP/s" if kernel["bound"] == "mfma" else "GB/s",
-            "frac": round(achieved / peak, 4), "traffic": kernel.get("traffic"),
+            "frac": round(achieved / peak, 4), "traffic": TRAFFIC_BYTES.get(args.probe),
             "kernel": kernel["name"], "avg_us": round(avg_s * 1e6, 2),
             "launches": kernel["count"],
         }

@@ -171,10 +171,12 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
 /*
  * Kernel probe, the device-side counterpart of the reference's per-phase
  * TrainStepProfile (src/model.rs:101-124): while a probe id is set, every
- * launch of that class inside ullis_hip_heron_step is bracketed by HIP events
- * on the step's stream (at most 512 launches are recorded). probe_read waits
- * for the recorded events and returns the summed kernel time and the number
- * of launches, then restarts the count.
+ * launch of that class inside ullis_hip_heron_step records the start and end
+ * timestamps of its kernel into HIP events (hipExtLaunchKernel), so the time
+ * is the kernel's own execution time; HEAD_CE, which is several kernels, is
+ * instead bracketed by event records on the step's stream. At most 512
+ * launches are recorded. probe_read waits for the recorded events and returns
+ * the summed time and the number of launches, then restarts the count.
  */
 #define ULLIS_HIP_PROBE_NONE 0
 #define ULLIS_HIP_PROBE_KEY_FORWARD 1       /* CMix key packed GEMM + ReLU^2, per layer */

@@ -288,3 +288,20 @@ def test_head_ce_parity_and_update(rt, rows, time, d, vocab, ignore):
     wbits = o.pack_latent_bits(wl)
     np.testing.assert_array_equal(got["next_bits"], wbits)
     np.testing.assert_array_equal(got["next_bits_t"], o.transpose_bits(wbits, vocab, d))
+
+
+# -------------------------------------------------------------- device copy
+@pytest.mark.parametrize("dst_off,src_off,n", [(0, 0, 1 << 20), (3, 3, 4099), (1, 6, 777),
+                                               (0, 0, 5), (16, 0, 4096 + 9)])
+def test_device_copy_kernel(rt, dst_off, src_off, n):
+    from ullis_amd.runtime import DeviceBuffer
+
+    data = np.random.default_rng(n).integers(0, 256, src_off + n + 32).astype(np.uint8)
+    src = rt.put(data)
+    dst = DeviceBuffer(rt, dst_off + n + 32).upload(np.full(dst_off + n + 32, 0xAB, np.uint8))
+    rt._check(rt.lib.ullis_hip_copy(rt.ctx, dst.ptr + dst_off, src.ptr + src_off, n), "copy")
+    got = dst.download(np.uint8, dst_off + n + 32)
+    np.testing.assert_array_equal(got[dst_off:dst_off + n], data[src_off:src_off + n])
+    assert (got[:dst_off] == 0xAB).all() and (got[dst_off + n:] == 0xAB).all()
+    src.free()
+    dst.free()

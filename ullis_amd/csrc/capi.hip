@@ -140,7 +140,8 @@ int ullis_hip_copy(ullis_hip_ctx* c, void* dst, const void* src, size_t bytes) {
   if (bytes == 0) return 0;
   NEED(dst, "dst");
   NEED(src, "src");
-  HIPCALL(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, c->stream), "device copy");
+  if (bytes > (size_t)INT64_MAX) return c->fail(ULLIS_HIP_ERR_INVALID, "copy size too large");
+  HIPCALL(copy_device(c->stream, dst, src, (long)bytes), "device copy");
   return 0;
 }
 

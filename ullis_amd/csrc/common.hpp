@@ -8,6 +8,7 @@
 //    -ffp-contract=off.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -123,6 +124,29 @@ __device__ __forceinline__ void atomic_amax(float* slot, float v) {
 // column = lane % 32, row = 8*(r/4) + 4*(lane/32) + r%4.
 __device__ __forceinline__ int mfma32_row(int r, int lane) {
   return ((r >> 2) << 3) + ((lane >> 5) << 2) + (r & 3);
+}
+
+// ------------------------------------------------------------ launching
+// Kernel-timestamp probe: when armed on the launching thread, the next
+// launch() records its kernel's start and end into these events
+// (hipExtLaunchKernelGGL), i.e. the execution time of the dispatch itself,
+// without the latency of separate event packets around it. launch() disarms
+// the probe when it consumes it.
+struct LaunchProbe {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+inline thread_local LaunchProbe* t_launch_probe = nullptr;
+
+template <typename... KArgs, typename... Args>
+inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds_bytes,
+                   hipStream_t s, Args... args) {
+  if (LaunchProbe* p = t_launch_probe) {
+    t_launch_probe = nullptr;
+    hipExtLaunchKernelGGL(kernel, grid, block, lds_bytes, s, p->start, p->stop, 0u, args...);
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, lds_bytes, s, args...);
+  }
 }
 
 }  // namespace ullis

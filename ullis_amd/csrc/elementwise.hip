@@ -11,6 +11,8 @@
 // Column reductions (g_mix, g_e, g_bias) are two-stage with fixed-order
 // partial sums: deterministic, unlike the Metal float CAS atomics
 // (rwkv8.metal:12-25, :295-323).
+#include <algorithm>
+
 #include "common.hpp"
 #include "ops.hpp"
 
@@ -23,6 +25,20 @@ constexpr int kColChunkRows = 16;
 __global__ void fill_kernel(float* p, long n, float v) {
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
+}
+
+// 16-byte vector copy, grid-stride; the head/tail bytes outside the aligned
+// middle are copied one byte per thread by block 0.
+__global__ void copy_kernel(uint8_t* dst, const uint8_t* src, long head, long vecs, long bytes) {
+  const long stride = (long)gridDim.x * blockDim.x;
+  const u32x4* s = reinterpret_cast<const u32x4*>(src + head);
+  u32x4* d = reinterpret_cast<u32x4*>(dst + head);
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < vecs; i += stride) d[i] = s[i];
+  if (blockIdx.x == 0) {
+    const long tail0 = head + vecs * 16;
+    for (long i = threadIdx.x; i < head; i += blockDim.x) dst[i] = src[i];
+    for (long i = tail0 + threadIdx.x; i < bytes; i += blockDim.x) dst[i] = src[i];
+  }
 }
 
 __global__ void clipped_sgd_kernel(uint16_t* values, float* residual, const float* grad, long n,
@@ -168,28 +184,45 @@ inline dim3 grid1d(long n, int threads = 256) { return dim3((unsigned)cdiv(n, th
 
 hipError_t fill_f32(hipStream_t s, float* p, long n, float v) {
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(fill_kernel, grid1d(n), dim3(256), 0, s, p, n, v);
+  launch(fill_kernel, grid1d(n), dim3(256), 0, s, p, n, v);
+  return hipGetLastError();
+}
+
+hipError_t copy_device(hipStream_t s, void* dst, const void* src, long bytes) {
+  if (bytes <= 0) return hipSuccess;
+  const uintptr_t a = reinterpret_cast<uintptr_t>(dst), b = reinterpret_cast<uintptr_t>(src);
+  long head = 0, vecs = 0;
+  if ((a & 15) == (b & 15)) {
+    head = std::min<long>((long)((16 - (a & 15)) & 15), bytes);
+    vecs = (bytes - head) / 16;
+  } else {
+    head = bytes;  // no common alignment: block 0 copies byte by byte
+  }
+  const long blocks = std::max<long>(1, std::min<long>(cdiv(vecs, 256), 8192));
+  launch(copy_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
+                     static_cast<uint8_t*>(dst), static_cast<const uint8_t*>(src), head, vecs,
+                     bytes);
   return hipGetLastError();
 }
 
 hipError_t clipped_sgd(hipStream_t s, uint16_t* values, float* residual, const float* grad, long n,
                        float lr) {
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(clipped_sgd_kernel, grid1d(n), dim3(256), 0, s, values, residual, grad, n, lr);
+  launch(clipped_sgd_kernel, grid1d(n), dim3(256), 0, s, values, residual, grad, n, lr);
   return hipGetLastError();
 }
 
 hipError_t binaryconnect_sgd(hipStream_t s, uint16_t* values, float* residual, const float* grad,
                              long n, float lr, float grad_scale) {
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(binaryconnect_sgd_kernel, grid1d(n), dim3(256), 0, s, values, residual, grad,
+  launch(binaryconnect_sgd_kernel, grid1d(n), dim3(256), 0, s, values, residual, grad,
                      n, lr, grad_scale);
   return hipGetLastError();
 }
 
 hipError_t sign_pack_bits(hipStream_t s, const float* x, long n, uint32_t* bits) {
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(sign_pack_kernel, grid1d(cdiv(n, 32)), dim3(256), 0, s, x, n, bits);
+  launch(sign_pack_kernel, grid1d(cdiv(n, 32)), dim3(256), 0, s, x, n, bits);
   return hipGetLastError();
 }
 
@@ -197,7 +230,7 @@ hipError_t amax_f32(hipStream_t s, const float* x, long n, float* slot) {
   if (n <= 0) return hipSuccess;
   long blocks = cdiv(n, 256 * 8);
   if (blocks > 1024) blocks = 1024;
-  hipLaunchKernelGGL(amax_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, n, slot);
+  launch(amax_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, n, slot);
   return hipGetLastError();
 }
 
@@ -207,7 +240,7 @@ hipError_t time_shift_mix(hipStream_t s, const uint16_t* x16, long rows, long ti
   if (rows <= 0 || ch <= 0 || time <= 0) return hipSuccess;
   const int group = ch % 8 == 0 ? 8 : 1;
   const long n = rows * (ch / group);
-  hipLaunchKernelGGL(time_shift_mix_kernel, grid1d(n), dim3(256), 0, s, x16, rows, time, ch, mix0,
+  launch(time_shift_mix_kernel, grid1d(n), dim3(256), 0, s, x16, rows, time, ch, mix0,
                      out0, mix1, out1, mix2, out2, group);
   return hipGetLastError();
 }
@@ -218,7 +251,7 @@ hipError_t time_shift_mix_backward(hipStream_t s, const float* g_shifted, const 
   const long nblk = cdiv(rows, kColChunkRows);
   if (nblk_out) *nblk_out = (int)nblk;
   if (rows <= 0 || ch <= 0) return hipSuccess;
-  hipLaunchKernelGGL(time_shift_mix_bwd_kernel, dim3((unsigned)cdiv(ch, 256), (unsigned)nblk),
+  launch(time_shift_mix_bwd_kernel, dim3((unsigned)cdiv(ch, 256), (unsigned)nblk),
                      dim3(256), 0, s, g_shifted, x16, mix, rows, time, ch, g_x, part);
   return hipGetLastError();
 }
@@ -228,7 +261,7 @@ hipError_t column_sum_partials(hipStream_t s, const float* v, const uint8_t* idx
   const long nblk = cdiv(rows, kColChunkRows);
   if (nblk_out) *nblk_out = (int)nblk;
   if (rows <= 0 || ch <= 0) return hipSuccess;
-  hipLaunchKernelGGL(column_sum_kernel, dim3((unsigned)cdiv(ch, 256), (unsigned)nblk), dim3(256), 0,
+  launch(column_sum_kernel, dim3((unsigned)cdiv(ch, 256), (unsigned)nblk), dim3(256), 0,
                      s, v, idx, rows, ch, part);
   return hipGetLastError();
 }
@@ -236,7 +269,7 @@ hipError_t column_sum_partials(hipStream_t s, const float* v, const uint8_t* idx
 hipError_t partial_reduce(hipStream_t s, const float* part, int nblk, long ncols, long split,
                           const VecTarget& a, const VecTarget& b) {
   if (ncols <= 0) return hipSuccess;
-  hipLaunchKernelGGL(partial_reduce_kernel, dim3((unsigned)cdiv(ncols, 64)), dim3(1024), 0, s,
+  launch(partial_reduce_kernel, dim3((unsigned)cdiv(ncols, 64)), dim3(1024), 0, s,
                      part, nblk, ncols, split, a, b);
   return hipGetLastError();
 }
@@ -251,7 +284,7 @@ hipError_t rosa_expand(hipStream_t s, const uint8_t* idx_cm, const uint16_t* e, 
                        long time, long ch, uint16_t* y16, uint8_t* idx_rm) {
   const long n = batch * time * ch;
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(rosa_expand_kernel, grid1d(n), dim3(256), 0, s, idx_cm, e, batch, time, ch,
+  launch(rosa_expand_kernel, grid1d(n), dim3(256), 0, s, idx_cm, e, batch, time, ch,
                      y16, idx_rm);
   return hipGetLastError();
 }

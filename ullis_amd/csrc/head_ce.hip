@@ -233,7 +233,7 @@ hipError_t logits_gemm(hipStream_t s, const uint16_t* hidden16, long rows, long 
     using LB = LoadBits<T::bn, T::bk>;
     LA la{reinterpret_cast<const half_t*>(hidden16), d, vec};
     LB lb{bits_rows, d, 0, nullptr, d % 8 == 0};
-    hipLaunchKernelGGL((gemm_kernel<T::bm, T::bn, T::bk, T::stages, LA, LB, Epi>),
+    launch((gemm_kernel<T::bm, T::bn, T::bk, T::stages, LA, LB, Epi>),
                        dim3((unsigned)(cdiv(rows, T::bm) * cdiv(ncols, T::bn))), dim3(kThreads),
                        0, s, la, lb, epi, (int)rows, (int)ncols, (int)d,
                        (int)(cdiv(d, T::bk) * T::bk));
@@ -264,11 +264,11 @@ hipError_t head_ce(hipStream_t s, const HeadCe& h, void* workspace) {
   EpiCeStats st{h.scale, h.bias, h.targets, h.ignore_id, h.time, w.part_m, w.part_s, w.tgt};
   if ((e = logits_gemm(s, h.hidden16, rows, d, h.bits, V, st)) != hipSuccess) return e;
   // 2. combine
-  hipLaunchKernelGGL(ce_combine_kernel, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, w.part_m,
+  launch(ce_combine_kernel, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, w.part_m,
                      w.part_s, nb32, rows, h.time, h.targets, h.ignore_id, w.tgt, w.lse,
                      h.row_loss);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL(ce_mean_kernel, dim3(1), dim3(1024), 0, s, h.row_loss, rows, h.time,
+  launch(ce_mean_kernel, dim3(1), dim3(1024), 0, s, h.row_loss, rows, h.time,
                      h.targets, h.ignore_id, h.stats);
   if ((e = hipGetLastError()) != hipSuccess) return e;
 

@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "../../include/ullis_hip.h"
+#include "common.hpp"
 #include "context.hpp"
 #include "ops.hpp"
 
@@ -123,16 +124,38 @@ bool bind_packed(ullis_hip_heron* h, const std::string& p, long out, long in, bo
 
 constexpr int kProbeMax = 512;
 
-// Brackets one launch with events when `id` is the probed launch class.
-#define PROBED(id, expr, what)                                                       \
-  do {                                                                               \
-    const bool on_ = h->probe == (id) && h->probe_used < kProbeMax;                  \
-    if (on_) STEP(hipEventRecord(h->probe_events[2 * h->probe_used], s), "probe");   \
-    STEP(expr, what);                                                                \
-    if (on_) {                                                                       \
-      STEP(hipEventRecord(h->probe_events[2 * h->probe_used + 1], s), "probe");      \
-      ++h->probe_used;                                                               \
-    }                                                                                \
+// When `id` is the probed launch class, the kernel that `expr` launches
+// records its own start and end timestamps into the next event pair
+// (LaunchProbe). `expr` must launch exactly one kernel.
+#define PROBED(id, expr, what)                                                     \
+  do {                                                                             \
+    const bool on_ = h->probe == (id) && h->probe_used < kProbeMax;                \
+    LaunchProbe lp_;                                                               \
+    if (on_) {                                                                     \
+      lp_.start = h->probe_events[2 * h->probe_used];                              \
+      lp_.stop = h->probe_events[2 * h->probe_used + 1];                           \
+      t_launch_probe = &lp_;                                                       \
+    }                                                                              \
+    const int rc_ = c->hip((expr), (what));                                        \
+    const bool consumed_ = t_launch_probe == nullptr;                              \
+    t_launch_probe = nullptr;                                                      \
+    if (rc_) return rc_;                                                           \
+    if (on_) {                                                                     \
+      if (!consumed_) return c->fail(ULLIS_HIP_ERR_RUNTIME, "probe: no kernel launched"); \
+      ++h->probe_used;                                                             \
+    }                                                                              \
+  } while (0)
+
+// Brackets a multi-kernel operation with events when `id` is the probed class.
+#define PROBED_SPAN(id, expr, what)                                                \
+  do {                                                                             \
+    const bool on_ = h->probe == (id) && h->probe_used < kProbeMax;                \
+    if (on_) STEP(hipEventRecord(h->probe_events[2 * h->probe_used], s), "probe"); \
+    STEP(expr, what);                                                              \
+    if (on_) {                                                                     \
+      STEP(hipEventRecord(h->probe_events[2 * h->probe_used + 1], s), "probe");    \
+      ++h->probe_used;                                                             \
+    }                                                                              \
   } while (0)
 
 }  // namespace
@@ -364,7 +387,7 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
     if (b.has_ln0) {
       STEP(layer_norm_forward(s, x_emb, R, D, b.ln0.w, b.ln0.b, x_l, nullptr), "ln0");
     } else if (l == 0) {
-      STEP(hipMemcpyAsync(x_l, x_emb, sizeof(float) * nd, hipMemcpyDeviceToDevice, s), "copy x");
+      STEP(copy_device(s, x_l, x_emb, (long)sizeof(float) * nd), "copy x");
     }
     // ROSA block (src/model.rs:1354-1440)
     STEP(layer_norm_forward(s, x_l, R, D, b.ln3.w, b.ln3.b, nullptr, h->ln16), "ln3");
@@ -437,7 +460,7 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
     hc.bias_res = h->head.bias_res;
     hc.bits_new = h->head.bits;
     hc.bits_t_new = h->head.bits_t;
-    PROBED(ULLIS_HIP_PROBE_HEAD_CE, head_ce(s, hc, h->head_ws), "head ce");
+    PROBED_SPAN(ULLIS_HIP_PROBE_HEAD_CE, head_ce(s, hc, h->head_ws), "head ce");
   }
   // LN_out backward + step (src/model.rs:2932-2937)
   STEP(layer_norm_backward_rows(s, x_last, h->g_a, R, D, h->ln_out.w, h->g_x, 0, h->slots + L,
@@ -549,8 +572,7 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
                                    b.ln0.b, b.ln0.b_res),
            "ln0 step");
     } else if (l == 0) {
-      STEP(hipMemcpyAsync(g_emb, h->g_x, sizeof(float) * nd, hipMemcpyDeviceToDevice, s),
-           "copy g_emb");
+      STEP(copy_device(s, g_emb, h->g_x, (long)sizeof(float) * nd), "copy g_emb");
     }
   }
   (void)F;

@@ -42,7 +42,7 @@ hipError_t launch_gemm(hipStream_t s, const LA& la, const LB& lb, const Epi& epi
   if (splits < 1) splits = 1;
   const long tiles = cdiv(M, T::bm) * cdiv(N, T::bn);
   const int ks = (int)(cdiv(cdiv(K, splits), T::bk) * T::bk);
-  hipLaunchKernelGGL((gemm_kernel<T::bm, T::bn, T::bk, T::stages, LA, LB, Epi>),
+  launch((gemm_kernel<T::bm, T::bn, T::bk, T::stages, LA, LB, Epi>),
                      dim3((unsigned)tiles, 1, splits), dim3(kThreads), 0, s, la, lb, epi, (int)M,
                      (int)N, (int)K, ks > 0 ? ks : T::bk);
   return hipGetLastError();
@@ -333,7 +333,7 @@ hipError_t packed_weight_grad_partials(hipStream_t s, GradIn gy32, const uint16_
 
 hipError_t packed_weight_finish(hipStream_t s, const PackedFinish& f) {
   if (f.out <= 0 || f.in <= 0) return hipSuccess;
-  hipLaunchKernelGGL(packed_finish_kernel, dim3((unsigned)f.out), dim3(256), 0, s, f);
+  launch(packed_finish_kernel, dim3((unsigned)f.out), dim3(256), 0, s, f);
   return hipGetLastError();
 }
 
@@ -342,7 +342,7 @@ hipError_t pack_latent_bits(hipStream_t s, const uint16_t* latent, long out, lon
   const long n = out * in;
   if (n <= 0) return hipSuccess;
   const long words = cdiv(n, 32);
-  hipLaunchKernelGGL(pack_bits_kernel, dim3((unsigned)cdiv(words, 256)), dim3(256), 0, s, latent,
+  launch(pack_bits_kernel, dim3((unsigned)cdiv(words, 256)), dim3(256), 0, s, latent,
                      n, bits);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !bits_t) return e;
@@ -356,10 +356,10 @@ hipError_t transpose_bits(hipStream_t s, const uint32_t* bits, long out, long in
   if (out % 32 == 0 && in % 32 == 0) {
     const long blocks32 = (out / 32) * (in / 32);
     const long threads = blocks32 * 32;
-    hipLaunchKernelGGL(transpose_bits_aligned_kernel, dim3((unsigned)cdiv(threads, 256)),
+    launch(transpose_bits_aligned_kernel, dim3((unsigned)cdiv(threads, 256)),
                        dim3(256), 0, s, bits, out, in, bits_t);
   } else {
-    hipLaunchKernelGGL(transpose_bits_generic_kernel, dim3((unsigned)cdiv(cdiv(n, 32), 256)),
+    launch(transpose_bits_generic_kernel, dim3((unsigned)cdiv(cdiv(n, 32), 256)),
                        dim3(256), 0, s, bits, out, in, bits_t);
   }
   return hipGetLastError();
@@ -409,7 +409,7 @@ hipError_t fp16_weight_finish(hipStream_t s, const float* part, int splits, long
                               float* g_w) {
   const long n = out * in;
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(fp16_finish_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, s, part,
+  launch(fp16_finish_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, s, part,
                      splits, n, amax, lr, w, w_res, g_w);
   return hipGetLastError();
 }

@@ -288,12 +288,12 @@ hipError_t layer_norm_forward(hipStream_t s, const float* x, long rows, long ch,
                    (!y16 || (reinterpret_cast<uintptr_t>(y16) & 7u) == 0);
   if (vec) {
     return by_nv(ch, [&](auto nv) {
-      hipLaunchKernelGGL(ln_fwd_vec_kernel<decltype(nv)::value>, grid, dim3(256), 0, s, x, rows,
+      launch(ln_fwd_vec_kernel<decltype(nv)::value>, grid, dim3(256), 0, s, x, rows,
                          (int)ch, w, b, y32, y16);
       return hipGetLastError();
     });
   }
-  hipLaunchKernelGGL(ln_fwd_any_kernel, grid, dim3(256), 0, s, x, rows, (int)ch, w, b, y32, y16);
+  launch(ln_fwd_any_kernel, grid, dim3(256), 0, s, x, rows, (int)ch, w, b, y32, y16);
   return hipGetLastError();
 }
 
@@ -318,12 +318,12 @@ hipError_t layer_norm_backward_rows(hipStream_t s, const float* x, const float* 
   if (nblk_out) *nblk_out = nblk;
   if (ln_bwd_vec_path(ch) && vec_ok(x) && vec_ok(gy) && vec_ok(gx)) {
     return by_nv(ch, [&](auto nv) {
-      hipLaunchKernelGGL(ln_bwd_vec_kernel<decltype(nv)::value>, dim3(nblk), dim3(256), 0, s, x,
+      launch(ln_bwd_vec_kernel<decltype(nv)::value>, dim3(nblk), dim3(256), 0, s, x,
                          gy, rows, (int)ch, w, gx, accumulate, amax, part);
       return hipGetLastError();
     });
   }
-  hipLaunchKernelGGL(ln_bwd_any_kernel, dim3(nblk), dim3(64), 0, s, x, gy, rows, (int)ch, w, gx,
+  launch(ln_bwd_any_kernel, dim3(nblk), dim3(64), 0, s, x, gy, rows, (int)ch, w, gx,
                      accumulate, amax, part);
   return hipGetLastError();
 }

@@ -118,6 +118,8 @@ hipError_t layer_norm_param_finish(hipStream_t s, const float* part, int nblk, l
 // ---------------------------------------------------------------- elementwise
 
 hipError_t fill_f32(hipStream_t s, float* p, long n, float v);
+// Device-to-device byte copy as a kernel on stream s.
+hipError_t copy_device(hipStream_t s, void* dst, const void* src, long bytes);
 hipError_t clipped_sgd(hipStream_t s, uint16_t* values, float* residual, const float* grad, long n,
                        float lr);
 hipError_t binaryconnect_sgd(hipStream_t s, uint16_t* values, float* residual, const float* grad,
