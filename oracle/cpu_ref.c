@@ -27,8 +27,10 @@
  *  - CMix: closed forms of tests/cmix.rs:33-72; finite differences of
  *    time-shift-mix backward.
  *  - ROSA y / g_e: float64 numpy.
- *  - heron step: composition of the above; update-order rules checked by
- *    comparing against a numpy float64 re-derivation at tiny size.
+ *  - heron step: tests/test_oracle_heron.py, an independent float64 numpy
+ *    re-derivation of train_step_on at tiny sizes, including a case with
+ *    large scales and learning rate in which any update-order mistake
+ *    changes the result.
  */
 #include "cpu_ref.h"
 
