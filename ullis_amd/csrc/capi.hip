@@ -13,6 +13,10 @@
 using namespace ullis;
 
 namespace {
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+}  // namespace
+
+namespace {
 
 constexpr int kVersion = 1;
 
@@ -236,7 +240,8 @@ int ullis_hip_binary_linear_backward(ullis_hip_ctx* c, const uint16_t* x16, cons
   const long words = cdiv(I * O, 32);
   const long nb = column_partial_blocks(R);
   const size_t need = Carver::bytes_for(4 * words) + Carver::bytes_for(4ul * splits * O * I) +
-                      Carver::bytes_for(4) + Carver::bytes_for(4ul * nb * O);
+                      Carver::bytes_for(4) + Carver::bytes_for(4ul * nb * O) +
+                      Carver::bytes_for(2ul * R * O);
   void* ws = nullptr;
   if (int rc = c->ensure_scratch(need, &ws)) return rc;
   Carver cv(ws);
@@ -244,16 +249,19 @@ int ullis_hip_binary_linear_backward(ullis_hip_ctx* c, const uint16_t* x16, cons
   float* part = cv.take<float>((size_t)splits * O * I);
   float* slot = cv.take<float>(1);
   float* cpart = cv.take<float>((size_t)nb * O);
+  uint16_t* gy16 = cv.take<uint16_t>((size_t)R * O);
   HIPCALL(fill_f32(c->stream, slot, 1, 0.0f), "fill");
   HIPCALL(amax_f32(c->stream, gy, R * O, slot), "amax");
+  // fp16 operand copy of the scaled gradient (the GEMMs use it when their
+  // shapes allow the streamed-LDS kernels)
+  const GradIn g{gy, slot, aligned16(gy) ? gy16 : nullptr};
+  if (g.p16) HIPCALL(scale_to_f16(c->stream, gy, R * O, slot, gy16), "gy fp16");
   if (gx) {
     HIPCALL(transpose_bits(c->stream, bits, O, I, bits_t), "transpose_bits");
-    HIPCALL(packed_backward_input(c->stream, GradIn{gy, slot}, nullptr, R, I, O, bits_t, scale, gx,
-                                  nullptr, 0),
+    HIPCALL(packed_backward_input(c->stream, g, nullptr, R, I, O, bits_t, scale, gx, nullptr, 0),
             "binary_linear input grad");
   }
-  HIPCALL(packed_weight_grad_partials(c->stream, GradIn{gy, slot}, nullptr, x16, R, I, O, splits,
-                                      part),
+  HIPCALL(packed_weight_grad_partials(c->stream, g, nullptr, x16, R, I, O, splits, part),
           "binary_linear weight grad");
   PackedFinish f;
   f.part = part;
@@ -322,17 +330,22 @@ int ullis_hip_fp16_linear_backward(ullis_hip_ctx* c, const uint16_t* x16, const 
   const long R = (long)rows, I = (long)in, O = (long)out;
   const int splits = dw_splits(O, I, R);
   void* ws = nullptr;
-  if (int rc = c->ensure_scratch(Carver::bytes_for(4ul * splits * O * I) + Carver::bytes_for(4), &ws))
+  if (int rc = c->ensure_scratch(Carver::bytes_for(4ul * splits * O * I) + Carver::bytes_for(4) +
+                                     Carver::bytes_for(2ul * R * O),
+                                 &ws))
     return rc;
   Carver cv(ws);
   float* part = cv.take<float>((size_t)splits * O * I);
   float* slot = cv.take<float>(1);
+  uint16_t* gy16 = cv.take<uint16_t>((size_t)R * O);
   HIPCALL(fill_f32(c->stream, slot, 1, 0.0f), "fill");
   HIPCALL(amax_f32(c->stream, gy, R * O, slot), "amax");
+  const GradIn g{gy, slot, aligned16(gy) ? gy16 : nullptr};
+  if (g.p16) HIPCALL(scale_to_f16(c->stream, gy, R * O, slot, gy16), "gy fp16");
   if (gx)
-    HIPCALL(fp16_backward_input(c->stream, GradIn{gy, slot}, R, I, O, w, gx, nullptr, nullptr),
+    HIPCALL(fp16_backward_input(c->stream, g, R, I, O, w, gx, nullptr, nullptr),
             "fp16_linear input grad");
-  HIPCALL(fp16_weight_grad_partials(c->stream, GradIn{gy, slot}, x16, R, I, O, splits, part),
+  HIPCALL(fp16_weight_grad_partials(c->stream, g, x16, R, I, O, splits, part),
           "fp16_linear weight grad");
   HIPCALL(fp16_weight_finish(c->stream, part, splits, O, I, slot, 0.0f, nullptr, nullptr, gw),
           "fp16_linear finish");

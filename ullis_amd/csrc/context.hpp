@@ -61,11 +61,11 @@ struct Carver {
   static size_t bytes_for(size_t bytes) { return (bytes + 255) / 256 * 256; }
 };
 
-// Split-K factor for a weight-gradient GEMM [out, in] over `rows`.
+// Split-K factor for a weight-gradient GEMM [out, in] over `rows`: enough
+// 64x64-tile blocks for two per CU (512), at least 256 rows per split, at most 8.
 inline int dw_splits(long out, long in, long rows) {
-  long tiles = cdiv(out, 128) * cdiv(in, 128);
-  if (tiles < 240) tiles = cdiv(out, 64) * cdiv(in, 64);
-  long s = 256 / (tiles > 0 ? tiles : 1);
+  const long tiles = cdiv(out, 64) * cdiv(in, 64);
+  long s = cdiv(512, tiles > 0 ? tiles : 1);
   const long by_rows = rows / 256;
   if (s > by_rows) s = by_rows;
   if (s > 8) s = 8;

@@ -121,18 +121,36 @@ __global__ void time_shift_mix_bwd_kernel(const float* g_s, const uint16_t* x16,
 }
 
 __global__ void column_sum_kernel(const float* v, const uint8_t* idx, long rows, long ch,
-                                  float* part) {
+                                  float* part, uint16_t* out16, const float* amax) {
   const long c = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= ch) return;
   const long r0 = (long)blockIdx.y * kColChunkRows;
   const long r1 = r0 + kColChunkRows < rows ? r0 + kColChunkRows : rows;
+  const float sc = out16 ? grad_scale_from_amax(*amax) : 1.0f;
   float s = 0.0f;
   for (long row = r0; row < r1; ++row) {
     const long i = row * ch + c;
     const float x = v[i];
     s += idx ? x * (2.0f * (float)idx[i] - 1.0f) : x;
+    if (out16) out16[i] = __builtin_bit_cast(uint16_t, f32_to_f16_sat(x * sc));
   }
   part[(long)blockIdx.y * ch + c] = s;
+}
+
+// out16 = f16_sat(v * grad_scale_from_amax(*amax)), 4 elements per thread.
+__global__ void scale_to_f16_kernel(const float* v, long n, const float* amax, uint16_t* out16) {
+  const float sc = grad_scale_from_amax(*amax);
+  const long i = ((long)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i + 3 < n) {
+    const floatx4 x = *reinterpret_cast<const floatx4*>(v + i);
+    uint32_t lo = __builtin_bit_cast(uint16_t, f32_to_f16_sat(x[0] * sc)) |
+                  ((uint32_t)__builtin_bit_cast(uint16_t, f32_to_f16_sat(x[1] * sc)) << 16);
+    uint32_t hi = __builtin_bit_cast(uint16_t, f32_to_f16_sat(x[2] * sc)) |
+                  ((uint32_t)__builtin_bit_cast(uint16_t, f32_to_f16_sat(x[3] * sc)) << 16);
+    *reinterpret_cast<uint2*>(out16 + i) = make_uint2(lo, hi);
+  } else {
+    for (long j = i; j < n; ++j) out16[j] = __builtin_bit_cast(uint16_t, f32_to_f16_sat(v[j] * sc));
+  }
 }
 
 // Sums part[nblk][ncols] over nblk: 64 columns per block, 16 partial subsets
@@ -257,12 +275,24 @@ hipError_t time_shift_mix_backward(hipStream_t s, const float* g_shifted, const 
 }
 
 hipError_t column_sum_partials(hipStream_t s, const float* v, const uint8_t* idx, long rows,
-                               long ch, float* part, int* nblk_out) {
+                               long ch, float* part, int* nblk_out, uint16_t* out16,
+                               const float* amax) {
   const long nblk = cdiv(rows, kColChunkRows);
   if (nblk_out) *nblk_out = (int)nblk;
   if (rows <= 0 || ch <= 0) return hipSuccess;
-  launch(column_sum_kernel, dim3((unsigned)cdiv(ch, 256), (unsigned)nblk), dim3(256), 0,
-                     s, v, idx, rows, ch, part);
+  if (out16 && !amax) return hipErrorInvalidValue;
+  launch(column_sum_kernel, dim3((unsigned)cdiv(ch, 256), (unsigned)nblk), dim3(256), 0, s, v,
+         idx, rows, ch, part, out16, amax);
+  return hipGetLastError();
+}
+
+hipError_t scale_to_f16(hipStream_t s, const float* v, long n, const float* amax,
+                        uint16_t* out16) {
+  if (n <= 0) return hipSuccess;
+  if ((reinterpret_cast<uintptr_t>(v) & 15u) != 0 || (reinterpret_cast<uintptr_t>(out16) & 7u) != 0)
+    return hipErrorInvalidValue;
+  launch(scale_to_f16_kernel, dim3((unsigned)cdiv(cdiv(n, 4), 256)), dim3(256), 0, s, v, n, amax,
+         out16);
   return hipGetLastError();
 }
 

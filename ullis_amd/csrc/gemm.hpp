@@ -586,16 +586,44 @@ struct EpiPartial {
     for_each_acc(acc, row0, col0, lane, M, N,
                  [&](int row, int col, float v) { dst[(long)row * N + col] = v; });
   }
+  // 16 consecutive columns of one row (streamed-LDS kernels).
+  __device__ void row16(int row, int col, float (&v)[16], int, int M, int N, float*, int, int) {
+    if (row >= M) return;
+    float* dst = part + (long)blockIdx.z * M * N + (long)row * N + col;
+    if (col + 16 <= N && N % 8 == 0 && (reinterpret_cast<uintptr_t>(part) & 15u) == 0) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        floatx4 t;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[e] = v[4 * q + e];
+        *reinterpret_cast<floatx4*>(dst + 4 * q) = t;
+      }
+    } else {
+      for (int k = 0; k < 16 && col + k < N; ++k) dst[k] = v[k];
+    }
+  }
 };
 
 // Tile configurations: 128x128 tiles (BK 32, 2 register stages: 16 MFMAs per
 // wave per step already cover a load, and a third stage spills) when they
 // alone give about one block per CU, else 64x64 tiles (BK 64, 3 stages).
+#ifndef ULLIS_XL_BK
+#define ULLIS_XL_BK 32
+#endif
+#ifndef ULLIS_XL_S
+#define ULLIS_XL_S 2
+#endif
+#ifndef ULLIS_XS_BK
+#define ULLIS_XS_BK 64
+#endif
+#ifndef ULLIS_XS_S
+#define ULLIS_XS_S 3
+#endif
 struct CfgLarge {
-  static constexpr int bm = 128, bn = 128, bk = 32, stages = 2;
+  static constexpr int bm = 128, bn = 128, bk = ULLIS_XL_BK, stages = ULLIS_XL_S;
 };
 struct CfgSmall {
-  static constexpr int bm = 64, bn = 64, bk = 64, stages = 3;
+  static constexpr int bm = 64, bn = 64, bk = ULLIS_XS_BK, stages = ULLIS_XS_S;
 };
 
 }  // namespace ullis

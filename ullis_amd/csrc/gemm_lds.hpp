@@ -1,0 +1,433 @@
+// Streamed-LDS fp16 MFMA GEMM for gfx950:  C[m][n] = sum_k A(m, k) * B(n, k).
+//
+// Operands move from HBM straight into LDS with global_load_lds_dwordx4 /
+// global_load_lds_dword (LDS DMA: lane i of a wave writes 16 or 4 bytes at
+// M0 + 16 i or M0 + 4 i), so no registers hold tiles in flight and the K loop
+// can keep NS-1 stages of loads outstanding in an NS-buffer LDS ring. Each
+// step waits for its own stage with an exact `s_waitcnt vmcnt(n)` (every wave
+// issues the same number of loads per stage), then one s_barrier; the loads
+// of stage t+NS-1 go out right after that barrier, into the buffer that stage
+// t-1 used.
+//
+// Block = 256 threads = 4 wave64s in a 2x2 grid, each owning a (BM/2) x (BN/2)
+// sub-tile of 32x32 v_mfma_f32_32x32x16_f16 tiles with fp32 accumulation
+// (the same accumulator layout and epilogue interface as gemm.hpp).
+//
+// Operand layouts in LDS (one stage):
+//   OpMK    fp16 [row][k], k contiguous in HBM. LDS rows of BK halves with the
+//           16-byte chunks XOR-swizzled by row, so the ds_read_b128 fragment
+//           reads of 16 consecutive rows hit 16 distinct 16-byte slots of a
+//           256-byte bank window.
+//   OpKM    fp16 [k][row], rows contiguous in HBM (a transposed operand, e.g.
+//           activations for a weight gradient). LDS keeps [k][row]; fragments
+//           come from ds_read_b64_tr_b16, which hands each lane of a 16-lane
+//           group 4 k-consecutive values of one row: with lane q of the group
+//           pointing at (k0 + q/4, m0 + 4 (q%4)), lane L receives
+//           (k0 + j, m0 + L) for j = 0..3. Chunks are swizzled by 2 (k%4).
+//   OpBits  LSB-first u32 sign words [row][k/32]; the raw words are streamed
+//           (1/16 of the bytes of an fp16 operand) and each fragment expands
+//           its 8 bits, one nibble at a time through a 16-entry LDS table of
+//           fp16 sign bits, to +-1 fp16, or to +-scale[k] when a per-k scale
+//           vector is given (staged in LDS once for the block's K range).
+//
+// Requirements (checked by the launchers, which fall back to gemm.hpp):
+// every split's K range is a multiple of BK, operand pointers are 16-byte
+// aligned with row pitches a multiple of 8 halves (4 words for bits), and
+// OpKM extents are multiples of 8. Tile rows past M / N read a clamped,
+// in-bounds row; their results are never stored.
+#pragma once
+
+#include "common.hpp"
+#include "gemm.hpp"
+#include "ops.hpp"
+
+namespace ullis {
+namespace lds {
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef const __attribute__((address_space(1))) void gbl_void_t;
+
+// Per-lane 16-byte (or 4-byte) copy HBM -> LDS at wave-uniform base + lane * size.
+__device__ __forceinline__ void dma16(const void* src, char* lds_base) {
+  __builtin_amdgcn_global_load_lds((gbl_void_t*)src, (lds_void_t*)lds_base, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* src, char* lds_base) {
+  __builtin_amdgcn_global_load_lds((gbl_void_t*)src, (lds_void_t*)lds_base, 4, 0, 0);
+}
+
+// Wait until at most N vector-memory operations of this wave are in flight
+// and its LDS operations are done, then barrier. No compiler fence: the
+// fence of __syncthreads() would wait for every load in flight.
+template <int N>
+__device__ __forceinline__ void wait_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// fp16 [row][k] with k contiguous.
+template <int ROWS, int BK>
+struct OpMK {
+  const half_t* p;
+  long ld;   // halves between rows
+  int rows;  // valid rows (tile rows past it are clamped)
+  static constexpr int CPR = BK / 8;  // 16-byte chunks per row
+  static constexpr int kBytes = ROWS * BK * 2;
+  static_assert(kBytes % 4096 == 0, "a stage must be whole wave-loads for 4 waves");
+  static constexpr int kInst = kBytes / 4096;  // loads per wave per stage
+  static constexpr int kExtra = 0;
+  static_assert(CPR == 4 || CPR == 8, "BK 32 or 64");
+  // LDS serves 16 lanes of a ds_read_b128 per cycle from a 256-byte bank
+  // window: 16 consecutive rows must land in 16 distinct 16-byte slots.
+  // Rows are 64 B (BK 32: 4 rows per window) or 128 B (BK 64: 2 per window),
+  // so the chunk index is XORed with the row bits above those.
+  __device__ static int swz(int row) {
+    if constexpr (CPR == 8)
+      return (row >> 1) & 7;
+    else
+      return (row >> 2) & 3;
+  }
+  __device__ void prepare(char*, int, int) const {}
+  __device__ __forceinline__ void issue(char* stage, int row0, int k0, int wave, int lane) const {
+#pragma unroll
+    for (int t = 0; t < kInst; ++t) {
+      const int id = (wave * kInst + t) * 64 + lane;
+      const int row = id / CPR, pos = id % CPR;
+      const int c = pos ^ swz(row);
+      const int r = min(row0 + row, rows - 1);
+      dma16(p + (long)r * ld + k0 + 8 * c, stage + (wave * kInst + t) * 1024);
+    }
+  }
+  // Fragment of the 32-row block starting at tile row `base`, k offset ks16 of
+  // the stage: lane l gets row base + l%32, k = ks16 + 8 (l/32) .. +7.
+  __device__ __forceinline__ half8 frag(const char* stage, const char*, int base, int ks16,
+                                        int lane, int) const {
+    const int row = base + (lane & 31);
+    const int c = (ks16 >> 3) + (lane >> 5);
+    return *reinterpret_cast<const half8*>(stage + row * (BK * 2) + 16 * (c ^ swz(row)));
+  }
+};
+
+// fp16 [k][row] with rows contiguous (a transposed operand).
+template <int ROWS, int BK>
+struct OpKM {
+  const half_t* p;
+  long ld;   // halves between k rows
+  int rows;  // valid rows (multiple of 8)
+  static constexpr int CPR = ROWS / 8;  // chunks per k row
+  static_assert(CPR >= 8, "OpKM needs at least 64 rows per tile");
+  static constexpr int kBytes = ROWS * BK * 2;
+  static_assert(kBytes % 4096 == 0, "a stage must be whole wave-loads for 4 waves");
+  static constexpr int kInst = kBytes / 4096;
+  static constexpr int kExtra = 0;
+  __device__ static int swz(int k) { return 2 * (k & 3); }
+  __device__ void prepare(char*, int, int) const {}
+  __device__ __forceinline__ void issue(char* stage, int row0, int k0, int wave, int lane) const {
+#pragma unroll
+    for (int t = 0; t < kInst; ++t) {
+      const int id = (wave * kInst + t) * 64 + lane;
+      const int kr = id / CPR, pos = id % CPR;
+      const int c = pos ^ swz(kr);
+      const int m = min(row0 + 8 * c, rows - 8);
+      dma16(p + (long)(k0 + kr) * ld + m, stage + (wave * kInst + t) * 1024);
+    }
+  }
+  __device__ __forceinline__ half8 frag(const char* stage, const char*, int base, int ks16,
+                                        int lane, int) const {
+    const int g = lane >> 4, q = lane & 15;
+    const int m = base + 16 * (g & 1) + 4 * (q & 3);
+    const int kq = ks16 + 8 * (g >> 1) + (q >> 2);
+    const int k0 = kq, k1 = kq + 4;
+    const char* a0 = stage + k0 * (ROWS * 2) + 16 * ((m >> 3) ^ swz(k0)) + 2 * (m & 7);
+    const char* a1 = stage + k1 * (ROWS * 2) + 16 * ((m >> 3) ^ swz(k1)) + 2 * (m & 7);
+    typedef __fp16 h4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const h4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+        (__attribute__((address_space(3))) h4*)(a0));
+    const h4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+        (__attribute__((address_space(3))) h4*)(a1));
+    const u32x2 l = __builtin_bit_cast(u32x2, lo), h = __builtin_bit_cast(u32x2, hi);
+    const u32x4 r = {l[0], l[1], h[0], h[1]};
+    return __builtin_bit_cast(half8, r);
+  }
+};
+
+// Packed sign bits [row][k/32] (LSB-first u32 words, row pitch `ldw` words).
+// With `scale` (fp16 bits, indexed by k), bit b becomes +-scale[k] instead of
+// +-1. The block's scale range is staged in LDS by prepare().
+template <int ROWS, int BK, bool SCALED>
+struct OpBits {
+  const uint32_t* p;
+  long ldw;  // words between rows
+  int rows;
+  const uint16_t* scale;  // SCALED only, indexed by kofs + k
+  int kofs;               // k offset into the rows (multiple of 32)
+  static constexpr int WPR = BK / 32;  // words per row per stage
+  static constexpr int kWords = ROWS * WPR;
+  static_assert(kWords % 4 == 0 && kWords / 4 <= 64, "bit tile must split into 4 wave loads");
+  static constexpr int kWordsPerWave = kWords / 4;
+  static constexpr int kBytes = ((kWords * 4 + 255) / 256) * 256;
+  static constexpr int kInst = 1;
+  static constexpr int kMaxScaleK = 8192;
+  // extra: 16-entry sign table (128 B), then the scale range when SCALED.
+  static constexpr int kLut = 128;
+  static constexpr int kExtra = kLut + (SCALED ? kMaxScaleK * 2 : 0);
+  __device__ void prepare(char* extra, int kbeg, int kend) const {
+    // Entry n (4 weight bits) = the fp16 sign bits of 4 halves: 0x8000 where
+    // bit j of n is 0 (weight -1). Every entry is 8 bytes, so 16 entries cover
+    // the 32 banks of a 128-byte row once: lookups never conflict.
+    if (threadIdx.x < 32) {
+      const int n = threadIdx.x >> 1, h = threadIdx.x & 1;
+      const uint32_t nb = ~(uint32_t)n >> (2 * h);
+      reinterpret_cast<uint32_t*>(extra)[threadIdx.x] = ((nb & 1u) << 15) | ((nb & 2u) << 30);
+    }
+    if constexpr (SCALED) {
+      uint16_t* s = reinterpret_cast<uint16_t*>(extra + kLut);
+      for (int k = kbeg + (int)threadIdx.x; k < kend; k += kThreads) s[k - kbeg] = scale[kofs + k];
+    }
+  }
+  __device__ __forceinline__ void issue(char* stage, int row0, int k0, int wave, int lane) const {
+    if (lane < kWordsPerWave) {
+      const int id = wave * kWordsPerWave + lane;
+      const int row = id / WPR, w = id % WPR;
+      const int r = min(row0 + row, rows - 1);
+      dma4(p + (long)r * ldw + ((kofs + k0) >> 5) + w, stage + wave * kWordsPerWave * 4);
+    }
+  }
+  // k0rel: the stage's first k relative to the block's kbeg (scale index).
+  __device__ __forceinline__ half8 frag(const char* stage, const char* extra, int base, int ks16,
+                                        int lane, int k0rel) const {
+    const int row = base + (lane & 31);
+    const int kk = ks16 + 8 * (lane >> 5);  // k offset within the stage
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const uint32_t word = reinterpret_cast<const uint32_t*>(stage)[row * WPR + (kk >> 5)];
+    const int sh = kk & 31;
+    const u32x2 lo = *reinterpret_cast<const u32x2*>(extra + 8 * ((word >> sh) & 15u));
+    const u32x2 hi = *reinterpret_cast<const u32x2*>(extra + 8 * ((word >> (sh + 4)) & 15u));
+    u32x4 o = {lo[0], lo[1], hi[0], hi[1]};
+    if constexpr (SCALED) {
+      o ^= *reinterpret_cast<const u32x4*>(extra + kLut + 2 * (k0rel + kk));
+    } else {
+      o |= 0x3C003C00u;
+    }
+    return __builtin_bit_cast(half8, o);
+  }
+};
+
+// wait_barrier<IPS * later>() for a runtime `later` in [0, S] (the K-loop tail).
+template <int IPS, int S>
+__device__ __forceinline__ void wait_stages(int later) {
+  if constexpr (S == 0) {
+    wait_barrier<0>();
+  } else {
+    if (later >= S)
+      wait_barrier<IPS * S>();
+    else
+      wait_stages<IPS, S - 1>(later);
+  }
+}
+
+// ------------------------------------------------------------ epilogue
+// Row-wise epilogue: each 32x32 accumulator block of a wave is scattered into
+// a per-wave LDS buffer [32][kBufPitch] fp32 and read back so that lane l
+// holds row l/2, columns 16 (l%2) .. +15 of the block. The epilogue functor's
+// row16(row, col, v, lane, M, N, buf, brow, bcol) then works on 16 consecutive
+// columns of one row (vector loads / stores, in-register row reductions);
+// (brow, bcol) is the block origin and buf the block in LDS, which a functor
+// may overwrite for column reductions (it must leave the lanes in step).
+constexpr int kBufPitch = 36;  // floats; 144-byte rows keep both passes conflict-light
+constexpr int kBufFloats = 32 * kBufPitch;
+
+__device__ __forceinline__ void lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+template <class Epi, int TM, int TN>
+__device__ __forceinline__ void epilogue_rows(Epi& epi, floatx16 (&acc)[TM][TN], float* buf,
+                                              int row0, int col0, int lane, int M, int N) {
+  const int rr = lane >> 1, cc = (lane & 1) * 16;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) buf[mfma32_row(r, lane) * kBufPitch + (lane & 31)] = acc[i][j][r];
+      lds_fence();
+      float v[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const floatx4 t = *reinterpret_cast<const floatx4*>(buf + rr * kBufPitch + cc + 4 * q);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[4 * q + e] = t[e];
+      }
+      lds_fence();
+      const int brow = row0 + i * 32, bcol = col0 + j * 32;
+      epi.row16(brow + rr, bcol + cc, v, lane, M, N, buf, brow, bcol);
+      lds_fence();
+    }
+}
+
+// 16 consecutive fp16 / fp32 values at p (16-byte aligned).
+__device__ __forceinline__ void load16h(const uint16_t* p, float (&v)[16]) {
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const half8 h = *reinterpret_cast<const half8*>(p + 8 * q);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[8 * q + e] = (float)h[e];
+  }
+}
+__device__ __forceinline__ void store16h(uint16_t* p, const float (&v)[16]) {
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    half8 h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = (half_t)v[8 * q + e];
+    *reinterpret_cast<half8*>(p + 8 * q) = h;
+  }
+}
+__device__ __forceinline__ void load16f(const float* p, float (&v)[16]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const floatx4 t = *reinterpret_cast<const floatx4*>(p + 4 * q);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[4 * q + e] = t[e];
+  }
+}
+__device__ __forceinline__ void store16f(float* p, const float (&v)[16]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    floatx4 t;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) t[e] = v[4 * q + e];
+    *reinterpret_cast<floatx4*>(p + 4 * q) = t;
+  }
+}
+
+__device__ __forceinline__ bool al16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+// p[col .. col+15] as float; entries past n read as 0. vec: whole and aligned.
+__device__ __forceinline__ void get16h(const uint16_t* p, int col, int n, bool vec,
+                                       float (&v)[16]) {
+  if (vec) {
+    load16h(p + col, v);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = col + k < n ? f16_bits_to_f32(p[col + k]) : 0.0f;
+  }
+}
+
+template <int BM, int BN, int BK, int NS, class OA, class OB, class Epi>
+__global__ __launch_bounds__(256) void gemm_lds_kernel(OA a, OB b, Epi epi, int M, int N, int K,
+                                                       int k_split) {
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int STAGE = OA::kBytes + OB::kBytes;
+  constexpr int IPS = OA::kInst + OB::kInst;  // loads per wave per stage
+  static_assert(TM >= 1 && TN >= 1, "tile too small");
+  static_assert(NS >= 2 && IPS * (NS - 2) < 64, "pipeline depth");
+  constexpr int RING = NS * STAGE > 4 * kBufFloats * 4 ? NS * STAGE : 4 * kBufFloats * 4;
+  __shared__ __attribute__((aligned(1024))) char smem[RING + OA::kExtra + OB::kExtra];
+  char* extra_a = smem + RING;
+  char* extra_b = extra_a + OA::kExtra;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  int tm, tn;
+  tile_of_block(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int kbeg = blockIdx.z * k_split;
+  const int kend = min(K, kbeg + k_split);
+  const int nk = kend > kbeg ? (kend - kbeg) / BK : 0;
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = (floatx16){};
+
+  a.prepare(extra_a, kbeg, kend);
+  b.prepare(extra_b, kbeg, kend);
+  auto issue = [&](int kt) {
+    char* st = smem + (kt % NS) * STAGE;
+    a.issue(st, m0, kbeg + kt * BK, wave, lane);
+    b.issue(st + OA::kBytes, n0, kbeg + kt * BK, wave, lane);
+  };
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < nk) issue(s);
+
+  for (int kt = 0; kt < nk; ++kt) {
+    // Stage kt is complete once at most the later stages' loads are in flight.
+    wait_stages<IPS, NS - 2>(nk - 1 - kt);
+    if (kt + NS - 1 < nk) issue(kt + NS - 1);
+    const char* st = smem + (kt % NS) * STAGE;
+    const int k0rel = kt * BK;
+#pragma unroll
+    for (int ks = 0; ks < BK; ks += 16) {
+      half8 af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = a.frag(st, extra_a, wm * WM + i * 32, ks, lane, k0rel);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        bf[j] = b.frag(st + OA::kBytes, extra_b, wn * WN + j * 32, ks, lane, k0rel);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+  }
+  wait_barrier<0>();  // every wave is done reading the ring
+  epilogue_rows(epi, acc, reinterpret_cast<float*>(smem) + wave * kBufFloats, m0 + wm * WM,
+                n0 + wn * WN, lane, M, N);
+}
+
+// ------------------------------------------------------------ host dispatch
+// Measured on MI355X for the heron shapes (2048 rows): 64x64 tiles with BK 64
+// and a 2-stage ring run four blocks per CU and beat 128x128 tiles (one block
+// per CU) everywhere except very wide outputs (the vocab head), where 128x128
+// tiles with 4 stages win; more ring stages did not help either.
+struct LdsBig {
+  static constexpr int bm = 128, bn = 128, bk = 32, ns = 4;
+};
+struct LdsMid {
+  static constexpr int bm = 64, bn = 64, bk = 64, ns = 2;
+};
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool mk_ok(const void* p, long ld) { return p && aligned16(p) && ld % 8 == 0; }
+inline bool km_ok(const void* p, long ld, long rows) {
+  return p && aligned16(p) && ld % 8 == 0 && rows % 8 == 0 && rows >= 8;
+}
+
+// Runs f(T) with the streamed-LDS tile config for an M x N output when K
+// splits into whole BK steps; returns false (and runs nothing) otherwise.
+// big_tiles: number of 128x128 tiles from which the 128x128 config is used.
+template <class F>
+bool with_lds(long M, long N, long K, int splits, hipError_t* err, F&& f, long big_tiles = 960) {
+  if (M <= 0 || N <= 0 || K <= 0 || splits < 1) return false;
+  auto go = [&](auto t) {
+    using T = decltype(t);
+    if (K % T::bk != 0) return false;
+    *err = f(t);
+    return true;
+  };
+  if (cdiv(M, 128) * cdiv(N, 128) >= big_tiles) return go(LdsBig{});
+  return go(LdsMid{});
+}
+
+template <class T, class OA, class OB, class Epi>
+hipError_t launch_lds(hipStream_t s, const OA& a, const OB& b, const Epi& epi, long M, long N,
+                      long K, int splits) {
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return hipErrorInvalidValue;
+  if (splits < 1) splits = 1;
+  const long tiles = cdiv(M, T::bm) * cdiv(N, T::bn);
+  const int ks = (int)(cdiv(cdiv(K, splits), T::bk) * T::bk);
+  launch((gemm_lds_kernel<T::bm, T::bn, T::bk, T::ns, OA, OB, Epi>),
+         dim3((unsigned)tiles, 1, splits), dim3(kThreads), 0, s, a, b, epi, (int)M, (int)N, (int)K,
+         ks);
+  return hipGetLastError();
+}
+
+}  // namespace lds
+}  // namespace ullis

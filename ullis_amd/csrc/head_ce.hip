@@ -25,6 +25,8 @@
 #include <math.h>
 
 #include "gemm.hpp"
+#include "context.hpp"
+#include "gemm_lds.hpp"
 #include "ops.hpp"
 
 namespace ullis {
@@ -83,6 +85,52 @@ struct EpiCeStats {
         }
       }
   }
+  // Streamed-LDS kernels: lanes 2r, 2r+1 hold the two 16-column halves of one
+  // row of a 32-column block; their (max, sum-exp) pairs merge in registers.
+  __device__ void row16(int row, int col, float (&v)[16], int lane, int M, int N, float*, int,
+                        int) {
+    const bool full = col + 16 <= N && N % 8 == 0;
+    float sc[16], bi[16];
+    lds::get16h(scale, col, N, full && lds::al16(scale), sc);
+    if (bias) {
+      lds::get16h(bias, col, N, full && lds::al16(bias), bi);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) bi[k] = 0.0f;
+    }
+    float l[16];
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      l[k] = col + k < N ? bi[k] + sc[k] * v[k] : -INFINITY;
+      m = __builtin_fmaxf(m, l[k]);
+    }
+    float se = 0.0f;
+    if (m > -INFINITY) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) se += col + k < N ? expf(l[k] - m) : 0.0f;
+    }
+    const float pm = __shfl_xor(m, 1, 64), ps = __shfl_xor(se, 1, 64);
+    const float mm = __builtin_fmaxf(m, pm);
+    float ss = 0.0f;
+    if (mm > -INFINITY) {
+      if (m > -INFINITY) ss += se * expf(m - mm);
+      if (pm > -INFINITY) ss += ps * expf(pm - mm);
+    }
+    if (row >= M) return;
+    if ((lane & 1) == 0 && col < N) {
+      part_m[(long)(col >> 5) * M + row] = mm;
+      part_s[(long)(col >> 5) * M + row] = ss;
+    }
+    if (ce_row_valid(row, M, time, targets, ignore_id)) {
+      const long t = (long)targets[row + 1] - col;
+      if (t >= 0 && t < 16 && col + t < N) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+          if (k == t) tgt[row] = l[k];
+      }
+    }
+  }
 };
 
 struct EpiCeGrad {
@@ -126,6 +174,56 @@ struct EpiCeGrad {
         const int tile_row = row0 + i * 32;
         if (lane < 32 && colok && tile_row < M) part_bias[(long)(tile_row / 32) * vocab + vcol] = csum;
       }
+  }
+  // Streamed-LDS kernels: gradient for 16 columns of one row, then the block's
+  // column sums over its 32 rows from the LDS block buffer (fixed order).
+  __device__ void row16(int row, int col, float (&v)[16], int lane, int M, int N, float* buf,
+                        int brow, int bcol) {
+    const bool rok = row < M;
+    const bool valid = rok && ce_row_valid(row, M, time, targets, ignore_id);
+    const bool full = col + 16 <= N && N % 8 == 0;
+    float g[16];
+    if (valid) {
+      float sc[16], bi[16];
+      lds::get16h(scale, col, N, full && lds::al16(scale), sc);
+      if (bias) {
+        lds::get16h(bias, col, N, full && lds::al16(bias), bi);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) bi[k] = 0.0f;
+      }
+      const float ls = lse[row];
+      const long t = (long)targets[row + 1] - (col_base + col);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const float p = expf(bi[k] + sc[k] * v[k] - ls);
+        g[k] = col + k < N ? (k == t ? p - 1.0f : p) : 0.0f;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) g[k] = 0.0f;
+    }
+    if (rok) {
+      const long idx = (long)row * N + col;
+      if (full && lds::al16(gy16)) {
+        lds::store16h(gy16 + idx, g);
+      } else {
+        for (int k = 0; k < 16 && col + k < N; ++k)
+          gy16[idx + k] = __builtin_bit_cast(uint16_t, (half_t)g[k]);
+      }
+    }
+    // g over the block's 32 rows -> per-column sums (rows past M hold 0)
+    float* rowp = buf + (lane >> 1) * lds::kBufPitch + (lane & 1) * 16;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) rowp[k] = g[k];
+    lds::lds_fence();
+    if (lane < 32) {
+      float cs = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 32; ++r) cs += buf[r * lds::kBufPitch + lane];
+      if (bcol + lane < N && brow < M)
+        part_bias[(long)(brow / 32) * vocab + col_base + bcol + lane] = cs;
+    }
   }
 };
 
@@ -215,7 +313,7 @@ Ws carve(void* base, long rows, long d, long vocab) {
   w.tgt = reinterpret_cast<float*>(take(sizeof(float) * rows));
   w.lse = reinterpret_cast<float*>(take(sizeof(float) * rows));
   w.part_bias = reinterpret_cast<float*>(take(sizeof(float) * cdiv(rows, 32) * vocab));
-  w.gpart = reinterpret_cast<float*>(take(sizeof(float) * vc * d));
+  w.gpart = reinterpret_cast<float*>(take(sizeof(float) * dw_splits(vc, d, rows) * vc * d));
   w.g_scale = reinterpret_cast<float*>(take(sizeof(float) * vocab));
   w.g_bias = reinterpret_cast<float*>(take(sizeof(float) * vocab));
   w.gy16 = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * rows * vc));
@@ -226,6 +324,15 @@ template <class Epi>
 hipError_t logits_gemm(hipStream_t s, const uint16_t* hidden16, long rows, long d,
                        const uint32_t* bits_rows, long ncols, const Epi& epi) {
   // C[rows][ncols] = hidden . S^T ; S rows start at bits_rows (word aligned).
+  hipError_t err = hipSuccess;
+  if (lds::mk_ok(hidden16, d) &&
+      lds::with_lds(rows, ncols, d, 1, &err, [&](auto t) {
+        using T = decltype(t);
+        lds::OpMK<T::bm, T::bk> a{reinterpret_cast<const half_t*>(hidden16), d, (int)rows};
+        lds::OpBits<T::bn, T::bk, false> b{bits_rows, d / 32, (int)ncols, nullptr, 0};
+        return lds::launch_lds<T>(s, a, b, epi, rows, ncols, d, 1);
+      }))
+    return err;
   const bool vec = (reinterpret_cast<uintptr_t>(hidden16) & 15u) == 0 && d % 8 == 0;
   auto run = [&](auto cfg) {
     using T = decltype(cfg);
@@ -250,7 +357,7 @@ size_t head_ce_workspace_bytes(long rows, long d, long vocab) {
   const long vc = chunk_cols(vocab, d);
   auto al = [](size_t b) { return (b + 255) / 256 * 256; };
   return al(4 * nb32 * rows) * 2 + al(4 * rows) * 2 + al(4 * cdiv(rows, 32) * vocab) +
-         al(4 * vc * d) + al(4 * vocab) * 2 + al(2 * rows * vc) + 256;
+         al(4 * dw_splits(vc, d, rows) * vc * d) + al(4 * vocab) * 2 + al(2 * rows * vc) + 256;
 }
 
 hipError_t head_ce(hipStream_t s, const HeadCe& h, void* workspace) {
@@ -287,12 +394,13 @@ hipError_t head_ce(hipStream_t s, const HeadCe& h, void* workspace) {
                                       h.g_hidden, gscale, ci > 0)) != hipSuccess)
       return e;
     // G_chunk = gy_chunk^T . hidden, then the latent step for these head rows
+    const int sp = dw_splits(vc, d, rows);  // the workspace holds this many [vc][d] partials
     if ((e = packed_weight_grad_partials(s, GradIn{nullptr, nullptr}, w.gy16, h.hidden16, rows, d,
-                                         n, 1, w.gpart)) != hipSuccess)
+                                         n, sp, w.gpart)) != hipSuccess)
       return e;
     PackedFinish f;
     f.part = w.gpart;
-    f.splits = 1;
+    f.splits = sp;
     f.out = n;
     f.in = d;
     f.scale = h.scale + c0;

@@ -69,7 +69,7 @@ struct ullis_hip_heron {
   uint16_t *ln16 = nullptr, *q16 = nullptr, *k16 = nullptr, *v16 = nullptr;
   uint16_t *y16 = nullptr, *ln2_16 = nullptr, *shifted16 = nullptr;
   uint8_t* idx_rm = nullptr;
-  uint16_t *key16 = nullptr, *relu2_16 = nullptr, *gk16 = nullptr;
+  uint16_t *key16 = nullptr, *relu2_16 = nullptr, *gk16 = nullptr, *gx16 = nullptr;
   float *g_x = nullptr, *g_a = nullptr, *g_b = nullptr;
   float *gpart = nullptr, *part = nullptr, *vec = nullptr, *slots = nullptr, *stats = nullptr;
   float* row_loss = nullptr;
@@ -250,6 +250,7 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
   add(2ul * nf * L);         // key16
   add(2ul * nf * L);         // relu2_16
   add(2ul * nf);             // gk16
+  add(2ul * nd);             // gx16
   add(4ul * nd * 3);         // g_x g_a g_b
   add(4ul * gpart);
   add(4ul * part);
@@ -279,6 +280,7 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
   h->key16 = cv.take<uint16_t>(nf * L);
   h->relu2_16 = cv.take<uint16_t>(nf * L);
   h->gk16 = cv.take<uint16_t>(nf);
+  h->gx16 = cv.take<uint16_t>(nd);
   h->g_x = cv.take<float>(nd);
   h->g_a = cv.take<float>(nd);
   h->g_b = cv.take<float>(nd);
@@ -469,6 +471,7 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
   STEP(layer_norm_param_finish(s, h->part, nb, D, nullptr, nullptr, lr, h->ln_out.w,
                                h->ln_out.w_res, h->ln_out.b, h->ln_out.b_res),
        "ln_out step");
+  STEP(scale_to_f16(s, h->g_x, nd, h->slots + L, h->gx16), "g_x fp16");
 
   // ------------------------------------------------------------ backward
   for (long l = L - 1; l >= 0; --l) {
@@ -483,9 +486,11 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
 
     // CMix backward_update (src/model.rs:1145-1177)
     PROBED(ULLIS_HIP_PROBE_VALUE_INPUT_GRAD,
-           fp16_backward_input(s, GradIn{h->g_x, slot_in}, R, F, D, b.value, nullptr, key, h->gk16),
+           fp16_backward_input(s, GradIn{h->g_x, slot_in, h->gx16}, R, F, D, b.value, nullptr, key,
+                               h->gk16),
            "value input grad + relu2 bwd");
-    STEP(fp16_weight_grad_partials(s, GradIn{h->g_x, slot_in}, r2, R, F, D, h->splits_value,
+    STEP(fp16_weight_grad_partials(s, GradIn{h->g_x, slot_in, h->gx16}, r2, R, F, D,
+                                   h->splits_value,
                                    h->gpart),
          "value weight grad");
     STEP(fp16_weight_finish(s, h->gpart, h->splits_value, D, F, slot_in, lr, b.value, b.value_res,
@@ -531,14 +536,19 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
     STEP(layer_norm_param_finish(s, h->part, nb, D, nullptr, nullptr, lr, b.ln2.w, b.ln2.w_res,
                                  b.ln2.b, b.ln2.b_res),
          "ln2 step");
+    // O bias gradient (column sums of g_x) and the fp16 copy of g_x for the
+    // O GEMMs here and the CMix GEMMs of the block below.
+    STEP(column_sum_partials(s, h->g_x, nullptr, R, D, h->part, &nb, h->gx16, slot_mid),
+         "o g_bias + g_x fp16");
+    STEP(vector_finish(s, h->part, nb, D, nullptr, lr, b.o.bias, b.o.bias_res), "o bias step");
 
     // ROSA O stop-grad backward (src/model.rs:1491-1522)
-    STEP(packed_backward_input(s, GradIn{h->g_x, slot_mid}, nullptr, R, D, D, b.o.bits_t,
+    STEP(packed_backward_input(s, GradIn{h->g_x, slot_mid, h->gx16}, nullptr, R, D, D, b.o.bits_t,
                                b.o.scale, h->g_a, nullptr, 0),
          "o input grad");
     STEP(column_sum_partials(s, h->g_a, h->idx_rm + l * nd, R, D, h->part, &nb), "g_e");
     STEP(vector_finish(s, h->part, nb, D, nullptr, lr, b.e, b.e_res), "e step");
-    STEP(packed_weight_grad_partials(s, GradIn{h->g_x, slot_mid}, nullptr, h->y16 + l * nd, R, D,
+    STEP(packed_weight_grad_partials(s, GradIn{h->g_x, slot_mid, h->gx16}, nullptr, h->y16 + l * nd, R, D,
                                      D, h->splits_o, h->gpart),
          "o weight grad");
     {
@@ -559,8 +569,6 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
       f.g_w = nullptr;
       STEP(packed_weight_finish(s, f), "o latent step");
     }
-    STEP(column_sum_partials(s, h->g_x, nullptr, R, D, h->part, &nb), "o g_bias");
-    STEP(vector_finish(s, h->part, nb, D, nullptr, lr, b.o.bias, b.o.bias_res), "o bias step");
     STEP(clipped_sgd(s, b.o.scale, b.o.scale_res, h->vec, D, lr), "o scale step");
     STEP(pack_latent_bits(s, b.o.latent, D, D, b.o.bits, b.o.bits_t), "o repack");
 

@@ -13,6 +13,7 @@
 #include <type_traits>
 
 #include "gemm.hpp"
+#include "gemm_lds.hpp"
 #include "ops.hpp"
 
 namespace ullis {
@@ -103,6 +104,73 @@ struct EpiPackedFwd {
         }
       }
   }
+  // Streamed-LDS kernels: 16 consecutive columns of one row (lds::epilogue_rows).
+  __device__ void row16(int row, int col, float (&v)[16], int lane, int M, int N, float*, int,
+                        int) {
+    const bool rok = row < M;
+    const bool full = col + 16 <= N && N % 8 == 0;
+    float sc[16], bi[16];
+    lds::get16h(scale, col, N, full && lds::al16(scale), sc);
+    if (bias) {
+      lds::get16h(bias, col, N, full && lds::al16(bias), bi);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) bi[k] = 0.0f;
+    }
+    float y[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) y[k] = bi[k] + sc[k] * v[k];
+    if constexpr ((OUT & kOutBits) != 0) {
+      // out % 32 == 0: lanes 2r and 2r+1 hold the two halves of one word
+      uint32_t m = 0;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) m |= (uint32_t)(rok && col + k < N && y[k] > 0.0f) << k;
+      const uint32_t other = (uint32_t)__shfl_xor((int)m, 1, 64);
+      if (rok && (lane & 1) == 0 && col < N)
+        o.sign_bits[((long)row * N + col) >> 5] = m | (other << 16);
+    }
+    if (!rok) return;
+    const long idx = (long)row * N + col;
+    if constexpr ((OUT & kOutY32) != 0) {
+      float z[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) z[k] = y[k];
+      if (full && lds::al16(o.y32) && (!((OUT & kOutResid) != 0) || lds::al16(o.resid))) {
+        if constexpr ((OUT & kOutResid) != 0) {
+          float rv[16];
+          lds::load16f(o.resid + idx, rv);
+#pragma unroll
+          for (int k = 0; k < 16; ++k) z[k] = rv[k] + y[k];
+        }
+        lds::store16f(o.y32 + idx, z);
+      } else {
+        for (int k = 0; k < 16 && col + k < N; ++k)
+          o.y32[idx + k] = ((OUT & kOutResid) != 0) ? o.resid[idx + k] + y[k] : y[k];
+      }
+    }
+    if constexpr ((OUT & kOutY16) != 0) {
+      if (full && lds::al16(o.y16)) {
+        lds::store16h(o.y16 + idx, y);
+      } else {
+        for (int k = 0; k < 16 && col + k < N; ++k)
+          o.y16[idx + k] = __builtin_bit_cast(uint16_t, (half_t)y[k]);
+      }
+    }
+    if constexpr ((OUT & kOutRelu2) != 0) {
+      float r2[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const float kk = y[k] > 0.0f ? y[k] : 0.0f;
+        r2[k] = kk * kk;
+      }
+      if (full && lds::al16(o.relu2_16)) {
+        lds::store16h(o.relu2_16 + idx, r2);
+      } else {
+        for (int k = 0; k < 16 && col + k < N; ++k)
+          o.relu2_16[idx + k] = __builtin_bit_cast(uint16_t, (half_t)r2[k]);
+      }
+    }
+  }
 };
 
 struct EpiStoreF32 {
@@ -120,6 +188,22 @@ struct EpiStoreF32 {
       out[idx] = accumulate ? out[idx] + g : g;
     });
   }
+  __device__ void row16(int row, int col, float (&v)[16], int, int M, int N, float*, int, int) {
+    if (row >= M) return;
+    float m = unscale_of(amax);
+    if (mul) m *= *mul;
+    const long idx = (long)row * N + col;
+    if (col + 16 <= N && N % 8 == 0 && lds::al16(out)) {
+      float g[16];
+      if (accumulate) lds::load16f(out + idx, g);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) g[k] = accumulate ? g[k] + v[k] * m : v[k] * m;
+      lds::store16f(out + idx, g);
+    } else {
+      for (int k = 0; k < 16 && col + k < N; ++k)
+        out[idx + k] = accumulate ? out[idx + k] + v[k] * m : v[k] * m;
+    }
+  }
 };
 
 struct EpiF16Fwd {
@@ -133,6 +217,31 @@ struct EpiF16Fwd {
       if (y32) y32[idx] = resid ? resid[idx] + y : y;
       if (y16) y16[idx] = __builtin_bit_cast(uint16_t, (half_t)y);
     });
+  }
+  __device__ void row16(int row, int col, float (&v)[16], int, int M, int N, float*, int, int) {
+    if (row >= M) return;
+    const long idx = (long)row * N + col;
+    const bool full = col + 16 <= N && N % 8 == 0;
+    if (y32) {
+      if (full && lds::al16(y32) && (!resid || lds::al16(resid))) {
+        float z[16];
+        if (resid) lds::load16f(resid + idx, z);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) z[k] = resid ? z[k] + v[k] : v[k];
+        lds::store16f(y32 + idx, z);
+      } else {
+        for (int k = 0; k < 16 && col + k < N; ++k)
+          y32[idx + k] = resid ? resid[idx + k] + v[k] : v[k];
+      }
+    }
+    if (y16) {
+      if (full && lds::al16(y16)) {
+        lds::store16h(y16 + idx, v);
+      } else {
+        for (int k = 0; k < 16 && col + k < N; ++k)
+          y16[idx + k] = __builtin_bit_cast(uint16_t, (half_t)v[k]);
+      }
+    }
   }
 };
 
@@ -149,6 +258,25 @@ struct EpiRelu2Bwd {
       const float gk = k > 0.0f ? 2.0f * k * g : 0.0f;
       gk16[idx] = __builtin_bit_cast(uint16_t, f32_to_f16_sat(gk));
     });
+  }
+  __device__ void row16(int row, int col, float (&v)[16], int, int M, int N, float*, int, int) {
+    if (row >= M) return;
+    const long idx = (long)row * N + col;
+    const bool full = col + 16 <= N && N % 8 == 0 && lds::al16(key16) && lds::al16(gk16);
+    float k[16];
+    lds::get16h(key16 + idx - col, col, N, full, k);
+    float gk[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float t = k[e] > 0.0f ? 2.0f * k[e] * v[e] : 0.0f;
+      gk[e] = __builtin_fminf(__builtin_fmaxf(t, -65504.0f), 65504.0f);  // f32_to_f16_sat
+    }
+    if (full) {
+      lds::store16h(gk16 + idx, gk);
+    } else {
+      for (int e = 0; e < 16 && col + e < N; ++e)
+        gk16[idx + e] = __builtin_bit_cast(uint16_t, (half_t)gk[e]);
+    }
   }
 };
 
@@ -259,6 +387,15 @@ hipError_t packed_forward(hipStream_t s, const void* x, int x_dtype, long rows, 
   auto run = [&](auto out_tag) {
     constexpr int OUT = decltype(out_tag)::value;
     EpiPackedFwd<OUT> epi{scale, bias, o};
+    hipError_t err = hipSuccess;
+    if (x_dtype == kF16 && lds::mk_ok(x, in) &&
+        lds::with_lds(rows, out, in, 1, &err, [&](auto t) {
+          using T = decltype(t);
+          lds::OpMK<T::bm, T::bk> a{static_cast<const half_t*>(x), in, (int)rows};
+          lds::OpBits<T::bn, T::bk, false> b{bits, in / 32, (int)out, nullptr, 0};
+          return lds::launch_lds<T>(s, a, b, epi, rows, out, in, 1);
+        }))
+      return err;
     return with_tile(rows, out, [&](auto t) {
       using T = decltype(t);
       LoadBits<T::bn, T::bk> lb{bits, in, 0, nullptr, bits_aligned(in, 0, nullptr)};
@@ -286,6 +423,16 @@ hipError_t packed_backward_input(hipStream_t s, GradIn gy32, const uint16_t* gy1
                                  long in, long out, const uint32_t* bits_t, const uint16_t* scale,
                                  float* gx, const float* out_mul, int accumulate) {
   EpiStoreF32 epi{gx, gy32.amax, out_mul, accumulate};
+  const uint16_t* g16 = gy16 ? gy16 : gy32.p16;
+  hipError_t err = hipSuccess;
+  if (lds::mk_ok(g16, out) && out <= 8192 &&
+      lds::with_lds(rows, in, out, 1, &err, [&](auto t) {
+        using T = decltype(t);
+        lds::OpMK<T::bm, T::bk> a{reinterpret_cast<const half_t*>(g16), out, (int)rows};
+        lds::OpBits<T::bn, T::bk, true> b{bits_t, out / 32, (int)in, scale, 0};
+        return lds::launch_lds<T>(s, a, b, epi, rows, in, out, 1);
+      }))
+    return err;
   return with_tile(rows, in, [&](auto t) {
     using T = decltype(t);
     LoadBits<T::bn, T::bk, true> lb{bits_t, out, 0, scale, bits_aligned(out, 0, scale)};
@@ -306,6 +453,15 @@ hipError_t packed_backward_input_ex(hipStream_t s, const uint16_t* gy16, long ld
                                     long kofs, const uint16_t* scale, float* gx,
                                     const float* out_mul, int accumulate) {
   EpiStoreF32 epi{gx, nullptr, out_mul, accumulate};
+  hipError_t err = hipSuccess;
+  if (lds::mk_ok(gy16, ldgy) && ldb % 32 == 0 && kofs % 32 == 0 && k_len <= 8192 &&
+      lds::with_lds(rows, in, k_len, 1, &err, [&](auto t) {
+        using T = decltype(t);
+        lds::OpMK<T::bm, T::bk> a{reinterpret_cast<const half_t*>(gy16), ldgy, (int)rows};
+        lds::OpBits<T::bn, T::bk, true> b{bits_t, ldb / 32, (int)in, scale, (int)kofs};
+        return lds::launch_lds<T>(s, a, b, epi, rows, in, k_len, 1);
+      }))
+    return err;
   return with_tile(rows, in, [&](auto t) {
     using T = decltype(t);
     LoadBits<T::bn, T::bk, true> lb{bits_t, ldb, kofs, scale, bits_aligned(ldb, kofs, scale)};
@@ -319,6 +475,16 @@ hipError_t packed_weight_grad_partials(hipStream_t s, GradIn gy32, const uint16_
                                        int splits, float* part) {
   EpiPartial epi{part};
   // G[out][in]: M = out, N = in, K = rows; both operands are row-contiguous.
+  const uint16_t* g16 = gy16 ? gy16 : gy32.p16;
+  hipError_t err = hipSuccess;
+  if (lds::km_ok(g16, out, out) && lds::km_ok(x16, in, in) &&
+      lds::with_lds(out, in, rows, splits, &err, [&](auto t) {
+        using T = decltype(t);
+        lds::OpKM<T::bm, T::bk> a{reinterpret_cast<const half_t*>(g16), out, (int)out};
+        lds::OpKM<T::bn, T::bk> b{reinterpret_cast<const half_t*>(x16), in, (int)in};
+        return lds::launch_lds<T>(s, a, b, epi, out, in, rows, splits);
+      }))
+    return err;
   return with_tile(out, in, [&](auto t) {
     using T = decltype(t);
     LoadF16T<T::bn, T::bk> lb{reinterpret_cast<const half_t*>(x16), in, vec_ok_f16(x16, in)};
@@ -370,6 +536,15 @@ hipError_t transpose_bits(hipStream_t s, const uint32_t* bits, long out, long in
 hipError_t fp16_forward(hipStream_t s, const void* x, int x_dtype, long rows, long in, long out,
                         const uint16_t* w, float* y32, const float* resid, uint16_t* y16) {
   EpiF16Fwd epi{y32, resid, y16};
+  hipError_t err = hipSuccess;
+  if (x_dtype == kF16 && lds::mk_ok(x, in) && lds::mk_ok(w, in) &&
+      lds::with_lds(rows, out, in, 1, &err, [&](auto t) {
+        using T = decltype(t);
+        lds::OpMK<T::bm, T::bk> a{static_cast<const half_t*>(x), in, (int)rows};
+        lds::OpMK<T::bn, T::bk> b{reinterpret_cast<const half_t*>(w), in, (int)out};
+        return lds::launch_lds<T>(s, a, b, epi, rows, out, in, 1);
+      }))
+    return err;
   return with_tile(rows, out, [&](auto t) {
     using T = decltype(t);
     LoadF16K<T::bn, T::bk> lb{reinterpret_cast<const half_t*>(w), in, vec_ok_f16(w, in)};
@@ -386,6 +561,16 @@ hipError_t fp16_backward_input(hipStream_t s, GradIn gy32, long rows, long in, l
                                const uint16_t* w, float* gx, const uint16_t* key16,
                                uint16_t* gk16) {
   // gX[rows][in] = gY[rows][out] . W[out][in]: B(n = i, k = o) = W[o*in + i].
+  hipError_t err = hipSuccess;
+  if (lds::mk_ok(gy32.p16, out) && lds::km_ok(w, in, in) &&
+      lds::with_lds(rows, in, out, 1, &err, [&](auto t) {
+        using T = decltype(t);
+        lds::OpMK<T::bm, T::bk> a{reinterpret_cast<const half_t*>(gy32.p16), out, (int)rows};
+        lds::OpKM<T::bn, T::bk> b{reinterpret_cast<const half_t*>(w), in, (int)in};
+        if (gk16) return lds::launch_lds<T>(s, a, b, EpiRelu2Bwd{key16, gk16}, rows, in, out, 1);
+        return lds::launch_lds<T>(s, a, b, EpiStoreF32{gx, gy32.amax, nullptr, 0}, rows, in, out, 1);
+      }, 240))
+    return err;
   return with_tile(rows, in, [&](auto t) {
     using T = decltype(t);
     LoadF32K<T::bm, T::bk> la{gy32.p, out, vec_ok_f32(gy32.p, out), gy32.amax, 1.0f};

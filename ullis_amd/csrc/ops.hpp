@@ -17,6 +17,9 @@ inline long cdiv(long a, long b) { return (a + b - 1) / b; }
 struct GradIn {
   const float* p;
   const float* amax;
+  // Optional fp16 copy of p already multiplied by grad_scale_from_amax(*amax)
+  // (f32_to_f16_sat); GEMMs that can stream fp16 straight to LDS use it.
+  const uint16_t* p16 = nullptr;
 };
 
 // ------------------------------------------------------------ packed linear
@@ -146,7 +149,13 @@ inline long column_partial_blocks(long rows) { return cdiv(rows, 16); }
 // Column sums of v[rows][ch] (times +-1 from idx when idx != null, i.e.
 // sum g_y * (2*idx - 1)) into part[nblk][ch].
 hipError_t column_sum_partials(hipStream_t s, const float* v, const uint8_t* idx, long rows,
-                               long ch, float* part, int* nblk_out);
+                               long ch, float* part, int* nblk_out, uint16_t* out16 = nullptr,
+                               const float* amax = nullptr);
+// out16 = f16_sat(v * grad_scale_from_amax(*amax)): the fp16 operand form of a
+// scaled fp32 gradient (GradIn::p16). column_sum_partials writes the same
+// copy when out16 / amax are given.
+hipError_t scale_to_f16(hipStream_t s, const float* v, long n, const float* amax,
+                        uint16_t* out16);
 // Sums part[nblk][ch] -> out (optional) and optional clipped SGD with lr.
 hipError_t vector_finish(hipStream_t s, const float* part, int nblk, long ch, float* out,
                          float lr, uint16_t* values, float* residual);
