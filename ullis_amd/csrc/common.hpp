@@ -114,10 +114,14 @@ __device__ __forceinline__ float halfwave_sum(float v) {
 
 // Non-negative floats order like their bit patterns, so a u32 atomicMax on the
 // bits is an exact, order-independent max.
+// The slot only grows, so a value not above a (possibly stale) read of it
+// cannot change it: skipping those atomics keeps same-address contention low.
 __device__ __forceinline__ void atomic_amax(float* slot, float v) {
   v = __builtin_fabsf(v);
   if (!(v >= 0.0f)) v = __builtin_inff();  // NaN: poison the scale deliberately
-  atomicMax(reinterpret_cast<unsigned int*>(slot), __float_as_uint(v));
+  unsigned int* p = reinterpret_cast<unsigned int*>(slot);
+  if (__float_as_uint(v) > __atomic_load_n(p, __ATOMIC_RELAXED))
+    atomicMax(p, __float_as_uint(v));
 }
 
 // Row/column of accumulator register r of a 32x32x16 MFMA tile held by `lane`:

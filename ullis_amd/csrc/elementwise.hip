@@ -96,6 +96,126 @@ __global__ void time_shift_mix_kernel(const uint16_t* x16, long rows, long time,
   }
 }
 
+// Vector form: 8 channels per thread, 32-bit index math (rows * ch < 2^31,
+// ch % 8 == 0, 16-byte aligned rows).
+__device__ __forceinline__ void mix8_one(const half8& x, const half8& p, const uint16_t* mix,
+                                         uint16_t* out, int c, long idx) {
+  const half8 m = *reinterpret_cast<const half8*>(mix + c);
+  half8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float xt = (float)x[e];
+    const float xx = (float)p[e] - xt;  // p = 0 at t == 0: xx = -x
+    o[e] = (half_t)(xt + xx * (float)m[e]);
+  }
+  *reinterpret_cast<half8*>(out + idx) = o;
+}
+
+__global__ void time_shift_mix8_kernel(const uint16_t* x16, int rows, int time, int ch,
+                                       const uint16_t* mix0, uint16_t* out0,
+                                       const uint16_t* mix1, uint16_t* out1,
+                                       const uint16_t* mix2, uint16_t* out2) {
+  const int g = blockIdx.x * blockDim.x + threadIdx.x;
+  const int gpr = ch >> 3;
+  if (g >= rows * gpr) return;
+  const int row = g / gpr;
+  const int c = (g - row * gpr) * 8;
+  const int t = row % time;
+  const long idx = (long)row * ch + c;
+  const half8 x = *reinterpret_cast<const half8*>(x16 + idx);
+  half8 p = {};
+  if (t > 0) p = *reinterpret_cast<const half8*>(x16 + idx - ch);
+  if (out0) mix8_one(x, p, mix0, out0, c, idx);
+  if (out1) mix8_one(x, p, mix1, out1, c, idx);
+  if (out2) mix8_one(x, p, mix2, out2, c, idx);
+}
+
+// Column-reduction blocks: 16 rows x 64 channels, 4 channels per thread; the
+// per-column partial of the block's rows is summed in row order through LDS.
+constexpr int kColBlockCh = 64;
+
+__device__ __forceinline__ void col_block_reduce(float (&red)[16][kColBlockCh], const float (&v)[4],
+                                                 int tx, int ty, long c, long ch, float* dst) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) red[ty][tx * 4 + e] = v[e];
+  __syncthreads();
+  if (threadIdx.x < kColBlockCh) {
+    float s = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s += red[r][threadIdx.x];
+    const long cc = (long)blockIdx.x * kColBlockCh + threadIdx.x;
+    if (cc < ch) dst[cc] = s;
+  }
+  (void)c;
+}
+
+// grid (ch / 64, ceil(rows / 16)), 256 threads; ch % 4 == 0, aligned rows.
+__global__ __launch_bounds__(256) void time_shift_mix_bwd4_kernel(
+    const float* g_s, const uint16_t* x16, const uint16_t* mix, int rows, int time, int ch,
+    float* g_x, float* part) {
+  __shared__ float red[16][kColBlockCh];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const long c = (long)blockIdx.x * kColBlockCh + tx * 4;
+  const int row = blockIdx.y * 16 + ty;
+  float gm[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (row < rows && c < ch) {
+    const int t = row % time;
+    const long idx = (long)row * ch + c;
+    const floatx4 gs = *reinterpret_cast<const floatx4*>(g_s + idx);
+    const half4 x = *reinterpret_cast<const half4*>(x16 + idx);
+    half4 p = {};
+    if (t > 0) p = *reinterpret_cast<const half4*>(x16 + idx - ch);
+    floatx4 gn = {};
+    const bool has_next = t + 1 < time;
+    if (has_next) gn = *reinterpret_cast<const floatx4*>(g_s + idx + ch);
+    const half4 m = *reinterpret_cast<const half4*>(mix + c);
+    floatx4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float xt = (float)x[e];
+      const float xx = (t == 0 ? 0.0f : (float)p[e]) - xt;
+      const float mm = (float)m[e];
+      gm[e] = gs[e] * xx;
+      float gx = gs[e] - gs[e] * mm;
+      if (has_next) gx = gx + gn[e] * mm;
+      o[e] = gx;
+    }
+    *reinterpret_cast<floatx4*>(g_x + idx) = o;
+  }
+  col_block_reduce(red, gm, tx, ty, c, ch, part + (long)blockIdx.y * ch);
+}
+
+// grid (ch / 64, ceil(rows / 16)), 256 threads; ch % 4 == 0, aligned rows.
+__global__ __launch_bounds__(256) void column_sum4_kernel(const float* v, const uint8_t* idx,
+                                                          int rows, int ch, float* part,
+                                                          uint16_t* out16, const float* amax) {
+  __shared__ float red[16][kColBlockCh];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const long c = (long)blockIdx.x * kColBlockCh + tx * 4;
+  const int row = blockIdx.y * 16 + ty;
+  float sv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (row < rows && c < ch) {
+    const long i = (long)row * ch + c;
+    const floatx4 x = *reinterpret_cast<const floatx4*>(v + i);
+    if (idx) {
+      const uint32_t b = *reinterpret_cast<const uint32_t*>(idx + i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sv[e] = x[e] * (2.0f * (float)((b >> (8 * e)) & 0xFFu) - 1.0f);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sv[e] = x[e];
+    }
+    if (out16) {
+      const float sc = grad_scale_from_amax(*amax);
+      half4 h;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) h[e] = f32_to_f16_sat(x[e] * sc);
+      *reinterpret_cast<half4*>(out16 + i) = h;
+    }
+  }
+  col_block_reduce(red, sv, tx, ty, c, ch, part + (long)blockIdx.y * ch);
+}
+
 // grid (ceil(ch/256), ceil(rows/64)); thread = one channel over a 64-row chunk.
 __global__ void time_shift_mix_bwd_kernel(const float* g_s, const uint16_t* x16,
                                           const uint16_t* mix, long rows, long time, long ch,
@@ -153,21 +273,21 @@ __global__ void scale_to_f16_kernel(const float* v, long n, const float* amax, u
   }
 }
 
-// Sums part[nblk][ncols] over nblk: 64 columns per block, 16 partial subsets
+// Sums part[nblk][ncols] over nblk: 16 columns per block, 64 partial subsets
 // per column summed in a fixed order (strided, then an LDS tree), so the result
 // does not depend on scheduling. Columns < split go to target a, the rest to b.
 __global__ __launch_bounds__(1024) void partial_reduce_kernel(const float* part, int nblk,
                                                               long ncols, long split, VecTarget a,
                                                               VecTarget b) {
-  __shared__ float red[16][64];
-  const int lc = threadIdx.x & 63, sub = threadIdx.x >> 6;
-  const long col = (long)blockIdx.x * 64 + lc;
+  __shared__ float red[64][16];
+  const int lc = threadIdx.x & 15, sub = threadIdx.x >> 4;
+  const long col = (long)blockIdx.x * 16 + lc;
   float s = 0.0f;
   if (col < ncols)
-    for (int k = sub; k < nblk; k += 16) s += part[(long)k * ncols + col];
+    for (int k = sub; k < nblk; k += 64) s += part[(long)k * ncols + col];
   red[sub][lc] = s;
   __syncthreads();
-  for (int st = 8; st > 0; st >>= 1) {
+  for (int st = 32; st > 0; st >>= 1) {
     if (sub < st) red[sub][lc] += red[sub + st][lc];
     __syncthreads();
   }
@@ -196,7 +316,46 @@ __global__ void rosa_expand_kernel(const uint8_t* idx_cm, const uint16_t* e, lon
   if (idx_rm) idx_rm[i] = bit;
 }
 
+// Channel-major [B][C][T] bits -> row-major [B*T][C] through a 64 x 64 LDS
+// tile (coalesced 16-byte reads along T and writes along C).
+// grid (T / 64, C / 64, B); requires T % 64 == 0, C % 64 == 0.
+__global__ __launch_bounds__(256) void rosa_expand_tile_kernel(const uint8_t* idx_cm,
+                                                               const uint16_t* e, int time, int ch,
+                                                               uint16_t* y16, uint8_t* idx_rm) {
+  __shared__ uint8_t tile[64][64 + 16];
+  const int t0 = blockIdx.x * 64, c0 = blockIdx.y * 64, b = blockIdx.z;
+  {
+    const int cl = threadIdx.x >> 2, tl = (threadIdx.x & 3) * 16;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(
+        idx_cm + ((long)b * ch + c0 + cl) * time + t0 + tl);
+    *reinterpret_cast<u32x4*>(&tile[cl][tl]) = v;
+  }
+  __syncthreads();
+  const int tl = threadIdx.x >> 2, cl = (threadIdx.x & 3) * 16;
+  const long row = (long)b * time + t0 + tl;
+  uint8_t bits[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) bits[k] = tile[cl + k][tl];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const half8 ev = *reinterpret_cast<const half8*>(e + c0 + cl + 8 * q);
+    half8 y;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) y[k] = (half_t)((2.0f * (float)bits[8 * q + k] - 1.0f) * (float)ev[k]);
+    *reinterpret_cast<half8*>(y16 + row * ch + c0 + cl + 8 * q) = y;
+  }
+  if (idx_rm) {
+    u32x4 w;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      w[q] = (uint32_t)bits[4 * q] | ((uint32_t)bits[4 * q + 1] << 8) |
+             ((uint32_t)bits[4 * q + 2] << 16) | ((uint32_t)bits[4 * q + 3] << 24);
+    *reinterpret_cast<u32x4*>(idx_rm + row * ch + c0 + cl) = w;
+  }
+}
+
 inline dim3 grid1d(long n, int threads = 256) { return dim3((unsigned)cdiv(n, threads)); }
+inline bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
 
@@ -256,6 +415,12 @@ hipError_t time_shift_mix(hipStream_t s, const uint16_t* x16, long rows, long ti
                           const uint16_t* mix0, uint16_t* out0, const uint16_t* mix1,
                           uint16_t* out1, const uint16_t* mix2, uint16_t* out2) {
   if (rows <= 0 || ch <= 0 || time <= 0) return hipSuccess;
+  if (ch % 8 == 0 && rows * ch < (1L << 31) && a16(x16) && (!out0 || (a16(out0) && a16(mix0))) &&
+      (!out1 || (a16(out1) && a16(mix1))) && (!out2 || (a16(out2) && a16(mix2)))) {
+    launch(time_shift_mix8_kernel, grid1d(rows * ch / 8), dim3(256), 0, s, x16, (int)rows,
+           (int)time, (int)ch, mix0, out0, mix1, out1, mix2, out2);
+    return hipGetLastError();
+  }
   const int group = ch % 8 == 0 ? 8 : 1;
   const long n = rows * (ch / group);
   launch(time_shift_mix_kernel, grid1d(n), dim3(256), 0, s, x16, rows, time, ch, mix0,
@@ -269,6 +434,12 @@ hipError_t time_shift_mix_backward(hipStream_t s, const float* g_shifted, const 
   const long nblk = cdiv(rows, kColChunkRows);
   if (nblk_out) *nblk_out = (int)nblk;
   if (rows <= 0 || ch <= 0) return hipSuccess;
+  if (ch % 4 == 0 && rows * ch < (1L << 31) && a16(g_shifted) && a16(g_x) &&
+      (reinterpret_cast<uintptr_t>(x16) & 7u) == 0 && (reinterpret_cast<uintptr_t>(mix) & 7u) == 0) {
+    launch(time_shift_mix_bwd4_kernel, dim3((unsigned)cdiv(ch, kColBlockCh), (unsigned)nblk),
+           dim3(256), 0, s, g_shifted, x16, mix, (int)rows, (int)time, (int)ch, g_x, part);
+    return hipGetLastError();
+  }
   launch(time_shift_mix_bwd_kernel, dim3((unsigned)cdiv(ch, 256), (unsigned)nblk),
                      dim3(256), 0, s, g_shifted, x16, mix, rows, time, ch, g_x, part);
   return hipGetLastError();
@@ -281,6 +452,13 @@ hipError_t column_sum_partials(hipStream_t s, const float* v, const uint8_t* idx
   if (nblk_out) *nblk_out = (int)nblk;
   if (rows <= 0 || ch <= 0) return hipSuccess;
   if (out16 && !amax) return hipErrorInvalidValue;
+  if (ch % 4 == 0 && rows * ch < (1L << 31) && a16(v) &&
+      (reinterpret_cast<uintptr_t>(idx) & 3u) == 0 &&
+      (reinterpret_cast<uintptr_t>(out16) & 7u) == 0) {
+    launch(column_sum4_kernel, dim3((unsigned)cdiv(ch, kColBlockCh), (unsigned)nblk), dim3(256), 0,
+           s, v, idx, (int)rows, (int)ch, part, out16, amax);
+    return hipGetLastError();
+  }
   launch(column_sum_kernel, dim3((unsigned)cdiv(ch, 256), (unsigned)nblk), dim3(256), 0, s, v,
          idx, rows, ch, part, out16, amax);
   return hipGetLastError();
@@ -299,8 +477,8 @@ hipError_t scale_to_f16(hipStream_t s, const float* v, long n, const float* amax
 hipError_t partial_reduce(hipStream_t s, const float* part, int nblk, long ncols, long split,
                           const VecTarget& a, const VecTarget& b) {
   if (ncols <= 0) return hipSuccess;
-  launch(partial_reduce_kernel, dim3((unsigned)cdiv(ncols, 64)), dim3(1024), 0, s,
-                     part, nblk, ncols, split, a, b);
+  launch(partial_reduce_kernel, dim3((unsigned)cdiv(ncols, 16)), dim3(1024), 0, s, part, nblk,
+         ncols, split, a, b);
   return hipGetLastError();
 }
 
@@ -314,6 +492,12 @@ hipError_t rosa_expand(hipStream_t s, const uint8_t* idx_cm, const uint16_t* e, 
                        long time, long ch, uint16_t* y16, uint8_t* idx_rm) {
   const long n = batch * time * ch;
   if (n <= 0) return hipSuccess;
+  if (time % 64 == 0 && ch % 64 == 0 && time * ch < (1L << 31) && a16(idx_cm) && a16(e) &&
+      a16(y16) && (!idx_rm || a16(idx_rm))) {
+    launch(rosa_expand_tile_kernel, dim3((unsigned)(time / 64), (unsigned)(ch / 64), (unsigned)batch),
+           dim3(256), 0, s, idx_cm, e, (int)time, (int)ch, y16, idx_rm);
+    return hipGetLastError();
+  }
   launch(rosa_expand_kernel, grid1d(n), dim3(256), 0, s, idx_cm, e, batch, time, ch,
                      y16, idx_rm);
   return hipGetLastError();

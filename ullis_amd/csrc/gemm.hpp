@@ -607,23 +607,11 @@ struct EpiPartial {
 // Tile configurations: 128x128 tiles (BK 32, 2 register stages: 16 MFMAs per
 // wave per step already cover a load, and a third stage spills) when they
 // alone give about one block per CU, else 64x64 tiles (BK 64, 3 stages).
-#ifndef ULLIS_XL_BK
-#define ULLIS_XL_BK 32
-#endif
-#ifndef ULLIS_XL_S
-#define ULLIS_XL_S 2
-#endif
-#ifndef ULLIS_XS_BK
-#define ULLIS_XS_BK 64
-#endif
-#ifndef ULLIS_XS_S
-#define ULLIS_XS_S 3
-#endif
 struct CfgLarge {
-  static constexpr int bm = 128, bn = 128, bk = ULLIS_XL_BK, stages = ULLIS_XL_S;
+  static constexpr int bm = 128, bn = 128, bk = 32, stages = 2;
 };
 struct CfgSmall {
-  static constexpr int bm = 64, bn = 64, bk = ULLIS_XS_BK, stages = ULLIS_XS_S;
+  static constexpr int bm = 64, bn = 64, bk = 64, stages = 3;
 };
 
 }  // namespace ullis

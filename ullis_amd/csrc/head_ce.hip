@@ -381,6 +381,8 @@ hipError_t head_ce(hipStream_t s, const HeadCe& h, void* workspace) {
 
   // 3. stream the vocabulary in chunks
   const long vc = chunk_cols(V, d);
+  const bool upd = h.lr > 0.0f;
+  const bool fuse = upd && h.scale_upd && h.bits_new && d % 64 == 0 && h.bits_new == h.bits;
   const float* gscale = h.stats + 2;
   float* g_scale = h.g_scale ? h.g_scale : w.g_scale;
   for (long c0 = 0, ci = 0; c0 < V; c0 += vc, ++ci) {
@@ -413,17 +415,24 @@ hipError_t head_ce(hipStream_t s, const HeadCe& h, void* workspace) {
     f.latent_res = h.lr > 0.0f ? h.latent_res + c0 * d : nullptr;
     f.g_scale = g_scale + c0;
     f.g_w = h.g_w ? h.g_w + c0 * d : nullptr;
+    if (fuse) {
+      // this chunk's rows are not read again in this call except through
+      // bits_t (rebuilt at the end): step their scales and repack them now
+      f.scale_upd = h.scale_upd + c0;
+      f.scale_res = h.scale_res + c0;
+      f.bits_new = h.bits_new + (c0 * d) / 32;
+    }
     if ((e = packed_weight_finish(s, f)) != hipSuccess) return e;
   }
 
   // 4. bias gradient, vector steps, repack
-  const bool upd = h.lr > 0.0f;
   // g_bias = gscale * sum over row tiles; head bias step at 8 lr (src/model.rs:3118-3130)
   VecTarget bias_t{h.g_bias ? h.g_bias : w.g_bias, upd ? h.bias_upd : nullptr, h.bias_res,
                    h.lr * kHeadBiasLrMult, gscale};
   if ((e = partial_reduce(s, w.part_bias, (int)cdiv(rows, 32), V, V, bias_t, bias_t)) !=
       hipSuccess)
     return e;
+  if (fuse) return h.bits_t_new ? transpose_bits(s, h.bits_new, V, d, h.bits_t_new) : hipSuccess;
   if (upd && h.scale_upd) {
     if ((e = clipped_sgd(s, h.scale_upd, h.scale_res, g_scale, V, h.lr)) != hipSuccess) return e;
   }

@@ -375,6 +375,9 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
   const long nd = R * D, nf = R * F;
   const long words = cdiv(nd, 32);
   const float ste = (float)(T - 1);  // binaryconnect_ste_scale(time - 1), src/model.rs:554-556
+  // latent rows of the packed weights are whole 64-weight chunks: the latent
+  // step, scale step and repack run in one kernel per matrix
+  const bool fuse_pack = D % 64 == 0;
   float* rl = row_loss ? row_loss : h->row_loss;
   float* st = stats4 ? stats4 : h->stats;
   uint32_t* qkv = qkv_bits ? qkv_bits : h->qkv;
@@ -520,10 +523,19 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
       f.latent_res = b.key.latent_res;
       f.g_scale = h->vec;
       f.g_w = nullptr;
+      if (fuse_pack) {
+        f.scale_upd = b.key.scale;
+        f.scale_res = b.key.scale_res;
+        f.bits_new = b.key.bits;
+      }
       STEP(packed_weight_finish(s, f), "key latent step");
     }
-    STEP(clipped_sgd(s, b.key.scale, b.key.scale_res, h->vec, F, lr), "key scale step");
-    STEP(pack_latent_bits(s, b.key.latent, F, D, b.key.bits, b.key.bits_t), "key repack");
+    if (fuse_pack) {
+      STEP(transpose_bits(s, b.key.bits, F, D, b.key.bits_t), "key bits_t");
+    } else {
+      STEP(clipped_sgd(s, b.key.scale, b.key.scale_res, h->vec, F, lr), "key scale step");
+      STEP(pack_latent_bits(s, b.key.latent, F, D, b.key.bits, b.key.bits_t), "key repack");
+    }
     STEP(time_shift_mix_backward(s, h->g_a, ln2, b.cx_k, R, T, D, h->g_b, h->part, &nb),
          "mix bwd");
     STEP(vector_finish(s, h->part, nb, D, nullptr, lr, b.cx_k, b.cx_k_res), "x_k step");
@@ -567,10 +579,19 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
       f.latent_res = b.o.latent_res;
       f.g_scale = h->vec;
       f.g_w = nullptr;
+      if (fuse_pack) {
+        f.scale_upd = b.o.scale;
+        f.scale_res = b.o.scale_res;
+        f.bits_new = b.o.bits;
+      }
       STEP(packed_weight_finish(s, f), "o latent step");
     }
-    STEP(clipped_sgd(s, b.o.scale, b.o.scale_res, h->vec, D, lr), "o scale step");
-    STEP(pack_latent_bits(s, b.o.latent, D, D, b.o.bits, b.o.bits_t), "o repack");
+    if (fuse_pack) {
+      STEP(transpose_bits(s, b.o.bits, D, D, b.o.bits_t), "o bits_t");
+    } else {
+      STEP(clipped_sgd(s, b.o.scale, b.o.scale_res, h->vec, D, lr), "o scale step");
+      STEP(pack_latent_bits(s, b.o.latent, D, D, b.o.bits, b.o.bits_t), "o repack");
+    }
 
     if (b.has_ln0) {  // (src/model.rs:2978-2982)
       STEP(layer_norm_backward_rows(s, x_emb, h->g_x, R, D, b.ln0.w, g_emb, 0, nullptr, h->part,

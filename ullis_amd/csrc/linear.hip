@@ -291,6 +291,7 @@ __global__ __launch_bounds__(256) void packed_finish_kernel(PackedFinish f) {
   const float sc = f16_bits_to_f32(f.scale[o]);
   const long wn = f.out * f.in;
   float gs = 0.0f;
+  const int lane = threadIdx.x & 63;
   for (long i = threadIdx.x; i < f.in; i += blockDim.x) {
     const long w = o * f.in + i;
     float G = 0.0f;
@@ -300,7 +301,16 @@ __global__ __launch_bounds__(256) void packed_finish_kernel(PackedFinish f) {
     gs += plus ? G : -G;
     const float gw = sc * G;
     if (f.g_w) f.g_w[w] = gw;
-    if (f.latent) binaryconnect_sgd_one(f.latent[w], f.latent_res[w], gw * f.ste, f.lr);
+    if (f.latent) {
+      binaryconnect_sgd_one(f.latent[w], f.latent_res[w], gw * f.ste, f.lr);
+      if (f.bits_new) {
+        // whole waves cover 64 consecutive weights of row o (in % 64 == 0);
+        // each word of the row is read above before it is rewritten here
+        const unsigned long long m = __ballot(latent_is_plus(f.latent[w]));
+        if (lane == 0) f.bits_new[w >> 5] = (uint32_t)m;
+        if (lane == 32) f.bits_new[w >> 5] = (uint32_t)(m >> 32);
+      }
+    }
   }
   red[threadIdx.x] = gs;
   __syncthreads();
@@ -308,7 +318,10 @@ __global__ __launch_bounds__(256) void packed_finish_kernel(PackedFinish f) {
     if ((int)threadIdx.x < st) red[threadIdx.x] += red[threadIdx.x + st];
     __syncthreads();
   }
-  if (threadIdx.x == 0 && f.g_scale) f.g_scale[o] = red[0];
+  if (threadIdx.x == 0) {
+    if (f.g_scale) f.g_scale[o] = red[0];
+    if (f.scale_upd && f.lr > 0.0f) clipped_sgd_one(f.scale_upd[o], f.scale_res[o], red[0], f.lr);
+  }
 }
 
 __global__ void fp16_finish_kernel(const float* part, int splits, long n, const float* amax,
@@ -499,6 +512,8 @@ hipError_t packed_weight_grad_partials(hipStream_t s, GradIn gy32, const uint16_
 
 hipError_t packed_weight_finish(hipStream_t s, const PackedFinish& f) {
   if (f.out <= 0 || f.in <= 0) return hipSuccess;
+  if (f.bits_new && (f.in % 64 != 0 || !f.latent)) return hipErrorInvalidValue;
+  if (f.scale_upd && !f.scale_res) return hipErrorInvalidValue;
   launch(packed_finish_kernel, dim3((unsigned)f.out), dim3(256), 0, s, f);
   return hipGetLastError();
 }

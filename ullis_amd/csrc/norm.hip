@@ -214,6 +214,115 @@ __global__ __launch_bounds__(256) void ln_bwd_vec_kernel(const float* __restrict
   }
 }
 
+// Backward, one row per wave (4 rows per block), ch % 4 == 0, ch <= 1024: all
+// of a row's loads (x, gy and, when accumulating, the old gx) are issued
+// before the first reduction, and the grid has one wave per row, so the
+// memory latency of every row overlaps. Column partials per block as above.
+template <int NV>
+__global__ __launch_bounds__(256) void ln_bwd_row_kernel(const float* __restrict__ x,
+                                                         const float* __restrict__ gy, long rows,
+                                                         int ch, const uint16_t* __restrict__ w,
+                                                         float* gx, int accumulate, float* amax,
+                                                         float* __restrict__ part) {
+  __shared__ float red[kRowsPerBlock][2][1024];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const long row = (long)blockIdx.x * kRowsPerBlock + wave;
+  const bool live = row < rows;
+  floatx4 v[NV], g[NV], old[NV], wv[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 4;
+    const bool ok = live && c < ch;
+    v[j] = ok ? *reinterpret_cast<const floatx4*>(x + row * ch + c) : (floatx4){};
+    g[j] = ok ? *reinterpret_cast<const floatx4*>(gy + row * ch + c) : (floatx4){};
+    old[j] = ok && accumulate ? *reinterpret_cast<const floatx4*>(gx + row * ch + c) : (floatx4){};
+    const half4 wh = c < ch ? *reinterpret_cast<const half4*>(w + c) : (half4){};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) wv[j][e] = (float)wh[e];
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) s += (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]);
+  const float mean = wave_sum(s) / (float)ch;
+  float q = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 4;
+    if (c < ch) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float d = v[j][e] - mean;
+        q += d * d;
+      }
+    }
+  }
+  const float var = wave_sum(q) / (float)ch;
+  const float inv = 1.0f / __builtin_sqrtf(var + kLayerNormEps);
+  float sd = 0.0f, sdx = 0.0f;
+  floatx4 pw[NV], pb[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float xhat = (v[j][e] - mean) * inv;
+      const float dxhat = g[j][e] * wv[j][e];
+      v[j][e] = xhat;
+      sd += dxhat;
+      sdx += dxhat * xhat;
+      pw[j][e] = g[j][e] * xhat;
+      pb[j][e] = g[j][e];
+    }
+  }
+  const float sum_dxhat = wave_sum(sd);
+  const float sum_dxhat_xhat = wave_sum(sdx);
+  const float inv_n = inv / (float)ch;
+  float local_max = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 4;
+    if (live && c < ch) {
+      floatx4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float dxhat = g[j][e] * wv[j][e];
+        o[e] = inv_n * ((float)ch * dxhat - sum_dxhat - v[j][e] * sum_dxhat_xhat);
+        if (accumulate) o[e] = old[j][e] + o[e];
+        local_max = __builtin_fmaxf(local_max, __builtin_fabsf(o[e]));
+      }
+      *reinterpret_cast<floatx4*>(gx + row * ch + c) = o;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (c < ch) {
+        red[wave][0][c + e] = pw[j][e];
+        red[wave][1][c + e] = pb[j][e];
+      }
+  }
+  __shared__ float wmax[kRowsPerBlock];
+  if (amax) {
+    const float m = wave_max(local_max);
+    if (lane == 0) wmax[wave] = m;
+  }
+  __syncthreads();
+  if (amax && threadIdx.x == 0) {
+    float m = wmax[0];
+#pragma unroll
+    for (int k = 1; k < kRowsPerBlock; ++k) m = __builtin_fmaxf(m, wmax[k]);
+    atomic_amax(amax, m);
+  }
+  for (int c = threadIdx.x; c < ch; c += blockDim.x) {
+    float a = 0.0f, bsum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kRowsPerBlock; ++k) {
+      a += red[k][0][c];
+      bsum += red[k][1][c];
+    }
+    part[((long)blockIdx.x * 2 + 0) * ch + c] = a;
+    part[((long)blockIdx.x * 2 + 1) * ch + c] = bsum;
+  }
+}
+
 // Any ch: one wave per (block, row slot); per-wave partials (block = 1 wave).
 __global__ __launch_bounds__(64) void ln_bwd_any_kernel(const float* x, const float* gy, long rows,
                                                         int ch, const uint16_t* w, float* gx,
@@ -299,8 +408,17 @@ hipError_t layer_norm_forward(hipStream_t s, const float* x, long rows, long ch,
 
 static bool ln_bwd_vec_path(long ch) { return ch % 4 == 0 && ch <= 1024; }
 
+// Blocks of the vector path (one row per wave) and of the any-ch path.
+static bool ln_bwd_row_path(long rows, long ch) { return ln_bwd_vec_path(ch) && rows <= (1L << 20); }
+
 int layer_norm_backward_blocks(long rows) {
-  // Two rows per wave at the heron shape; never more blocks than row slots.
+  // Upper bound over both paths (sizes the partial buffers).
+  long nblk = cdiv(rows, kRowsPerBlock);
+  if (nblk < 256) nblk = 256;
+  return (int)nblk;
+}
+
+static int ln_bwd_blocks_any(long rows) {
   long nblk = cdiv(rows, 2 * kRowsPerBlock);
   if (nblk > 256) nblk = 256;
   if (nblk < 1) nblk = 1;
@@ -314,7 +432,17 @@ hipError_t layer_norm_backward_rows(hipStream_t s, const float* x, const float* 
     if (nblk_out) *nblk_out = 0;
     return hipSuccess;
   }
-  const int nblk = layer_norm_backward_blocks(rows);
+  if (ln_bwd_row_path(rows, ch) && vec_ok(x) && vec_ok(gy) && vec_ok(gx) &&
+      (reinterpret_cast<uintptr_t>(w) & 7u) == 0) {
+    const int nblk = (int)cdiv(rows, kRowsPerBlock);
+    if (nblk_out) *nblk_out = nblk;
+    return by_nv(ch, [&](auto nv) {
+      launch(ln_bwd_row_kernel<decltype(nv)::value>, dim3(nblk), dim3(256), 0, s, x, gy, rows,
+             (int)ch, w, gx, accumulate, amax, part);
+      return hipGetLastError();
+    });
+  }
+  const int nblk = ln_bwd_blocks_any(rows);
   if (nblk_out) *nblk_out = nblk;
   if (ln_bwd_vec_path(ch) && vec_ok(x) && vec_ok(gy) && vec_ok(gx)) {
     return by_nv(ch, [&](auto nv) {

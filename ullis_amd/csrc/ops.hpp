@@ -68,6 +68,12 @@ struct PackedFinish {
   float* latent_res;
   float* g_scale;          // may be null
   float* g_w;              // may be null
+  // Fused tail of the update (optional, with latent set): clipped SGD of
+  // scale[o] at lr with g_scale[o] (scale_upd/scale_res), and the repack of
+  // the updated latent rows into bits_new (requires in % 64 == 0).
+  uint16_t* scale_upd = nullptr;
+  float* scale_res = nullptr;
+  uint32_t* bits_new = nullptr;
 };
 hipError_t packed_weight_finish(hipStream_t s, const PackedFinish& f);
 
