@@ -15,6 +15,7 @@
 
 #include "common.hpp"
 #include "ops.hpp"
+#include "update.hpp"
 
 namespace ullis {
 
@@ -280,26 +281,7 @@ __global__ __launch_bounds__(1024) void partial_reduce_kernel(const float* part,
                                                               long ncols, long split, VecTarget a,
                                                               VecTarget b) {
   __shared__ float red[64][16];
-  const int lc = threadIdx.x & 15, sub = threadIdx.x >> 4;
-  const long col = (long)blockIdx.x * 16 + lc;
-  float s = 0.0f;
-  if (col < ncols)
-    for (int k = sub; k < nblk; k += 64) s += part[(long)k * ncols + col];
-  red[sub][lc] = s;
-  __syncthreads();
-  for (int st = 32; st > 0; st >>= 1) {
-    if (sub < st) red[sub][lc] += red[sub + st][lc];
-    __syncthreads();
-  }
-  if (sub == 0 && col < ncols) {
-    const bool first = col < split;
-    const VecTarget& t = first ? a : b;
-    const long i = first ? col : col - split;
-    float v = red[0][lc];
-    if (t.mul) v *= *t.mul;
-    if (t.out) t.out[i] = v;
-    if (t.values && t.lr > 0.0f) clipped_sgd_one(t.values[i], t.residual[i], v, t.lr);
-  }
+  vec_reduce_block(part, nblk, ncols, split, a, a.lr, b, b.lr, blockIdx.x, red);
 }
 
 __global__ void rosa_expand_kernel(const uint8_t* idx_cm, const uint16_t* e, long batch, long time,

@@ -315,8 +315,8 @@ __device__ __forceinline__ void get16h(const uint16_t* p, int col, int n, bool v
 }
 
 template <int BM, int BN, int BK, int NS, class OA, class OB, class Epi>
-__global__ __launch_bounds__(256) void gemm_lds_kernel(OA a, OB b, Epi epi, int M, int N, int K,
-                                                       int k_split) {
+__device__ __forceinline__ void gemm_lds_body(const OA& a, const OB& b, Epi& epi, int M, int N,
+                                              int K, int k_split) {
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int STAGE = OA::kBytes + OB::kBytes;
@@ -382,16 +382,120 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(OA a, OB b, Epi epi, int 
                 n0 + wn * WN, lane, M, N);
 }
 
+template <int BM, int BN, int BK, int NS, class OA, class OB, class Epi>
+__global__ __launch_bounds__(256) void gemm_lds_kernel(OA a, OB b, Epi epi, int M, int N, int K,
+                                                       int k_split) {
+  gemm_lds_body<BM, BN, BK, NS>(a, b, epi, M, N, K, k_split);
+}
+
+template <class T, int G>
+struct Group {
+  T v[G];
+};
+
+// G independent problems of one shape in one launch (blockIdx.y = problem).
+template <int BM, int BN, int BK, int NS, class OA, class OB, class Epi, int G>
+__global__ __launch_bounds__(256) void gemm_lds_group_kernel(Group<OA, G> a, Group<OB, G> b,
+                                                             Group<Epi, G> epi, int M, int N,
+                                                             int K, int k_split) {
+  const int g = blockIdx.y;
+  gemm_lds_body<BM, BN, BK, NS>(a.v[g], b.v[g], epi.v[g], M, N, K, k_split);
+}
+
+// K split across the 4 waves of a block: every wave accumulates the whole
+// 64x64 tile (2x2 MFMA blocks, 4 MFMAs per pair of fragment fetches instead of
+// 1) over one 16-wide slice of each BK = 64 stage, and the four partial tiles
+// are summed through LDS in wave order before the epilogue, where wave w owns
+// the 32x32 block (w/2, w%2). Same operands, stages and epilogue interface as
+// gemm_lds_kernel.
+template <int BK, int NS, class OA, class OB, class Epi>
+__global__ __launch_bounds__(256) void gemm_lds_ksplit_kernel(OA a, OB b, Epi epi, int M, int N,
+                                                              int K, int k_split) {
+  constexpr int BM = 64, BN = 64, TM = 2, TN = 2;
+  static_assert(BK == 64, "one 16-wide k slice per wave");
+  constexpr int STAGE = OA::kBytes + OB::kBytes;
+  constexpr int IPS = OA::kInst + OB::kInst;
+  constexpr int RED = 4 * TM * TN * 64 * 16 * 4;  // [block][wave][r][lane] fp32
+  constexpr int RING0 = NS * STAGE > RED ? NS * STAGE : RED;
+  constexpr int RING = RING0 > 4 * kBufFloats * 4 ? RING0 : 4 * kBufFloats * 4;
+  static_assert(NS >= 2 && IPS * (NS - 2) < 64, "pipeline depth");
+  __shared__ __attribute__((aligned(1024))) char smem[RING + OA::kExtra + OB::kExtra];
+  char* extra_a = smem + RING;
+  char* extra_b = extra_a + OA::kExtra;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  int tm, tn;
+  tile_of_block(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int kbeg = blockIdx.z * k_split;
+  const int kend = min(K, kbeg + k_split);
+  const int nk = kend > kbeg ? (kend - kbeg) / BK : 0;
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = (floatx16){};
+
+  a.prepare(extra_a, kbeg, kend);
+  b.prepare(extra_b, kbeg, kend);
+  auto issue = [&](int kt) {
+    char* st = smem + (kt % NS) * STAGE;
+    a.issue(st, m0, kbeg + kt * BK, wave, lane);
+    b.issue(st + OA::kBytes, n0, kbeg + kt * BK, wave, lane);
+  };
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < nk) issue(s);
+  const int ks = wave * 16;
+  for (int kt = 0; kt < nk; ++kt) {
+    wait_stages<IPS, NS - 2>(nk - 1 - kt);
+    if (kt + NS - 1 < nk) issue(kt + NS - 1);
+    const char* st = smem + (kt % NS) * STAGE;
+    const int k0rel = kt * BK;
+    half8 af[TM], bf[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) af[i] = a.frag(st, extra_a, i * 32, ks, lane, k0rel);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bf[j] = b.frag(st + OA::kBytes, extra_b, j * 32, ks, lane, k0rel);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+  }
+  wait_barrier<0>();  // every wave is done reading the ring
+  float* red = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[(((i * TN + j) * 4 + wave) * 16 + r) * 64 + lane] = acc[i][j][r];
+  wait_barrier<0>();
+  floatx16 sum[1][1];
+  sum[0][0] = (floatx16){};
+#pragma unroll
+  for (int v = 0; v < 4; ++v)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sum[0][0][r] += red[((wave * 4 + v) * 16 + r) * 64 + lane];
+  wait_barrier<0>();  // the epilogue buffers reuse the reduction area
+  epilogue_rows(epi, sum, reinterpret_cast<float*>(smem) + wave * kBufFloats,
+                m0 + 32 * (wave >> 1), n0 + 32 * (wave & 1), lane, M, N);
+}
+
 // ------------------------------------------------------------ host dispatch
 // Measured on MI355X for the heron shapes (2048 rows): 64x64 tiles with BK 64
-// and a 2-stage ring run four blocks per CU and beat 128x128 tiles (one block
-// per CU) everywhere except very wide outputs (the vocab head), where 128x128
-// tiles with 4 stages win; more ring stages did not help either.
+// beat 128x128 tiles (one block per CU) everywhere except very wide outputs
+// (the vocab head), where 128x128 tiles win; a 4-stage ring was best inside
+// the train step (2, 3 and 6 stages were slower).
 struct LdsBig {
   static constexpr int bm = 128, bn = 128, bk = 32, ns = 4;
 };
 struct LdsMid {
-  static constexpr int bm = 64, bn = 64, bk = 64, ns = 2;
+  static constexpr int bm = 64, bn = 64, bk = 64, ns = 4;
 };
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -414,6 +518,17 @@ bool with_lds(long M, long N, long K, int splits, hipError_t* err, F&& f, long b
   };
   if (cdiv(M, 128) * cdiv(N, 128) >= big_tiles) return go(LdsBig{});
   return go(LdsMid{});
+}
+
+template <class T, class OA, class OB, class Epi, int G>
+hipError_t launch_lds_group(hipStream_t s, const Group<OA, G>& a, const Group<OB, G>& b,
+                            const Group<Epi, G>& epi, long M, long N, long K) {
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return hipErrorInvalidValue;
+  const long tiles = cdiv(M, T::bm) * cdiv(N, T::bn);
+  const int ks = (int)(cdiv(K, T::bk) * T::bk);
+  launch((gemm_lds_group_kernel<T::bm, T::bn, T::bk, T::ns, OA, OB, Epi, G>),
+         dim3((unsigned)tiles, G, 1), dim3(kThreads), 0, s, a, b, epi, (int)M, (int)N, (int)K, ks);
+  return hipGetLastError();
 }
 
 template <class T, class OA, class OB, class Epi>

@@ -255,7 +255,8 @@ __global__ __launch_bounds__(256) void ce_combine_kernel(const float* part_m, co
 // Single block: n_valid, loss sum (fixed-order tree), mean and gscale.
 __global__ __launch_bounds__(1024) void ce_mean_kernel(const float* row_loss, long rows, long time,
                                                        const uint32_t* targets,
-                                                       uint32_t ignore_id, float* stats) {
+                                                       uint32_t ignore_id, float* stats,
+                                                       float* stats2) {
   __shared__ float ls[1024];
   __shared__ float nv[1024];
   float a = 0.0f, n = 0.0f;
@@ -281,6 +282,12 @@ __global__ __launch_bounds__(1024) void ce_mean_kernel(const float* row_loss, lo
     stats[1] = count;
     stats[2] = (count > 0.0f && time >= 2) ? 1.0f / (float)(time - 1) : 0.0f;  // :49-55
     stats[3] = ls[0];
+    if (stats2) {
+      stats2[0] = stats[0];
+      stats2[1] = stats[1];
+      stats2[2] = stats[2];
+      stats2[3] = stats[3];
+    }
   }
 }
 
@@ -360,6 +367,16 @@ size_t head_ce_workspace_bytes(long rows, long d, long vocab) {
          al(4 * dw_splits(vc, d, rows) * vc * d) + al(4 * vocab) * 2 + al(2 * rows * vc) + 256;
 }
 
+long head_ce_chunk_cols(long vocab, long d) { return chunk_cols(vocab, d); }
+
+int head_ce_splits(long rows, long d, long vocab) {
+  return dw_splits(chunk_cols(vocab, d), d, rows);
+}
+
+float* head_ce_bias_partials(void* workspace, long rows, long d, long vocab) {
+  return carve(workspace, rows, d, vocab).part_bias;
+}
+
 hipError_t head_ce(hipStream_t s, const HeadCe& h, void* workspace) {
   const long rows = h.rows, d = h.d, V = h.vocab;
   if (rows <= 0 || d <= 0 || V <= 0) return hipErrorInvalidValue;
@@ -375,8 +392,8 @@ hipError_t head_ce(hipStream_t s, const HeadCe& h, void* workspace) {
                      w.part_s, nb32, rows, h.time, h.targets, h.ignore_id, w.tgt, w.lse,
                      h.row_loss);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  launch(ce_mean_kernel, dim3(1), dim3(1024), 0, s, h.row_loss, rows, h.time,
-                     h.targets, h.ignore_id, h.stats);
+  launch(ce_mean_kernel, dim3(1), dim3(1024), 0, s, h.row_loss, rows, h.time, h.targets,
+         h.ignore_id, h.stats, h.stats2);
   if ((e = hipGetLastError()) != hipSuccess) return e;
 
   // 3. stream the vocabulary in chunks
@@ -397,9 +414,11 @@ hipError_t head_ce(hipStream_t s, const HeadCe& h, void* workspace) {
       return e;
     // G_chunk = gy_chunk^T . hidden, then the latent step for these head rows
     const int sp = dw_splits(vc, d, rows);  // the workspace holds this many [vc][d] partials
+    float* gp = h.gpart_all ? h.gpart_all + ci * sp * vc * d : w.gpart;
     if ((e = packed_weight_grad_partials(s, GradIn{nullptr, nullptr}, w.gy16, h.hidden16, rows, d,
-                                         n, sp, w.gpart)) != hipSuccess)
+                                         n, sp, gp)) != hipSuccess)
       return e;
+    if (h.gpart_all) continue;  // deferred: the caller runs the update
     PackedFinish f;
     f.part = w.gpart;
     f.splits = sp;
@@ -425,6 +444,7 @@ hipError_t head_ce(hipStream_t s, const HeadCe& h, void* workspace) {
     if ((e = packed_weight_finish(s, f)) != hipSuccess) return e;
   }
 
+  if (h.gpart_all) return hipSuccess;
   // 4. bias gradient, vector steps, repack
   // g_bias = gscale * sum over row tiles; head bias step at 8 lr (src/model.rs:3118-3130)
   VecTarget bias_t{h.g_bias ? h.g_bias : w.g_bias, upd ? h.bias_upd : nullptr, h.bias_res,

@@ -6,16 +6,26 @@
 // Order of operations (and which weights each GEMM sees) follows the
 // reference: per block forward LN0 (block 0) -> LN3 -> time-shift mix3 ->
 // Q/K/V (sign bit-planes for the automaton) -> y = (2 idx - 1) e -> O (+x)
-// -> LN2 -> mix -> key (ReLU^2) -> value (+x); LN_out; head + CE with the head
-// update; LN_out backward; per block in reverse: CMix backward (value input
-// gradient with the pre-update value weights, value step, key input gradient
-// with the pre-update bits, key latent / scale steps, x_k step), LN2
-// backward (+= into g_x), ROSA O stop-grad backward (e step from g_y, O
-// latent / scale / bias steps), LN0 backward at block 0.
+// -> LN2 -> mix -> key (ReLU^2) -> value (+x); LN_out; head + CE; LN_out
+// backward; per block in reverse: CMix backward (value input gradient, value
+// weight gradient, key input and weight gradients, x_k gradient), LN2
+// backward (+= into g_x), ROSA O stop-grad backward (e, O weight and O bias
+// gradients), LN0 backward at block 0.
 // Tapes stay resident in HBM between the forward and the backward.
+//
+// Parameter updates: each tensor is read only by its own layer's forward and
+// backward, and the reference updates it after its last read, so no kernel
+// later in the step reads an updated parameter. Every update is therefore
+// deferred to the end of the step: the gradient partials of each tensor stay
+// in their own buffers and five batched launches (vector steps, fp16 weight
+// steps, packed latent / scale steps with the repack, latent repack where
+// rows are not whole 64-weight chunks, bit transposes) apply them, with the
+// same per-tensor arithmetic as updating each tensor at the reference's
+// update call.
 #include <hip/hip_runtime.h>
 
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/ullis_hip.h"
@@ -71,8 +81,26 @@ struct ullis_hip_heron {
   uint8_t* idx_rm = nullptr;
   uint16_t *key16 = nullptr, *relu2_16 = nullptr, *gk16 = nullptr, *gx16 = nullptr;
   float *g_x = nullptr, *g_a = nullptr, *g_b = nullptr;
-  float *gpart = nullptr, *part = nullptr, *vec = nullptr, *slots = nullptr, *stats = nullptr;
+  float *slots = nullptr, *stats = nullptr;
   float* row_loss = nullptr;
+  // gradient partials, one buffer per tensor, consumed by the end-of-step updates
+  float *gp_value = nullptr, *gp_key = nullptr, *gp_o = nullptr, *gp_head = nullptr;
+  float *pt_mix = nullptr, *pt_ln2 = nullptr, *pt_ob = nullptr, *pt_e = nullptr;
+  float *pt_lnout = nullptr, *pt_ln0 = nullptr;
+  int nb_col = 0, nb_ln = 0;
+  // batched update job tables (device memory) and their grid sizes; the LN0
+  // job is the last vector job so that it can be left out when LN0 backward
+  // took a path with another partial count (unaligned x_emb)
+  void* job_mem = nullptr;
+  const VecJob* vec_jobs = nullptr;
+  const F16Job* f16_jobs = nullptr;
+  const FinishJob* fin_jobs = nullptr;
+  const PackJob* pack_jobs = nullptr;
+  const TransJob* trans_jobs = nullptr;
+  int n_vec = 0, n_f16 = 0, n_fin = 0, n_pack = 0, n_trans = 0;
+  int vec_blocks = 0, f16_blocks = 0, fin_blocks = 0, pack_blocks = 0, trans_blocks = 0;
+  int ln0_job_blocks = 0;  // blocks of the trailing LN0 job (0: none)
+  std::vector<const Packed*> trans_generic;  // bits_t rebuilt by the generic transpose
   uint32_t* qkv = nullptr;
   void* head_ws = nullptr;
   int splits_o = 1, splits_key = 1, splits_value = 1;
@@ -158,6 +186,138 @@ constexpr int kProbeMax = 512;
     }                                                                              \
   } while (0)
 
+// Job tables of the end-of-step updates (every pointer in them is fixed for
+// the life of the trainer), uploaded once.
+int build_update_jobs(ullis_hip_heron* h) {
+  ullis_hip_ctx* c = h->ctx;
+  const long R = h->rows, D = h->D, F = h->F, V = h->V, L = h->L;
+  const float ste = (float)(h->time - 1);  // binaryconnect_ste_scale(time - 1), src/model.rs:554-556
+  const bool fuse_pack = D % 64 == 0;       // whole 64-weight chunks per latent row
+  std::vector<VecJob> vj;
+  std::vector<F16Job> fj;
+  std::vector<FinishJob> pj;
+  std::vector<PackJob> kj;
+  std::vector<TransJob> tj;
+  int vb = 0, fb = 0, pb = 0, kb = 0, tb = 0;
+  auto vec2 = [&](const float* part, int nblk, long ch, bool two, VecTarget a, VecTarget b) {
+    VecJob j{part, nblk, two ? 2 * ch : ch, ch, a, two ? b : a, vb};
+    vb += vec_job_blocks(j.ncols);
+    vj.push_back(j);
+  };
+  auto sgd = [](uint16_t* v, float* r, float mult, const float* mul) {
+    return VecTarget{nullptr, v, r, mult, mul};
+  };
+  auto ln = [&](const Ln& n, const float* part, int nblk) {
+    vec2(part, nblk, D, true, sgd(n.w, n.w_res, 1.0f, nullptr), sgd(n.b, n.b_res, 1.0f, nullptr));
+  };
+  // packed latent / scale steps (+ repack in the finish or as a pack job),
+  // then the bit transpose
+  auto packed = [&](const Packed& k, long row0, long rows, const float* part, int splits,
+                    const float* amax, const float* extra_mul) {
+    PackedFinish f;
+    f.part = part;
+    f.splits = splits;
+    f.out = rows;
+    f.in = k.in;
+    f.scale = k.scale + row0;
+    f.bits_old = k.bits + row0 * k.in / 32;
+    f.amax = amax;
+    f.extra_mul = extra_mul;
+    f.ste = ste;
+    f.lr = 0.0f;
+    f.latent = k.latent + row0 * k.in;
+    f.latent_res = k.latent_res + row0 * k.in;
+    f.g_scale = nullptr;
+    f.g_w = nullptr;
+    f.scale_upd = k.scale + row0;
+    f.scale_res = k.scale_res + row0;
+    f.bits_new = fuse_pack ? k.bits + row0 * k.in / 32 : nullptr;
+    pj.push_back(FinishJob{f, pb});
+    pb += (int)rows;
+  };
+  auto rebuild = [&](const Packed& k) {
+    if (!fuse_pack) {
+      const long n = k.out * k.in;
+      kj.push_back(PackJob{k.latent, n, k.bits, kb});
+      kb += (int)cdiv(cdiv(n, 32), 256);
+    }
+    if (!k.bits_t) return;
+    if (k.out % 32 == 0 && k.in % 32 == 0) {
+      tj.push_back(TransJob{k.bits, k.out, k.in, k.bits_t, tb});
+      tb += (int)cdiv((k.out / 32) * (k.in / 32), 8);
+    } else {
+      h->trans_generic.push_back(&k);
+    }
+  };
+
+  for (long l = 0; l < L; ++l) {
+    Block& b = h->blocks[l];
+    const long pc = (long)h->nb_col * D;
+    vec2(h->pt_mix + l * pc, h->nb_col, D, false, sgd(b.cx_k, b.cx_k_res, 1.0f, nullptr), {});
+    ln(b.ln2, h->pt_ln2 + l * 2L * h->nb_ln * D, h->nb_ln);
+    vec2(h->pt_ob + l * pc, h->nb_col, D, false, sgd(b.o.bias, b.o.bias_res, 1.0f, nullptr), {});
+    vec2(h->pt_e + l * pc, h->nb_col, D, false, sgd(b.e, b.e_res, 1.0f, nullptr), {});
+    const long nv = D * F;
+    fj.push_back(F16Job{h->gp_value + l * h->splits_value * nv, h->splits_value, nv, h->slots + l + 1,
+                        b.value, b.value_res, fb});
+    fb += (int)cdiv(nv, 256);
+    packed(b.key, 0, F, h->gp_key + l * h->splits_key * F * D, h->splits_key, h->slots + l + 1,
+           nullptr);
+    packed(b.o, 0, D, h->gp_o + l * h->splits_o * D * D, h->splits_o, h->slots + l, nullptr);
+  }
+  ln(h->ln_out, h->pt_lnout, h->nb_ln);
+  // head bias: g_bias = gscale * column sums, step at 8 lr (src/model.rs:3118-3130)
+  vec2(head_ce_bias_partials(h->head_ws, R, D, V), (int)cdiv(R, 32), V, false,
+       sgd(h->head.bias, h->head.bias_res, kHeadBiasLrMult, h->stats + 2), {});
+  {
+    const long vc = head_ce_chunk_cols(V, D);
+    const int sp = head_ce_splits(R, D, V);
+    for (long c0 = 0, ci = 0; c0 < V; c0 += vc, ++ci)
+      packed(h->head, c0, V - c0 < vc ? V - c0 : vc, h->gp_head + ci * sp * vc * D, sp, nullptr,
+             h->stats + 2);
+  }
+  if (h->blocks[0].has_ln0) {
+    const int before = vb;
+    ln(h->blocks[0].ln0, h->pt_ln0, h->nb_ln);
+    h->ln0_job_blocks = vb - before;
+  }
+  for (const Block& b : h->blocks) {
+    rebuild(b.key);
+    rebuild(b.o);
+  }
+  rebuild(h->head);
+
+  size_t bytes = 0;
+  auto add = [&](size_t b) { bytes += Carver::bytes_for(b); };
+  add(sizeof(VecJob) * vj.size());
+  add(sizeof(F16Job) * fj.size());
+  add(sizeof(FinishJob) * pj.size());
+  add(sizeof(PackJob) * kj.size());
+  add(sizeof(TransJob) * tj.size());
+  if (int rc = c->hip(hipMalloc(&h->job_mem, bytes), "heron update job tables")) return rc;
+  Carver cv(h->job_mem);
+  auto up = [&](auto& v, auto*& dst, int& n) -> int {
+    using J = typename std::remove_reference_t<decltype(v)>::value_type;
+    J* d = cv.take<J>(v.size());
+    dst = d;
+    n = (int)v.size();
+    if (v.empty()) return 0;
+    return c->hip(hipMemcpy(d, v.data(), sizeof(J) * v.size(), hipMemcpyHostToDevice),
+                  "heron update job upload");
+  };
+  if (int rc = up(vj, h->vec_jobs, h->n_vec)) return rc;
+  if (int rc = up(fj, h->f16_jobs, h->n_f16)) return rc;
+  if (int rc = up(pj, h->fin_jobs, h->n_fin)) return rc;
+  if (int rc = up(kj, h->pack_jobs, h->n_pack)) return rc;
+  if (int rc = up(tj, h->trans_jobs, h->n_trans)) return rc;
+  h->vec_blocks = vb;
+  h->f16_blocks = fb;
+  h->fin_blocks = pb;
+  h->pack_blocks = kb;
+  h->trans_blocks = tb;
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -230,12 +390,15 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
   h->splits_o = dw_splits(D, D, R);
   h->splits_key = dw_splits(F, D, R);
   h->splits_value = dw_splits(D, F, R);
-  long gpart = (long)h->splits_o * D * D;
-  if ((long)h->splits_key * F * D > gpart) gpart = (long)h->splits_key * F * D;
-  if ((long)h->splits_value * D * F > gpart) gpart = (long)h->splits_value * D * F;
-  long part = 2L * layer_norm_backward_blocks(R) * D;
-  if (column_partial_blocks(R) * D > part) part = column_partial_blocks(R) * D;
-  const long vec = F > V ? F : (V > D ? V : D);
+  h->nb_col = (int)column_partial_blocks(R);
+  h->nb_ln = layer_norm_backward_nblk(R, D);
+  const long nb_ln0 = layer_norm_backward_blocks(R);  // any LN backward path fits
+  const long head_vc = head_ce_chunk_cols(V, D);
+  const long head_sp = head_ce_splits(R, D, V);
+  const long head_chunks = cdiv(V, head_vc);
+  const long gp_value = (long)h->splits_value * D * F, gp_key = (long)h->splits_key * F * D;
+  const long gp_o = (long)h->splits_o * D * D, gp_head = head_chunks * head_sp * head_vc * D;
+  const long pt_col = (long)h->nb_col * D, pt_ln = 2L * h->nb_ln * D;
   const size_t head_ws = head_ce_workspace_bytes(R, D, V);
 
   size_t bytes = 0;
@@ -252,9 +415,14 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
   add(2ul * nf);             // gk16
   add(2ul * nd);             // gx16
   add(4ul * nd * 3);         // g_x g_a g_b
-  add(4ul * gpart);
-  add(4ul * part);
-  add(4ul * vec);
+  add(4ul * gp_value * L);
+  add(4ul * gp_key * L);
+  add(4ul * gp_o * L);
+  add(4ul * gp_head);
+  for (int i = 0; i < 3; ++i) add(4ul * pt_col * L);  // pt_mix pt_ob pt_e
+  add(4ul * pt_ln * L);      // pt_ln2
+  add(4ul * pt_ln);          // pt_lnout
+  add(4ul * 2 * nb_ln0 * D); // pt_ln0
   add(4ul * (L + 2));        // slots
   add(4ul * 4);              // stats
   add(4ul * R);              // row_loss
@@ -284,14 +452,25 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
   h->g_x = cv.take<float>(nd);
   h->g_a = cv.take<float>(nd);
   h->g_b = cv.take<float>(nd);
-  h->gpart = cv.take<float>(gpart);
-  h->part = cv.take<float>(part);
-  h->vec = cv.take<float>(vec);
+  h->gp_value = cv.take<float>(gp_value * L);
+  h->gp_key = cv.take<float>(gp_key * L);
+  h->gp_o = cv.take<float>(gp_o * L);
+  h->gp_head = cv.take<float>(gp_head);
+  h->pt_mix = cv.take<float>(pt_col * L);
+  h->pt_ob = cv.take<float>(pt_col * L);
+  h->pt_e = cv.take<float>(pt_col * L);
+  h->pt_ln2 = cv.take<float>(pt_ln * L);
+  h->pt_lnout = cv.take<float>(pt_ln);
+  h->pt_ln0 = cv.take<float>(2 * nb_ln0 * D);
   h->slots = cv.take<float>(L + 2);
   h->stats = cv.take<float>(4);
   h->row_loss = cv.take<float>(R);
   h->qkv = cv.take<uint32_t>(words * 3 * L);
   h->head_ws = cv.take<char>(head_ws);
+  if (int rc = build_update_jobs(h)) {
+    ullis_hip_heron_destroy(h);
+    return rc;
+  }
   h->probe_events.resize(2 * kProbeMax);
   for (auto& e : h->probe_events) {
     if (hipEventCreate(&e) != hipSuccess) {
@@ -314,6 +493,7 @@ void ullis_hip_heron_destroy(ullis_hip_heron* h) {
   for (auto& e : h->probe_events) (void)hipEventDestroy(e);
   if (h->arena) (void)hipFree(h->arena);
   if (h->act) (void)hipFree(h->act);
+  if (h->job_mem) (void)hipFree(h->job_mem);
   delete h;
 }
 
@@ -375,13 +555,10 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
   const long nd = R * D, nf = R * F;
   const long words = cdiv(nd, 32);
   const float ste = (float)(T - 1);  // binaryconnect_ste_scale(time - 1), src/model.rs:554-556
-  // latent rows of the packed weights are whole 64-weight chunks: the latent
-  // step, scale step and repack run in one kernel per matrix
-  const bool fuse_pack = D % 64 == 0;
   float* rl = row_loss ? row_loss : h->row_loss;
-  float* st = stats4 ? stats4 : h->stats;
   uint32_t* qkv = qkv_bits ? qkv_bits : h->qkv;
   int nb = 0;
+  bool ln0_now = false;
 
   STEP(fill_f32(s, h->slots, L + 2, 0.0f), "clear amax slots");
 
@@ -397,14 +574,14 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
     // ROSA block (src/model.rs:1354-1440)
     STEP(layer_norm_forward(s, x_l, R, D, b.ln3.w, b.ln3.b, nullptr, h->ln16), "ln3");
     STEP(time_shift_mix(s, h->ln16, R, T, D, b.x_q, h->q16, b.x_k, h->k16, b.x_v, h->v16), "mix3");
-    const Packed* qkvp[3] = {&b.q, &b.k, &b.v};
-    const uint16_t* qkv_in[3] = {h->q16, h->k16, h->v16};
-    for (int j = 0; j < 3; ++j) {
-      PackedFwdOut o;
-      o.sign_bits = qkv + (l * 3 + j) * words;
-      STEP(packed_forward(s, qkv_in[j], kF16, R, D, D, qkvp[j]->bits, qkvp[j]->scale,
-                          qkvp[j]->bias, o),
-           "qkv");
+    {
+      const uint16_t* const xin[3] = {h->q16, h->k16, h->v16};
+      const uint32_t* const wb[3] = {b.q.bits, b.k.bits, b.v.bits};
+      const uint16_t* const sc[3] = {b.q.scale, b.k.scale, b.v.scale};
+      const uint16_t* const bi[3] = {b.q.bias, b.k.bias, b.v.bias};
+      uint32_t* const planes[3] = {qkv + (l * 3 + 0) * words, qkv + (l * 3 + 1) * words,
+                                   qkv + (l * 3 + 2) * words};
+      STEP(packed_forward_bits3(s, xin, R, D, D, wb, sc, bi, planes), "qkv");
     }
     uint16_t* y16 = h->y16 + l * nd;
     STEP(rosa_expand(s, rosa_idx + l * nd, b.e, B, T, D, y16, h->idx_rm + l * nd), "rosa y");
@@ -437,8 +614,10 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
   float* x_last = h->resid + L * nd;
   STEP(layer_norm_forward(s, x_last, R, D, h->ln_out.w, h->ln_out.b, nullptr, h->ln16), "ln_out");
 
-  // ------------------------------------------------- head + CE with update
+  // ------------------------------------------------------------ head + CE
   {
+    // gradients only: the head's weight-gradient partials stay in gp_head
+    // for the end-of-step update
     HeadCe hc{};
     hc.rows = R;
     hc.time = T;
@@ -452,28 +631,18 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
     hc.targets = labels;
     hc.ignore_id = ignore_id;
     hc.row_loss = rl;
-    hc.stats = st;
+    hc.stats = h->stats;  // the update jobs read gscale from here
+    hc.stats2 = stats4;
     hc.g_hidden = h->g_a;
-    hc.g_scale = h->vec;
-    hc.lr = lr;
     hc.ste = ste;
-    hc.latent = h->head.latent;
-    hc.latent_res = h->head.latent_res;
-    hc.scale_upd = h->head.scale;
-    hc.scale_res = h->head.scale_res;
-    hc.bias_upd = h->head.bias;
-    hc.bias_res = h->head.bias_res;
-    hc.bits_new = h->head.bits;
-    hc.bits_t_new = h->head.bits_t;
+    hc.gpart_all = h->gp_head;
     PROBED_SPAN(ULLIS_HIP_PROBE_HEAD_CE, head_ce(s, hc, h->head_ws), "head ce");
   }
-  // LN_out backward + step (src/model.rs:2932-2937)
+  // LN_out backward (src/model.rs:2932-2937)
   STEP(layer_norm_backward_rows(s, x_last, h->g_a, R, D, h->ln_out.w, h->g_x, 0, h->slots + L,
-                                h->part, &nb),
+                                h->pt_lnout, &nb),
        "ln_out bwd");
-  STEP(layer_norm_param_finish(s, h->part, nb, D, nullptr, nullptr, lr, h->ln_out.w,
-                               h->ln_out.w_res, h->ln_out.b, h->ln_out.b_res),
-       "ln_out step");
+  if (nb != h->nb_ln) return c->fail(ULLIS_HIP_ERR_RUNTIME, "ln_out backward partial count");
   STEP(scale_to_f16(s, h->g_x, nd, h->slots + L, h->gx16), "g_x fp16");
 
   // ------------------------------------------------------------ backward
@@ -486,125 +655,79 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
     const uint16_t* key = h->key16 + l * nf;
     const uint16_t* r2 = h->relu2_16 + l * nf;
     const float* ar = h->after_rosa + l * nd;
+    const long pc = (long)h->nb_col * D;
 
-    // CMix backward_update (src/model.rs:1145-1177)
+    // CMix backward (src/model.rs:1145-1177)
     PROBED(ULLIS_HIP_PROBE_VALUE_INPUT_GRAD,
            fp16_backward_input(s, GradIn{h->g_x, slot_in, h->gx16}, R, F, D, b.value, nullptr, key,
                                h->gk16),
            "value input grad + relu2 bwd");
     STEP(fp16_weight_grad_partials(s, GradIn{h->g_x, slot_in, h->gx16}, r2, R, F, D,
-                                   h->splits_value,
-                                   h->gpart),
+                                   h->splits_value, h->gp_value + l * h->splits_value * D * F),
          "value weight grad");
-    STEP(fp16_weight_finish(s, h->gpart, h->splits_value, D, F, slot_in, lr, b.value, b.value_res,
-                            nullptr),
-         "value step");
     PROBED(ULLIS_HIP_PROBE_KEY_INPUT_GRAD,
            packed_backward_input(s, GradIn{nullptr, slot_in}, h->gk16, R, D, F, b.key.bits_t,
                                  b.key.scale, h->g_a, nullptr, 0),
            "key input grad");
     PROBED(ULLIS_HIP_PROBE_KEY_WEIGHT_GRAD,
            packed_weight_grad_partials(s, GradIn{nullptr, slot_in}, h->gk16, sh, R, D, F,
-                                       h->splits_key, h->gpart),
+                                       h->splits_key, h->gp_key + l * h->splits_key * F * D),
            "key weight grad");
-    {
-      PackedFinish f;
-      f.part = h->gpart;
-      f.splits = h->splits_key;
-      f.out = F;
-      f.in = D;
-      f.scale = b.key.scale;
-      f.bits_old = b.key.bits;
-      f.amax = slot_in;
-      f.extra_mul = nullptr;
-      f.ste = ste;
-      f.lr = lr;
-      f.latent = b.key.latent;
-      f.latent_res = b.key.latent_res;
-      f.g_scale = h->vec;
-      f.g_w = nullptr;
-      if (fuse_pack) {
-        f.scale_upd = b.key.scale;
-        f.scale_res = b.key.scale_res;
-        f.bits_new = b.key.bits;
-      }
-      STEP(packed_weight_finish(s, f), "key latent step");
-    }
-    if (fuse_pack) {
-      STEP(transpose_bits(s, b.key.bits, F, D, b.key.bits_t), "key bits_t");
-    } else {
-      STEP(clipped_sgd(s, b.key.scale, b.key.scale_res, h->vec, F, lr), "key scale step");
-      STEP(pack_latent_bits(s, b.key.latent, F, D, b.key.bits, b.key.bits_t), "key repack");
-    }
-    STEP(time_shift_mix_backward(s, h->g_a, ln2, b.cx_k, R, T, D, h->g_b, h->part, &nb),
+    STEP(time_shift_mix_backward(s, h->g_a, ln2, b.cx_k, R, T, D, h->g_b, h->pt_mix + l * pc, &nb),
          "mix bwd");
-    STEP(vector_finish(s, h->part, nb, D, nullptr, lr, b.cx_k, b.cx_k_res), "x_k step");
+    if (nb != h->nb_col) return c->fail(ULLIS_HIP_ERR_RUNTIME, "mix backward partial count");
 
     // LN2 backward, += into g_x (src/model.rs:2958-2963)
     PROBED(ULLIS_HIP_PROBE_LN_BACKWARD,
-           layer_norm_backward_rows(s, ar, h->g_b, R, D, b.ln2.w, h->g_x, 1, slot_mid, h->part,
-                                    &nb),
+           layer_norm_backward_rows(s, ar, h->g_b, R, D, b.ln2.w, h->g_x, 1, slot_mid,
+                                    h->pt_ln2 + l * 2L * h->nb_ln * D, &nb),
            "ln2 bwd");
-    STEP(layer_norm_param_finish(s, h->part, nb, D, nullptr, nullptr, lr, b.ln2.w, b.ln2.w_res,
-                                 b.ln2.b, b.ln2.b_res),
-         "ln2 step");
+    if (nb != h->nb_ln) return c->fail(ULLIS_HIP_ERR_RUNTIME, "ln2 backward partial count");
     // O bias gradient (column sums of g_x) and the fp16 copy of g_x for the
     // O GEMMs here and the CMix GEMMs of the block below.
-    STEP(column_sum_partials(s, h->g_x, nullptr, R, D, h->part, &nb, h->gx16, slot_mid),
+    STEP(column_sum_partials(s, h->g_x, nullptr, R, D, h->pt_ob + l * pc, &nb, h->gx16, slot_mid),
          "o g_bias + g_x fp16");
-    STEP(vector_finish(s, h->part, nb, D, nullptr, lr, b.o.bias, b.o.bias_res), "o bias step");
+    if (nb != h->nb_col) return c->fail(ULLIS_HIP_ERR_RUNTIME, "o bias partial count");
 
     // ROSA O stop-grad backward (src/model.rs:1491-1522)
     STEP(packed_backward_input(s, GradIn{h->g_x, slot_mid, h->gx16}, nullptr, R, D, D, b.o.bits_t,
                                b.o.scale, h->g_a, nullptr, 0),
          "o input grad");
-    STEP(column_sum_partials(s, h->g_a, h->idx_rm + l * nd, R, D, h->part, &nb), "g_e");
-    STEP(vector_finish(s, h->part, nb, D, nullptr, lr, b.e, b.e_res), "e step");
-    STEP(packed_weight_grad_partials(s, GradIn{h->g_x, slot_mid, h->gx16}, nullptr, h->y16 + l * nd, R, D,
-                                     D, h->splits_o, h->gpart),
+    STEP(column_sum_partials(s, h->g_a, h->idx_rm + l * nd, R, D, h->pt_e + l * pc, &nb), "g_e");
+    if (nb != h->nb_col) return c->fail(ULLIS_HIP_ERR_RUNTIME, "e gradient partial count");
+    STEP(packed_weight_grad_partials(s, GradIn{h->g_x, slot_mid, h->gx16}, nullptr,
+                                     h->y16 + l * nd, R, D, D, h->splits_o,
+                                     h->gp_o + l * h->splits_o * D * D),
          "o weight grad");
-    {
-      PackedFinish f;
-      f.part = h->gpart;
-      f.splits = h->splits_o;
-      f.out = D;
-      f.in = D;
-      f.scale = b.o.scale;
-      f.bits_old = b.o.bits;
-      f.amax = slot_mid;
-      f.extra_mul = nullptr;
-      f.ste = ste;
-      f.lr = lr;
-      f.latent = b.o.latent;
-      f.latent_res = b.o.latent_res;
-      f.g_scale = h->vec;
-      f.g_w = nullptr;
-      if (fuse_pack) {
-        f.scale_upd = b.o.scale;
-        f.scale_res = b.o.scale_res;
-        f.bits_new = b.o.bits;
-      }
-      STEP(packed_weight_finish(s, f), "o latent step");
-    }
-    if (fuse_pack) {
-      STEP(transpose_bits(s, b.o.bits, D, D, b.o.bits_t), "o bits_t");
-    } else {
-      STEP(clipped_sgd(s, b.o.scale, b.o.scale_res, h->vec, D, lr), "o scale step");
-      STEP(pack_latent_bits(s, b.o.latent, D, D, b.o.bits, b.o.bits_t), "o repack");
-    }
 
     if (b.has_ln0) {  // (src/model.rs:2978-2982)
-      STEP(layer_norm_backward_rows(s, x_emb, h->g_x, R, D, b.ln0.w, g_emb, 0, nullptr, h->part,
+      STEP(layer_norm_backward_rows(s, x_emb, h->g_x, R, D, b.ln0.w, g_emb, 0, nullptr, h->pt_ln0,
                                     &nb),
            "ln0 bwd");
-      STEP(layer_norm_param_finish(s, h->part, nb, D, nullptr, nullptr, lr, b.ln0.w, b.ln0.w_res,
-                                   b.ln0.b, b.ln0.b_res),
-           "ln0 step");
+      if (nb != h->nb_ln) {
+        // another LN backward path (unaligned x_emb / g_emb): step LN0 here
+        // and leave its batched job out
+        ln0_now = true;
+        STEP(layer_norm_param_finish(s, h->pt_ln0, nb, D, nullptr, nullptr, lr, b.ln0.w,
+                                     b.ln0.w_res, b.ln0.b, b.ln0.b_res),
+             "ln0 step");
+      }
     } else if (l == 0) {
       STEP(copy_device(s, g_emb, h->g_x, (long)sizeof(float) * nd), "copy g_emb");
     }
   }
-  (void)F;
+
+  // ------------------------------------------------ end-of-step updates
+  // vector steps (LN gamma / beta, x_k, O bias, e, head bias at 8 lr)
+  STEP(run_vec_jobs(s, h->vec_jobs, h->n_vec - (ln0_now && h->ln0_job_blocks ? 1 : 0),
+                    h->vec_blocks - (ln0_now ? h->ln0_job_blocks : 0), lr),
+       "vector steps");
+  STEP(run_f16_jobs(s, h->f16_jobs, h->n_f16, h->f16_blocks, lr), "value steps");
+  STEP(run_finish_jobs(s, h->fin_jobs, h->n_fin, h->fin_blocks, lr), "latent / scale steps");
+  STEP(run_pack_jobs(s, h->pack_jobs, h->n_pack, h->pack_blocks), "latent repack");
+  STEP(run_trans_jobs(s, h->trans_jobs, h->n_trans, h->trans_blocks), "bits_t");
+  for (const Packed* k : h->trans_generic)
+    STEP(transpose_bits(s, k->bits, k->out, k->in, k->bits_t), "bits_t");
   return 0;
 }
 

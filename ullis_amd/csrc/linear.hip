@@ -15,6 +15,7 @@
 #include "gemm.hpp"
 #include "gemm_lds.hpp"
 #include "ops.hpp"
+#include "update.hpp"
 
 namespace ullis {
 
@@ -283,57 +284,17 @@ struct EpiRelu2Bwd {
 // ------------------------------------------------------------ finish kernels
 
 __global__ __launch_bounds__(256) void packed_finish_kernel(PackedFinish f) {
+  __shared__ float red[256];
   const long o = blockIdx.x;
   if (o >= f.out) return;
-  __shared__ float red[256];
-  float gmul = f.amax ? 1.0f / grad_scale_from_amax(*f.amax) : 1.0f;
-  if (f.extra_mul) gmul *= *f.extra_mul;
-  const float sc = f16_bits_to_f32(f.scale[o]);
-  const long wn = f.out * f.in;
-  float gs = 0.0f;
-  const int lane = threadIdx.x & 63;
-  for (long i = threadIdx.x; i < f.in; i += blockDim.x) {
-    const long w = o * f.in + i;
-    float G = 0.0f;
-    for (int z = 0; z < f.splits; ++z) G += f.part[(long)z * wn + w];
-    G *= gmul;
-    const bool plus = (f.bits_old[w >> 5] >> (w & 31)) & 1u;
-    gs += plus ? G : -G;
-    const float gw = sc * G;
-    if (f.g_w) f.g_w[w] = gw;
-    if (f.latent) {
-      binaryconnect_sgd_one(f.latent[w], f.latent_res[w], gw * f.ste, f.lr);
-      if (f.bits_new) {
-        // whole waves cover 64 consecutive weights of row o (in % 64 == 0);
-        // each word of the row is read above before it is rewritten here
-        const unsigned long long m = __ballot(latent_is_plus(f.latent[w]));
-        if (lane == 0) f.bits_new[w >> 5] = (uint32_t)m;
-        if (lane == 32) f.bits_new[w >> 5] = (uint32_t)(m >> 32);
-      }
-    }
-  }
-  red[threadIdx.x] = gs;
-  __syncthreads();
-  for (int st = 128; st > 0; st >>= 1) {
-    if ((int)threadIdx.x < st) red[threadIdx.x] += red[threadIdx.x + st];
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) {
-    if (f.g_scale) f.g_scale[o] = red[0];
-    if (f.scale_upd && f.lr > 0.0f) clipped_sgd_one(f.scale_upd[o], f.scale_res[o], red[0], f.lr);
-  }
+  packed_finish_row(f, o, f.lr, red);
 }
 
 __global__ void fp16_finish_kernel(const float* part, int splits, long n, const float* amax,
                                    float lr, uint16_t* w, float* w_res, float* g_w) {
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const float m = amax ? 1.0f / grad_scale_from_amax(*amax) : 1.0f;
-  float G = 0.0f;
-  for (int z = 0; z < splits; ++z) G += part[(long)z * n + i];
-  G *= m;
-  if (g_w) g_w[i] = G;
-  if (w) clipped_sgd_one(w[i], w_res[i], G, lr);
+  fp16_finish_one(part, splits, n, i, amax, lr, w, w_res, g_w);
 }
 
 // One thread per word: bit j of word w is latent[32w + j] >= 0 (ullis_pack_latent_bits).
@@ -353,20 +314,8 @@ __global__ void pack_bits_kernel(const uint16_t* latent, long n, uint32_t* bits)
 // 32x32 bit block with 32 ballots.
 __global__ void transpose_bits_aligned_kernel(const uint32_t* bits, long out, long in,
                                               uint32_t* bits_t) {
-  const int lane = threadIdx.x & 63;
   const long blk = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 5;  // one block per half-wave
-  const long ob = out / 32, ib = in / 32;
-  const bool active = blk < ob * ib;
-  const long bo = active ? blk / ib : 0, bi = active ? blk % ib : 0;
-  const long o = bo * 32 + (lane & 31);
-  const uint32_t word = active ? bits[(o * in + bi * 32) >> 5] : 0u;
-  for (int b = 0; b < 32; ++b) {
-    const unsigned long long m = __ballot((word >> b) & 1u);
-    if ((lane & 31) == 0 && active) {
-      const long i = bi * 32 + b;
-      bits_t[(i * out + bo * 32) >> 5] = (lane < 32) ? (uint32_t)m : (uint32_t)(m >> 32);
-    }
-  }
+  transpose_bits_block(bits, out, in, bits_t, blk, blk < (out / 32) * (in / 32));
 }
 
 __global__ void transpose_bits_generic_kernel(const uint32_t* bits, long out, long in,
@@ -430,6 +379,39 @@ hipError_t packed_forward(hipStream_t s, const void* x, int x_dtype, long rows, 
     case kOutBits: return run(std::integral_constant<int, kOutBits>{});
     default: return hipErrorInvalidValue;
   }
+}
+
+hipError_t packed_forward_bits3(hipStream_t s, const uint16_t* const x[3], long rows, long in,
+                               long out, const uint32_t* const bits[3],
+                               const uint16_t* const scale[3], const uint16_t* const bias[3],
+                               uint32_t* const sign_bits[3]) {
+  if (out % 32 != 0) return hipErrorInvalidValue;
+  bool lds_ok = true;
+  for (int j = 0; j < 3; ++j) lds_ok = lds_ok && lds::mk_ok(x[j], in);
+  hipError_t err = hipSuccess;
+  if (lds_ok && lds::with_lds(rows, out, in, 1, &err, [&](auto t) {
+        using T = decltype(t);
+        lds::Group<lds::OpMK<T::bm, T::bk>, 3> a;
+        lds::Group<lds::OpBits<T::bn, T::bk, false>, 3> b;
+        lds::Group<EpiPackedFwd<kOutBits>, 3> e;
+        for (int j = 0; j < 3; ++j) {
+          a.v[j] = {reinterpret_cast<const half_t*>(x[j]), in, (int)rows};
+          b.v[j] = {bits[j], in / 32, (int)out, nullptr, 0};
+          PackedFwdOut o;
+          o.sign_bits = sign_bits[j];
+          e.v[j] = {scale[j], bias[j], o};
+        }
+        return lds::launch_lds_group<T>(s, a, b, e, rows, out, in);
+      }))
+    return err;
+  for (int j = 0; j < 3; ++j) {
+    PackedFwdOut o;
+    o.sign_bits = sign_bits[j];
+    if ((err = packed_forward(s, x[j], kF16, rows, in, out, bits[j], scale[j], bias[j], o)) !=
+        hipSuccess)
+      return err;
+  }
+  return hipSuccess;
 }
 
 hipError_t packed_backward_input(hipStream_t s, GradIn gy32, const uint16_t* gy16, long rows,

@@ -411,6 +411,17 @@ static bool ln_bwd_vec_path(long ch) { return ch % 4 == 0 && ch <= 1024; }
 // Blocks of the vector path (one row per wave) and of the any-ch path.
 static bool ln_bwd_row_path(long rows, long ch) { return ln_bwd_vec_path(ch) && rows <= (1L << 20); }
 
+static int ln_bwd_blocks_any(long rows) {
+  long nblk = cdiv(rows, 2 * kRowsPerBlock);
+  if (nblk > 256) nblk = 256;
+  if (nblk < 1) nblk = 1;
+  return (int)nblk;
+}
+
+int layer_norm_backward_nblk(long rows, long ch) {
+  return ln_bwd_row_path(rows, ch) ? (int)cdiv(rows, kRowsPerBlock) : ln_bwd_blocks_any(rows);
+}
+
 int layer_norm_backward_blocks(long rows) {
   // Upper bound over both paths (sizes the partial buffers).
   long nblk = cdiv(rows, kRowsPerBlock);
@@ -418,12 +429,6 @@ int layer_norm_backward_blocks(long rows) {
   return (int)nblk;
 }
 
-static int ln_bwd_blocks_any(long rows) {
-  long nblk = cdiv(rows, 2 * kRowsPerBlock);
-  if (nblk > 256) nblk = 256;
-  if (nblk < 1) nblk = 1;
-  return (int)nblk;
-}
 
 hipError_t layer_norm_backward_rows(hipStream_t s, const float* x, const float* gy, long rows,
                                     long ch, const uint16_t* w, float* gx, int accumulate,

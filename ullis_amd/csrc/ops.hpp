@@ -37,6 +37,13 @@ hipError_t packed_forward(hipStream_t s, const void* x, int x_dtype, long rows, 
                           const uint32_t* bits, const uint16_t* scale, const uint16_t* bias,
                           const PackedFwdOut& o);
 
+// Three packed forwards of one shape (Q, K, V) in one launch, each writing
+// only its sign bit-plane (bit = y > 0).
+hipError_t packed_forward_bits3(hipStream_t s, const uint16_t* const x[3], long rows, long in,
+                               long out, const uint32_t* const bits[3],
+                               const uint16_t* const scale[3], const uint16_t* const bias[3],
+                               uint32_t* const sign_bits[3]);
+
 // gX = (gY * scale) . S  via bits_t ([in, out] transpose bits) -> fp32 gx.
 // gy is fp32 (scaled by amax) or fp16 (already scaled by 1/unscale); result is
 // multiplied by out_mul (device scalar, may be null) and 1/gy-scale.
@@ -117,6 +124,8 @@ hipError_t layer_norm_backward_rows(hipStream_t s, const float* x, const float* 
                                     long ch, const uint16_t* w, float* gx, int accumulate,
                                     float* amax, float* part, int* nblk_out);
 int layer_norm_backward_blocks(long rows);
+// Partial blocks layer_norm_backward_rows uses for 16-byte aligned x / gy / gx.
+int layer_norm_backward_nblk(long rows, long ch);
 
 // Sums part[nblk][2][ch] -> gw, gb (optional outputs) and, when lr > 0,
 // clipped SGD on (w, b) with their carries.
@@ -214,8 +223,75 @@ struct HeadCe {
   float* bias_res;
   uint32_t* bits_new;   // repacked bits (may alias bits only after all reads)
   uint32_t* bits_t_new;
+  float* stats2 = nullptr;  // optional second copy of stats
+  // Deferred mode (non-null): the weight-gradient partials of every vocab
+  // chunk go to gpart_all[chunk][splits][vc][d] and no update runs; the
+  // caller runs them later (head_ce_bias_partials, head_ce_chunk_cols,
+  // head_ce_splits describe the layout).
+  float* gpart_all = nullptr;
 };
 size_t head_ce_workspace_bytes(long rows, long d, long vocab);
 hipError_t head_ce(hipStream_t s, const HeadCe& h, void* workspace);
+long head_ce_chunk_cols(long vocab, long d);
+int head_ce_splits(long rows, long d, long vocab);
+// g_bias partials [ceil(rows/32)][vocab] (unscaled: multiply by gscale).
+float* head_ce_bias_partials(void* workspace, long rows, long d, long vocab);
+
+// ------------------------------------------- batched end-of-step updates
+// A train step can defer every parameter update to its end (no later kernel
+// of the step reads an updated parameter), then run all updates of one kind
+// in a single launch: blocks [block0, block0 + blocks) of the batched grid
+// belong to one job. Job tables live in device memory, ordered by block0.
+
+// Column reduction of part[nblk][ncols] with steps on up to two targets
+// (see partial_reduce); a.lr / b.lr hold multipliers of the launch's lr.
+struct VecJob {
+  const float* part;
+  int nblk;
+  long ncols, split;
+  VecTarget a, b;
+  int block0;
+};
+inline int vec_job_blocks(long ncols) { return (int)cdiv(ncols, 16); }
+
+// One row per block; f.lr is ignored (the launch's lr is used).
+struct FinishJob {
+  PackedFinish f;
+  int block0;
+};
+
+// fp16 weight finish, 256 elements per block.
+struct F16Job {
+  const float* part;
+  int splits;
+  long n;
+  const float* amax;
+  uint16_t* w;
+  float* w_res;
+  int block0;
+};
+
+// latent -> bits repack, 256 words per block.
+struct PackJob {
+  const uint16_t* latent;
+  long n;
+  uint32_t* bits;
+  int block0;
+};
+
+// bits [out][in] -> bits_t [in][out], out % 32 == 0, in % 32 == 0; eight 32x32
+// bit blocks per 256-thread block.
+struct TransJob {
+  const uint32_t* bits;
+  long out, in;
+  uint32_t* bits_t;
+  int block0;
+};
+
+hipError_t run_vec_jobs(hipStream_t s, const VecJob* jobs, int njobs, int nblocks, float lr);
+hipError_t run_finish_jobs(hipStream_t s, const FinishJob* jobs, int njobs, int nblocks, float lr);
+hipError_t run_f16_jobs(hipStream_t s, const F16Job* jobs, int njobs, int nblocks, float lr);
+hipError_t run_pack_jobs(hipStream_t s, const PackJob* jobs, int njobs, int nblocks);
+hipError_t run_trans_jobs(hipStream_t s, const TransJob* jobs, int njobs, int nblocks);
 
 }  // namespace ullis
