@@ -19,7 +19,7 @@ __device__ __forceinline__ int find_job(const J* jobs, int njobs, int blk) {
 }
 
 __global__ __launch_bounds__(1024) void vec_jobs_kernel(const VecJob* jobs, int njobs, float lr) {
-  __shared__ float red[64][16];
+  __shared__ float red[64][64];
   const int j = find_job(jobs, njobs, blockIdx.x);
   const VecJob& jb = jobs[j];
   vec_reduce_block(jb.part, jb.nblk, jb.ncols, jb.split, jb.a, jb.a.lr * lr, jb.b, jb.b.lr * lr,
@@ -28,30 +28,17 @@ __global__ __launch_bounds__(1024) void vec_jobs_kernel(const VecJob* jobs, int 
 
 __global__ __launch_bounds__(256) void finish_jobs_kernel(const FinishJob* jobs, int njobs,
                                                           float lr) {
-  __shared__ float red[256];
   const int j = find_job(jobs, njobs, blockIdx.x);
   const PackedFinish f = jobs[j].f;
-  const long o = (long)blockIdx.x - jobs[j].block0;
-  if (o < f.out) packed_finish_row(f, o, lr, red);
+  const long o = ((long)blockIdx.x - jobs[j].block0) * 4 + (threadIdx.x >> 6);
+  if (o < f.out) packed_finish_row_wave(f, o, lr);
 }
 
 __global__ __launch_bounds__(256) void f16_jobs_kernel(const F16Job* jobs, int njobs, float lr) {
   const int j = find_job(jobs, njobs, blockIdx.x);
   const F16Job& jb = jobs[j];
-  const long i = ((long)blockIdx.x - jb.block0) * blockDim.x + threadIdx.x;
-  if (i < jb.n) fp16_finish_one(jb.part, jb.splits, jb.n, i, jb.amax, lr, jb.w, jb.w_res, nullptr);
-}
-
-__global__ __launch_bounds__(256) void pack_jobs_kernel(const PackJob* jobs, int njobs) {
-  const int j = find_job(jobs, njobs, blockIdx.x);
-  const PackJob& jb = jobs[j];
-  const long w = ((long)blockIdx.x - jb.block0) * blockDim.x + threadIdx.x;
-  const long base = w * 32;
-  if (base >= jb.n) return;
-  uint32_t packed = 0;
-  for (int k = 0; k < 32; ++k)
-    if (base + k < jb.n && latent_is_plus(jb.latent[base + k])) packed |= 1u << k;
-  jb.bits[w] = packed;
+  const long i = (((long)blockIdx.x - jb.block0) * blockDim.x + threadIdx.x) * 4;
+  if (i < jb.n) fp16_finish_four(jb.part, jb.splits, jb.n, i, jb.amax, lr, jb.w, jb.w_res, nullptr);
 }
 
 __global__ __launch_bounds__(256) void trans_jobs_kernel(const TransJob* jobs, int njobs) {
@@ -80,12 +67,6 @@ hipError_t run_finish_jobs(hipStream_t s, const FinishJob* jobs, int njobs, int 
 hipError_t run_f16_jobs(hipStream_t s, const F16Job* jobs, int njobs, int nblocks, float lr) {
   if (njobs <= 0 || nblocks <= 0) return hipSuccess;
   launch(f16_jobs_kernel, dim3((unsigned)nblocks), dim3(256), 0, s, jobs, njobs, lr);
-  return hipGetLastError();
-}
-
-hipError_t run_pack_jobs(hipStream_t s, const PackJob* jobs, int njobs, int nblocks) {
-  if (njobs <= 0 || nblocks <= 0) return hipSuccess;
-  launch(pack_jobs_kernel, dim3((unsigned)nblocks), dim3(256), 0, s, jobs, njobs);
   return hipGetLastError();
 }
 

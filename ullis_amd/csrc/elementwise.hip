@@ -280,7 +280,7 @@ __global__ void scale_to_f16_kernel(const float* v, long n, const float* amax, u
 __global__ __launch_bounds__(1024) void partial_reduce_kernel(const float* part, int nblk,
                                                               long ncols, long split, VecTarget a,
                                                               VecTarget b) {
-  __shared__ float red[64][16];
+  __shared__ float red[64][64];
   vec_reduce_block(part, nblk, ncols, split, a, a.lr, b, b.lr, blockIdx.x, red);
 }
 
@@ -459,7 +459,7 @@ hipError_t scale_to_f16(hipStream_t s, const float* v, long n, const float* amax
 hipError_t partial_reduce(hipStream_t s, const float* part, int nblk, long ncols, long split,
                           const VecTarget& a, const VecTarget& b) {
   if (ncols <= 0) return hipSuccess;
-  launch(partial_reduce_kernel, dim3((unsigned)cdiv(ncols, 16)), dim3(1024), 0, s, part, nblk,
+  launch(partial_reduce_kernel, dim3((unsigned)vec_job_blocks(ncols)), dim3(1024), 0, s, part, nblk,
          ncols, split, a, b);
   return hipGetLastError();
 }

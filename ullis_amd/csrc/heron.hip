@@ -17,11 +17,10 @@
 // backward, and the reference updates it after its last read, so no kernel
 // later in the step reads an updated parameter. Every update is therefore
 // deferred to the end of the step: the gradient partials of each tensor stay
-// in their own buffers and five batched launches (vector steps, fp16 weight
-// steps, packed latent / scale steps with the repack, latent repack where
-// rows are not whole 64-weight chunks, bit transposes) apply them, with the
-// same per-tensor arithmetic as updating each tensor at the reference's
-// update call.
+// in their own buffers and four batched launches (vector steps, fp16 weight
+// steps, packed latent / scale steps with the repack, bit transposes) apply
+// them, with the same per-tensor arithmetic as updating each tensor at the
+// reference's update call.
 #include <hip/hip_runtime.h>
 
 #include <string>
@@ -95,10 +94,9 @@ struct ullis_hip_heron {
   const VecJob* vec_jobs = nullptr;
   const F16Job* f16_jobs = nullptr;
   const FinishJob* fin_jobs = nullptr;
-  const PackJob* pack_jobs = nullptr;
   const TransJob* trans_jobs = nullptr;
-  int n_vec = 0, n_f16 = 0, n_fin = 0, n_pack = 0, n_trans = 0;
-  int vec_blocks = 0, f16_blocks = 0, fin_blocks = 0, pack_blocks = 0, trans_blocks = 0;
+  int n_vec = 0, n_f16 = 0, n_fin = 0, n_trans = 0;
+  int vec_blocks = 0, f16_blocks = 0, fin_blocks = 0, trans_blocks = 0;
   int ln0_job_blocks = 0;  // blocks of the trailing LN0 job (0: none)
   std::vector<const Packed*> trans_generic;  // bits_t rebuilt by the generic transpose
   uint32_t* qkv = nullptr;
@@ -192,13 +190,12 @@ int build_update_jobs(ullis_hip_heron* h) {
   ullis_hip_ctx* c = h->ctx;
   const long R = h->rows, D = h->D, F = h->F, V = h->V, L = h->L;
   const float ste = (float)(h->time - 1);  // binaryconnect_ste_scale(time - 1), src/model.rs:554-556
-  const bool fuse_pack = D % 64 == 0;       // whole 64-weight chunks per latent row
   std::vector<VecJob> vj;
   std::vector<F16Job> fj;
   std::vector<FinishJob> pj;
-  std::vector<PackJob> kj;
   std::vector<TransJob> tj;
-  int vb = 0, fb = 0, pb = 0, kb = 0, tb = 0;
+  int vb = 0, fb = 0, pb = 0, tb = 0;
+  bool vec_ok = true;
   auto vec2 = [&](const float* part, int nblk, long ch, bool two, VecTarget a, VecTarget b) {
     VecJob j{part, nblk, two ? 2 * ch : ch, ch, a, two ? b : a, vb};
     vb += vec_job_blocks(j.ncols);
@@ -210,8 +207,8 @@ int build_update_jobs(ullis_hip_heron* h) {
   auto ln = [&](const Ln& n, const float* part, int nblk) {
     vec2(part, nblk, D, true, sgd(n.w, n.w_res, 1.0f, nullptr), sgd(n.b, n.b_res, 1.0f, nullptr));
   };
-  // packed latent / scale steps (+ repack in the finish or as a pack job),
-  // then the bit transpose
+  // packed latent / scale steps with the repack (rows of in % 32 == 0
+  // weights), then the bit transpose
   auto packed = [&](const Packed& k, long row0, long rows, const float* part, int splits,
                     const float* amax, const float* extra_mul) {
     PackedFinish f;
@@ -231,16 +228,12 @@ int build_update_jobs(ullis_hip_heron* h) {
     f.g_w = nullptr;
     f.scale_upd = k.scale + row0;
     f.scale_res = k.scale_res + row0;
-    f.bits_new = fuse_pack ? k.bits + row0 * k.in / 32 : nullptr;
+    f.bits_new = k.bits + row0 * k.in / 32;
+    vec_ok = vec_ok && packed_finish_wave_ok(f);
     pj.push_back(FinishJob{f, pb});
-    pb += (int)rows;
+    pb += finish_job_blocks(rows);
   };
   auto rebuild = [&](const Packed& k) {
-    if (!fuse_pack) {
-      const long n = k.out * k.in;
-      kj.push_back(PackJob{k.latent, n, k.bits, kb});
-      kb += (int)cdiv(cdiv(n, 32), 256);
-    }
     if (!k.bits_t) return;
     if (k.out % 32 == 0 && k.in % 32 == 0) {
       tj.push_back(TransJob{k.bits, k.out, k.in, k.bits_t, tb});
@@ -258,9 +251,10 @@ int build_update_jobs(ullis_hip_heron* h) {
     vec2(h->pt_ob + l * pc, h->nb_col, D, false, sgd(b.o.bias, b.o.bias_res, 1.0f, nullptr), {});
     vec2(h->pt_e + l * pc, h->nb_col, D, false, sgd(b.e, b.e_res, 1.0f, nullptr), {});
     const long nv = D * F;
-    fj.push_back(F16Job{h->gp_value + l * h->splits_value * nv, h->splits_value, nv, h->slots + l + 1,
-                        b.value, b.value_res, fb});
-    fb += (int)cdiv(nv, 256);
+    const float* gpv = h->gp_value + l * h->splits_value * nv;
+    vec_ok = vec_ok && fp16_finish_vec_ok(gpv, nv, b.value, b.value_res, nullptr);
+    fj.push_back(F16Job{gpv, h->splits_value, nv, h->slots + l + 1, b.value, b.value_res, fb});
+    fb += f16_job_blocks(nv);
     packed(b.key, 0, F, h->gp_key + l * h->splits_key * F * D, h->splits_key, h->slots + l + 1,
            nullptr);
     packed(b.o, 0, D, h->gp_o + l * h->splits_o * D * D, h->splits_o, h->slots + l, nullptr);
@@ -286,13 +280,14 @@ int build_update_jobs(ullis_hip_heron* h) {
     rebuild(b.o);
   }
   rebuild(h->head);
+  if (!vec_ok)
+    return c->fail(ULLIS_HIP_ERR_INVALID, "heron update tensors are not 16-byte aligned");
 
   size_t bytes = 0;
   auto add = [&](size_t b) { bytes += Carver::bytes_for(b); };
   add(sizeof(VecJob) * vj.size());
   add(sizeof(F16Job) * fj.size());
   add(sizeof(FinishJob) * pj.size());
-  add(sizeof(PackJob) * kj.size());
   add(sizeof(TransJob) * tj.size());
   if (int rc = c->hip(hipMalloc(&h->job_mem, bytes), "heron update job tables")) return rc;
   Carver cv(h->job_mem);
@@ -308,12 +303,10 @@ int build_update_jobs(ullis_hip_heron* h) {
   if (int rc = up(vj, h->vec_jobs, h->n_vec)) return rc;
   if (int rc = up(fj, h->f16_jobs, h->n_f16)) return rc;
   if (int rc = up(pj, h->fin_jobs, h->n_fin)) return rc;
-  if (int rc = up(kj, h->pack_jobs, h->n_pack)) return rc;
   if (int rc = up(tj, h->trans_jobs, h->n_trans)) return rc;
   h->vec_blocks = vb;
   h->f16_blocks = fb;
   h->fin_blocks = pb;
-  h->pack_blocks = kb;
   h->trans_blocks = tb;
   return 0;
 }
@@ -724,7 +717,6 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
        "vector steps");
   STEP(run_f16_jobs(s, h->f16_jobs, h->n_f16, h->f16_blocks, lr), "value steps");
   STEP(run_finish_jobs(s, h->fin_jobs, h->n_fin, h->fin_blocks, lr), "latent / scale steps");
-  STEP(run_pack_jobs(s, h->pack_jobs, h->n_pack, h->pack_blocks), "latent repack");
   STEP(run_trans_jobs(s, h->trans_jobs, h->n_trans, h->trans_blocks), "bits_t");
   for (const Packed* k : h->trans_generic)
     STEP(transpose_bits(s, k->bits, k->out, k->in, k->bits_t), "bits_t");

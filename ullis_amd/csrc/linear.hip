@@ -290,11 +290,23 @@ __global__ __launch_bounds__(256) void packed_finish_kernel(PackedFinish f) {
   packed_finish_row(f, o, f.lr, red);
 }
 
+__global__ __launch_bounds__(256) void packed_finish_wave_kernel(PackedFinish f) {
+  const long o = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (o < f.out) packed_finish_row_wave(f, o, f.lr);
+}
+
 __global__ void fp16_finish_kernel(const float* part, int splits, long n, const float* amax,
                                    float lr, uint16_t* w, float* w_res, float* g_w) {
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   fp16_finish_one(part, splits, n, i, amax, lr, w, w_res, g_w);
+}
+
+__global__ __launch_bounds__(256) void fp16_finish4_kernel(const float* part, int splits, long n,
+                                                           const float* amax, float lr,
+                                                           uint16_t* w, float* w_res, float* g_w) {
+  const long i = ((long)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i < n) fp16_finish_four(part, splits, n, i, amax, lr, w, w_res, g_w);
 }
 
 // One thread per word: bit j of word w is latent[32w + j] >= 0 (ullis_pack_latent_bits).
@@ -492,11 +504,28 @@ hipError_t packed_weight_grad_partials(hipStream_t s, GradIn gy32, const uint16_
   });
 }
 
+bool packed_finish_wave_ok(const PackedFinish& f) {
+  auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  return f.in % 32 == 0 && a16(f.part) && (!f.latent || (a16(f.latent) && a16(f.latent_res))) &&
+         (!f.g_w || a16(f.g_w));
+}
+
+bool fp16_finish_vec_ok(const float* part, long n, const uint16_t* w, const float* w_res,
+                        const float* g_w) {
+  auto al = [](const void* p, unsigned m) { return (reinterpret_cast<uintptr_t>(p) & m) == 0; };
+  return n % 4 == 0 && al(part, 15u) && (!w || (al(w, 7u) && al(w_res, 15u))) &&
+         (!g_w || al(g_w, 15u));
+}
+
 hipError_t packed_weight_finish(hipStream_t s, const PackedFinish& f) {
   if (f.out <= 0 || f.in <= 0) return hipSuccess;
-  if (f.bits_new && (f.in % 64 != 0 || !f.latent)) return hipErrorInvalidValue;
+  const bool wave = packed_finish_wave_ok(f);
+  if (f.bits_new && (!f.latent || (!wave && f.in % 64 != 0))) return hipErrorInvalidValue;
   if (f.scale_upd && !f.scale_res) return hipErrorInvalidValue;
-  launch(packed_finish_kernel, dim3((unsigned)f.out), dim3(256), 0, s, f);
+  if (wave)
+    launch(packed_finish_wave_kernel, dim3((unsigned)finish_job_blocks(f.out)), dim3(256), 0, s, f);
+  else
+    launch(packed_finish_kernel, dim3((unsigned)f.out), dim3(256), 0, s, f);
   return hipGetLastError();
 }
 
@@ -591,8 +620,12 @@ hipError_t fp16_weight_finish(hipStream_t s, const float* part, int splits, long
                               float* g_w) {
   const long n = out * in;
   if (n <= 0) return hipSuccess;
-  launch(fp16_finish_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, s, part,
-                     splits, n, amax, lr, w, w_res, g_w);
+  if (fp16_finish_vec_ok(part, n, w, w_res, g_w))
+    launch(fp16_finish4_kernel, dim3((unsigned)f16_job_blocks(n)), dim3(256), 0, s, part, splits,
+           n, amax, lr, w, w_res, g_w);
+  else
+    launch(fp16_finish_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, s, part, splits, n,
+           amax, lr, w, w_res, g_w);
   return hipGetLastError();
 }
 

@@ -77,12 +77,19 @@ struct PackedFinish {
   float* g_w;              // may be null
   // Fused tail of the update (optional, with latent set): clipped SGD of
   // scale[o] at lr with g_scale[o] (scale_upd/scale_res), and the repack of
-  // the updated latent rows into bits_new (requires in % 64 == 0).
+  // the updated latent rows into bits_new (requires packed_finish_wave_ok,
+  // or in % 64 == 0).
   uint16_t* scale_upd = nullptr;
   float* scale_res = nullptr;
   uint32_t* bits_new = nullptr;
 };
 hipError_t packed_weight_finish(hipStream_t s, const PackedFinish& f);
+// in % 32 == 0 and 16-byte aligned part / latent / latent_res / g_w: the
+// finish runs one wave per row with vector loads.
+bool packed_finish_wave_ok(const PackedFinish& f);
+// n % 4 == 0, part / w_res / g_w 16-byte and w 8-byte aligned.
+bool fp16_finish_vec_ok(const float* part, long n, const uint16_t* w, const float* w_res,
+                        const float* g_w);
 
 // Latent -> bits (row-major) and, if bits_t is non-null, the transposed bits.
 hipError_t pack_latent_bits(hipStream_t s, const uint16_t* latent, long out, long in,
@@ -252,15 +259,18 @@ struct VecJob {
   VecTarget a, b;
   int block0;
 };
-inline int vec_job_blocks(long ncols) { return (int)cdiv(ncols, 16); }
+inline int vec_job_blocks(long ncols) { return (int)cdiv(ncols, 64); }
 
-// One row per block; f.lr is ignored (the launch's lr is used).
+// Four rows per block, one wave each (packed_finish_wave_ok must hold, with
+// bits_new set or null); f.lr is ignored (the launch's lr is used).
+inline int finish_job_blocks(long rows) { return (int)cdiv(rows, 4); }
 struct FinishJob {
   PackedFinish f;
   int block0;
 };
 
-// fp16 weight finish, 256 elements per block.
+// fp16 weight finish, 1024 elements per block (fp16_finish_vec_ok must hold).
+inline int f16_job_blocks(long n) { return (int)cdiv(n, 1024); }
 struct F16Job {
   const float* part;
   int splits;
@@ -268,14 +278,6 @@ struct F16Job {
   const float* amax;
   uint16_t* w;
   float* w_res;
-  int block0;
-};
-
-// latent -> bits repack, 256 words per block.
-struct PackJob {
-  const uint16_t* latent;
-  long n;
-  uint32_t* bits;
   int block0;
 };
 
@@ -291,7 +293,6 @@ struct TransJob {
 hipError_t run_vec_jobs(hipStream_t s, const VecJob* jobs, int njobs, int nblocks, float lr);
 hipError_t run_finish_jobs(hipStream_t s, const FinishJob* jobs, int njobs, int nblocks, float lr);
 hipError_t run_f16_jobs(hipStream_t s, const F16Job* jobs, int njobs, int nblocks, float lr);
-hipError_t run_pack_jobs(hipStream_t s, const PackJob* jobs, int njobs, int nblocks);
 hipError_t run_trans_jobs(hipStream_t s, const TransJob* jobs, int njobs, int nblocks);
 
 }  // namespace ullis
