@@ -182,9 +182,9 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
 #define ULLIS_HIP_PROBE_KEY_FORWARD 1       /* CMix key packed GEMM + ReLU^2, per layer */
 #define ULLIS_HIP_PROBE_VALUE_FORWARD 2     /* CMix value fp16 GEMM + residual add */
 #define ULLIS_HIP_PROBE_HEAD_CE 3           /* whole head + streamed CE (several kernels) */
-#define ULLIS_HIP_PROBE_VALUE_INPUT_GRAD 4  /* value dX GEMM + ReLU^2 backward */
-#define ULLIS_HIP_PROBE_KEY_INPUT_GRAD 5    /* key dX packed GEMM */
-#define ULLIS_HIP_PROBE_KEY_WEIGHT_GRAD 6   /* key dW GEMM (partials) */
+#define ULLIS_HIP_PROBE_VALUE_BACKWARD 4    /* value dX (+ ReLU^2 bwd) and dW in one launch */
+#define ULLIS_HIP_PROBE_KEY_BACKWARD 5      /* key dX (packed) and dW in one launch */
+#define ULLIS_HIP_PROBE_O_BACKWARD 6        /* ROSA O dX (packed) and dW in one launch */
 #define ULLIS_HIP_PROBE_LN_FORWARD 7        /* ln2 forward */
 #define ULLIS_HIP_PROBE_LN_BACKWARD 8       /* ln2 backward rows */
 #define ULLIS_HIP_PROBE_COUNT 9

@@ -53,3 +53,48 @@ def test_null_context_is_rejected_without_a_gpu():
     assert rc == -1
     assert lib.ullis_hip_sync(None) == -1
     assert lib.ullis_hip_heron_step(None, None, None, 0, 0.01, None, None, None, None, None) == -1
+
+
+class _FakeLib:
+    """Records the C-ABI calls of the runtime's object lifecycle (no GPU)."""
+
+    def __init__(self):
+        self.calls = []
+
+    def ullis_hip_malloc(self, ctx, nbytes, out):
+        out._obj.value = 4096
+        self.calls.append(("malloc", ctx))
+        return 0
+
+    def ullis_hip_free(self, ctx, ptr):
+        self.calls.append(("free", ctx, ptr))
+        return 0
+
+    def ullis_hip_heron_destroy(self, h):
+        self.calls.append(("heron_destroy", h))
+
+    def ullis_hip_destroy(self, ctx):
+        self.calls.append(("destroy", ctx))
+
+
+def test_runtime_close_frees_dependents_first_and_leaves_them_inert():
+    """Objects that outlive HipRuntime.close (a traceback holding a trainer)
+    must not call into the destroyed context."""
+    import weakref
+
+    from ullis_amd.runtime import DeviceBuffer, HeronTrainer, HipRuntime
+
+    rt = HipRuntime.__new__(HipRuntime)
+    rt.lib, rt.ctx, rt._owned = _FakeLib(), 77, weakref.WeakSet()
+    buf = DeviceBuffer(rt, 64)
+    tr = HeronTrainer.__new__(HeronTrainer)
+    tr.rt, tr.h = rt, 99
+    rt._own(tr)
+    rt.close()
+    assert rt.lib.calls[-1] == ("destroy", 77)
+    assert ("free", 77, 4096) in rt.lib.calls and ("heron_destroy", 99) in rt.lib.calls
+    n = len(rt.lib.calls)
+    buf.free()
+    tr.close()
+    del buf, tr
+    assert len(rt.lib.calls) == n

@@ -577,9 +577,12 @@ __device__ __forceinline__ void for_each_acc(floatx16 (&acc)[TM][TN], int row0, 
     }
 }
 
-// Split-K partial: writes fp32 C for split blockIdx.z to part[z][M][N].
+// Split-K partial: writes fp32 C of split z to part[z][M][N] (z = blockIdx.z
+// in gemm_kernel; the streamed-LDS kernels pass their split via set_split).
 struct EpiPartial {
   float* part;
+  int split = 0;
+  __device__ void set_split(int z) { split = z; }
   template <int TM, int TN>
   __device__ void run(floatx16 (&acc)[TM][TN], int row0, int col0, int lane, int M, int N) {
     float* dst = part + (long)blockIdx.z * M * N;
@@ -589,7 +592,7 @@ struct EpiPartial {
   // 16 consecutive columns of one row (streamed-LDS kernels).
   __device__ void row16(int row, int col, float (&v)[16], int, int M, int N, float*, int, int) {
     if (row >= M) return;
-    float* dst = part + (long)blockIdx.z * M * N + (long)row * N + col;
+    float* dst = part + (long)split * M * N + (long)row * N + col;
     if (col + 16 <= N && N % 8 == 0 && (reinterpret_cast<uintptr_t>(part) & 15u) == 0) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {

@@ -37,6 +37,8 @@
 // in-bounds row; their results are never stored.
 #pragma once
 
+#include <utility>
+
 #include "common.hpp"
 #include "gemm.hpp"
 #include "ops.hpp"
@@ -314,17 +316,41 @@ __device__ __forceinline__ void get16h(const uint16_t* p, int col, int n, bool v
   }
 }
 
+// Epilogues of split-K outputs take the block's K split through set_split(kz).
+template <class E, class = void>
+inline constexpr bool kHasSplit = false;
+template <class E>
+inline constexpr bool kHasSplit<E, decltype(std::declval<E&>().set_split(0))> = true;
+
+#ifndef ULLIS_LDS_SCHED
+#define ULLIS_LDS_SCHED 0
+#endif
+
+// LDS bytes of one block of the streamed-LDS GEMM: the stage ring (which the
+// epilogue reuses) and the operands' extra tables.
+template <int BM, int BN, int BK, int NS, class OA, class OB>
+constexpr int lds_ring_bytes() {
+  constexpr int STAGE = OA::kBytes + OB::kBytes;
+  return NS * STAGE > 4 * kBufFloats * 4 ? NS * STAGE : 4 * kBufFloats * 4;
+}
+template <int BM, int BN, int BK, int NS, class OA, class OB>
+constexpr int lds_smem_bytes() {
+  return lds_ring_bytes<BM, BN, BK, NS, OA, OB>() + OA::kExtra + OB::kExtra;
+}
+
+// One output tile (bid: tile index, kz: K split) of C = A . B^T in the block's
+// LDS (smem: lds_smem_bytes, 1024-byte aligned).
 template <int BM, int BN, int BK, int NS, class OA, class OB, class Epi>
-__device__ __forceinline__ void gemm_lds_body(const OA& a, const OB& b, Epi& epi, int M, int N,
-                                              int K, int k_split) {
+__device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const OA& a,
+                                              const OB& b, Epi& epi, int M, int N, int K,
+                                              int k_split) {
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int STAGE = OA::kBytes + OB::kBytes;
   constexpr int IPS = OA::kInst + OB::kInst;  // loads per wave per stage
   static_assert(TM >= 1 && TN >= 1, "tile too small");
   static_assert(NS >= 2 && IPS * (NS - 2) < 64, "pipeline depth");
-  constexpr int RING = NS * STAGE > 4 * kBufFloats * 4 ? NS * STAGE : 4 * kBufFloats * 4;
-  __shared__ __attribute__((aligned(1024))) char smem[RING + OA::kExtra + OB::kExtra];
+  constexpr int RING = lds_ring_bytes<BM, BN, BK, NS, OA, OB>();
   char* extra_a = smem + RING;
   char* extra_b = extra_a + OA::kExtra;
 
@@ -333,11 +359,21 @@ __device__ __forceinline__ void gemm_lds_body(const OA& a, const OB& b, Epi& epi
   const int wm = wave >> 1, wn = wave & 1;
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   int tm, tn;
-  tile_of_block(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  tile_of_block(bid, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int kbeg = blockIdx.z * k_split;
+  const int kbeg = kz * k_split;
   const int kend = min(K, kbeg + k_split);
   const int nk = kend > kbeg ? (kend - kbeg) / BK : 0;
+#ifndef ULLIS_LDS_ROT
+#define ULLIS_LDS_ROT 0
+#endif
+#if ULLIS_LDS_ROT
+  const int rot = nk > 0 ? (bid >> 3) % nk : 0;
+#else
+  const int rot = 0;
+#endif
+  // K step of iteration kt
+  auto kstep = [&](int kt) { return kt + rot < nk ? kt + rot : kt + rot - nk; };
 
   floatx16 acc[TM][TN];
 #pragma unroll
@@ -349,9 +385,72 @@ __device__ __forceinline__ void gemm_lds_body(const OA& a, const OB& b, Epi& epi
   b.prepare(extra_b, kbeg, kend);
   auto issue = [&](int kt) {
     char* st = smem + (kt % NS) * STAGE;
-    a.issue(st, m0, kbeg + kt * BK, wave, lane);
-    b.issue(st + OA::kBytes, n0, kbeg + kt * BK, wave, lane);
+    a.issue(st, m0, kbeg + kstep(kt) * BK, wave, lane);
+    b.issue(st + OA::kBytes, n0, kbeg + kstep(kt) * BK, wave, lane);
   };
+  constexpr int KS = BK / 16;
+  // all MFMA operand fragments of stage kt (LDS -> registers)
+  auto read = [&](int kt, half8 (&xa)[KS][TM], half8 (&xb)[KS][TN]) {
+    const char* st = smem + (kt % NS) * STAGE;
+    const int k0rel = kstep(kt) * BK;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        xa[ks][i] = a.frag(st, extra_a, wm * WM + i * 32, ks * 16, lane, k0rel);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        xb[ks][j] = b.frag(st + OA::kBytes, extra_b, wn * WN + j * 32, ks * 16, lane, k0rel);
+    }
+  };
+  auto math = [&](const half8 (&xa)[KS][TM], const half8 (&xb)[KS][TN]) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa[ks][i], xb[ks][j], acc[i][j], 0, 0, 0);
+  };
+#if ULLIS_LDS_SCHED == 2
+  static_assert(IPS * (NS - 1) < 64, "pipeline depth");
+  // Register double buffer: the fragments of stage kt + 1 are read from LDS
+  // while the MFMAs of stage kt run. Once a stage's fragments are in
+  // registers its ring slot is free, so NS stages of global loads are issued
+  // ahead of the fragment reads. The K loop is unrolled twice so that the two
+  // fragment sets swap roles without register copies or branches around the
+  // reads (either would make the MFMAs wait for the reads just issued).
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+    if (s < nk) issue(s);
+  // stage kt (kt + 1 < nk): fragments of kt in (ca, cb), read kt + 1 into (na, nb)
+  auto step = [&](int kt, const half8 (&ca)[KS][TM], const half8 (&cb)[KS][TN],
+                  half8 (&na)[KS][TM], half8 (&nb)[KS][TN]) {
+    // stage kt + 1 has landed and every wave holds its stage-kt fragments
+    wait_stages<IPS, NS - 2>(nk - 2 - kt);
+    if (kt + NS < nk) issue(kt + NS);  // into the slot of stage kt
+    read(kt + 1, na, nb);
+    __builtin_amdgcn_sched_barrier(0);
+    math(ca, cb);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  half8 fa[KS][TM], fb[KS][TN], ga[KS][TM], gb[KS][TN];
+  if (nk > 0) {
+    wait_stages<IPS, NS - 1>(nk - 1);  // stage 0 has landed
+    read(0, fa, fb);
+  }
+  int kt = 0;
+  for (; kt + 2 < nk; kt += 2) {
+    step(kt, fa, fb, ga, gb);
+    step(kt + 1, ga, gb, fa, fb);
+  }
+  if (kt + 1 < nk) {
+    step(kt, fa, fb, ga, gb);
+    math(ga, gb);
+  } else if (kt < nk) {
+    math(fa, fb);
+  }
+#else
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
     if (s < nk) issue(s);
@@ -360,8 +459,14 @@ __device__ __forceinline__ void gemm_lds_body(const OA& a, const OB& b, Epi& epi
     // Stage kt is complete once at most the later stages' loads are in flight.
     wait_stages<IPS, NS - 2>(nk - 1 - kt);
     if (kt + NS - 1 < nk) issue(kt + NS - 1);
+#if ULLIS_LDS_SCHED == 1
+    half8 fa[KS][TM], fb[KS][TN];
+    read(kt, fa, fb);
+    __builtin_amdgcn_sched_barrier(0);
+    math(fa, fb);
+#else
     const char* st = smem + (kt % NS) * STAGE;
-    const int k0rel = kt * BK;
+    const int k0rel = kstep(kt) * BK;
 #pragma unroll
     for (int ks = 0; ks < BK; ks += 16) {
       half8 af[TM], bf[TN];
@@ -376,8 +481,11 @@ __device__ __forceinline__ void gemm_lds_body(const OA& a, const OB& b, Epi& epi
         for (int j = 0; j < TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
+#endif
   }
+#endif
   wait_barrier<0>();  // every wave is done reading the ring
+  if constexpr (kHasSplit<Epi>) epi.set_split(kz);
   epilogue_rows(epi, acc, reinterpret_cast<float*>(smem) + wave * kBufFloats, m0 + wm * WM,
                 n0 + wn * WN, lane, M, N);
 }
@@ -385,7 +493,8 @@ __device__ __forceinline__ void gemm_lds_body(const OA& a, const OB& b, Epi& epi
 template <int BM, int BN, int BK, int NS, class OA, class OB, class Epi>
 __global__ __launch_bounds__(256) void gemm_lds_kernel(OA a, OB b, Epi epi, int M, int N, int K,
                                                        int k_split) {
-  gemm_lds_body<BM, BN, BK, NS>(a, b, epi, M, N, K, k_split);
+  __shared__ __attribute__((aligned(1024))) char smem[lds_smem_bytes<BM, BN, BK, NS, OA, OB>()];
+  gemm_lds_body<BM, BN, BK, NS>(smem, blockIdx.x, blockIdx.z, a, b, epi, M, N, K, k_split);
 }
 
 template <class T, int G>
@@ -398,92 +507,40 @@ template <int BM, int BN, int BK, int NS, class OA, class OB, class Epi, int G>
 __global__ __launch_bounds__(256) void gemm_lds_group_kernel(Group<OA, G> a, Group<OB, G> b,
                                                              Group<Epi, G> epi, int M, int N,
                                                              int K, int k_split) {
+  __shared__ __attribute__((aligned(1024))) char smem[lds_smem_bytes<BM, BN, BK, NS, OA, OB>()];
   const int g = blockIdx.y;
-  gemm_lds_body<BM, BN, BK, NS>(a.v[g], b.v[g], epi.v[g], M, N, K, k_split);
+  gemm_lds_body<BM, BN, BK, NS>(smem, blockIdx.x, blockIdx.z, a.v[g], b.v[g], epi.v[g], M, N, K,
+                                k_split);
 }
 
-// K split across the 4 waves of a block: every wave accumulates the whole
-// 64x64 tile (2x2 MFMA blocks, 4 MFMAs per pair of fragment fetches instead of
-// 1) over one 16-wide slice of each BK = 64 stage, and the four partial tiles
-// are summed through LDS in wave order before the epilogue, where wave w owns
-// the 32x32 block (w/2, w%2). Same operands, stages and epilogue interface as
-// gemm_lds_kernel.
-template <int BK, int NS, class OA, class OB, class Epi>
-__global__ __launch_bounds__(256) void gemm_lds_ksplit_kernel(OA a, OB b, Epi epi, int M, int N,
-                                                              int K, int k_split) {
-  constexpr int BM = 64, BN = 64, TM = 2, TN = 2;
-  static_assert(BK == 64, "one 16-wide k slice per wave");
-  constexpr int STAGE = OA::kBytes + OB::kBytes;
-  constexpr int IPS = OA::kInst + OB::kInst;
-  constexpr int RED = 4 * TM * TN * 64 * 16 * 4;  // [block][wave][r][lane] fp32
-  constexpr int RING0 = NS * STAGE > RED ? NS * STAGE : RED;
-  constexpr int RING = RING0 > 4 * kBufFloats * 4 ? RING0 : 4 * kBufFloats * 4;
-  static_assert(NS >= 2 && IPS * (NS - 2) < 64, "pipeline depth");
-  __shared__ __attribute__((aligned(1024))) char smem[RING + OA::kExtra + OB::kExtra];
-  char* extra_a = smem + RING;
-  char* extra_b = extra_a + OA::kExtra;
+// One GEMM of a pair launch: tile config T, operands, epilogue and shape;
+// tiles * splits blocks.
+template <class T, class OA, class OB, class Epi>
+struct LdsProblem {
+  OA a;
+  OB b;
+  Epi epi;
+  int M, N, K, k_split, tiles, blocks;
+};
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  int tm, tn;
-  tile_of_block(blockIdx.x, tiles_m, tiles_n, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
-  const int kbeg = blockIdx.z * k_split;
-  const int kend = min(K, kbeg + k_split);
-  const int nk = kend > kbeg ? (kend - kbeg) / BK : 0;
-
-  floatx16 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = (floatx16){};
-
-  a.prepare(extra_a, kbeg, kend);
-  b.prepare(extra_b, kbeg, kend);
-  auto issue = [&](int kt) {
-    char* st = smem + (kt % NS) * STAGE;
-    a.issue(st, m0, kbeg + kt * BK, wave, lane);
-    b.issue(st + OA::kBytes, n0, kbeg + kt * BK, wave, lane);
-  };
-#pragma unroll
-  for (int s = 0; s < NS - 1; ++s)
-    if (s < nk) issue(s);
-  const int ks = wave * 16;
-  for (int kt = 0; kt < nk; ++kt) {
-    wait_stages<IPS, NS - 2>(nk - 1 - kt);
-    if (kt + NS - 1 < nk) issue(kt + NS - 1);
-    const char* st = smem + (kt % NS) * STAGE;
-    const int k0rel = kt * BK;
-    half8 af[TM], bf[TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i) af[i] = a.frag(st, extra_a, i * 32, ks, lane, k0rel);
-#pragma unroll
-    for (int j = 0; j < TN; ++j) bf[j] = b.frag(st + OA::kBytes, extra_b, j * 32, ks, lane, k0rel);
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+// Two independent GEMMs (possibly of different tile configs and operand
+// kinds) in one launch: blocks [0, p1.blocks) run p1, the rest p2, so the
+// blocks of both share the CUs and their operand streams overlap.
+template <class T1, class OA1, class OB1, class E1, class T2, class OA2, class OB2, class E2>
+__global__ __launch_bounds__(256) void gemm_lds_pair_kernel(LdsProblem<T1, OA1, OB1, E1> p1,
+                                                            LdsProblem<T2, OA2, OB2, E2> p2) {
+  constexpr int S1 = lds_smem_bytes<T1::bm, T1::bn, T1::bk, T1::ns, OA1, OB1>();
+  constexpr int S2 = lds_smem_bytes<T2::bm, T2::bn, T2::bk, T2::ns, OA2, OB2>();
+  __shared__ __attribute__((aligned(1024))) char smem[S1 > S2 ? S1 : S2];
+  const int bid = blockIdx.x;
+  if (bid < p1.blocks) {
+    gemm_lds_body<T1::bm, T1::bn, T1::bk, T1::ns>(smem, bid % p1.tiles, bid / p1.tiles, p1.a, p1.b,
+                                                  p1.epi, p1.M, p1.N, p1.K, p1.k_split);
+  } else {
+    const int b2 = bid - p1.blocks;
+    gemm_lds_body<T2::bm, T2::bn, T2::bk, T2::ns>(smem, b2 % p2.tiles, b2 / p2.tiles, p2.a, p2.b,
+                                                  p2.epi, p2.M, p2.N, p2.K, p2.k_split);
   }
-  wait_barrier<0>();  // every wave is done reading the ring
-  float* red = reinterpret_cast<float*>(smem);
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) red[(((i * TN + j) * 4 + wave) * 16 + r) * 64 + lane] = acc[i][j][r];
-  wait_barrier<0>();
-  floatx16 sum[1][1];
-  sum[0][0] = (floatx16){};
-#pragma unroll
-  for (int v = 0; v < 4; ++v)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) sum[0][0][r] += red[((wave * 4 + v) * 16 + r) * 64 + lane];
-  wait_barrier<0>();  // the epilogue buffers reuse the reduction area
-  epilogue_rows(epi, sum, reinterpret_cast<float*>(smem) + wave * kBufFloats,
-                m0 + 32 * (wave >> 1), n0 + 32 * (wave & 1), lane, M, N);
 }
 
 // ------------------------------------------------------------ host dispatch
@@ -541,6 +598,32 @@ hipError_t launch_lds(hipStream_t s, const OA& a, const OB& b, const Epi& epi, l
   launch((gemm_lds_kernel<T::bm, T::bn, T::bk, T::ns, OA, OB, Epi>),
          dim3((unsigned)tiles, 1, splits), dim3(kThreads), 0, s, a, b, epi, (int)M, (int)N, (int)K,
          ks);
+  return hipGetLastError();
+}
+
+template <class T, class OA, class OB, class Epi>
+LdsProblem<T, OA, OB, Epi> lds_problem(const OA& a, const OB& b, const Epi& epi, long M, long N,
+                                       long K, int splits) {
+  if (splits < 1) splits = 1;
+  const int tiles = (int)(cdiv(M, T::bm) * cdiv(N, T::bn));
+  const int ks = (int)(cdiv(cdiv(K, splits), T::bk) * T::bk);
+  return LdsProblem<T, OA, OB, Epi>{a, b, epi, (int)M, (int)N, (int)K, ks, tiles, tiles * splits};
+}
+
+template <class T, class OA, class OB, class Epi>
+hipError_t launch_lds_problem(hipStream_t s, const LdsProblem<T, OA, OB, Epi>& p) {
+  launch((gemm_lds_kernel<T::bm, T::bn, T::bk, T::ns, OA, OB, Epi>),
+         dim3((unsigned)p.tiles, 1, (unsigned)(p.blocks / p.tiles)), dim3(kThreads), 0, s, p.a, p.b,
+         p.epi, p.M, p.N, p.K, p.k_split);
+  return hipGetLastError();
+}
+
+// Shapes must fit int32 (lds_problem's callers check M, N, K).
+template <class T1, class OA1, class OB1, class E1, class T2, class OA2, class OB2, class E2>
+hipError_t launch_lds_pair(hipStream_t s, const LdsProblem<T1, OA1, OB1, E1>& p1,
+                           const LdsProblem<T2, OA2, OB2, E2>& p2) {
+  launch((gemm_lds_pair_kernel<T1, OA1, OB1, E1, T2, OA2, OB2, E2>),
+         dim3((unsigned)(p1.blocks + p2.blocks)), dim3(kThreads), 0, s, p1, p2);
   return hipGetLastError();
 }
 

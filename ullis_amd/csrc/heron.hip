@@ -650,22 +650,25 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
     const float* ar = h->after_rosa + l * nd;
     const long pc = (long)h->nb_col * D;
 
-    // CMix backward (src/model.rs:1145-1177)
-    PROBED(ULLIS_HIP_PROBE_VALUE_INPUT_GRAD,
-           fp16_backward_input(s, GradIn{h->g_x, slot_in, h->gx16}, R, F, D, b.value, nullptr, key,
-                               h->gk16),
-           "value input grad + relu2 bwd");
-    STEP(fp16_weight_grad_partials(s, GradIn{h->g_x, slot_in, h->gx16}, r2, R, F, D,
-                                   h->splits_value, h->gp_value + l * h->splits_value * D * F),
-         "value weight grad");
-    PROBED(ULLIS_HIP_PROBE_KEY_INPUT_GRAD,
-           packed_backward_input(s, GradIn{nullptr, slot_in}, h->gk16, R, D, F, b.key.bits_t,
-                                 b.key.scale, h->g_a, nullptr, 0),
-           "key input grad");
-    PROBED(ULLIS_HIP_PROBE_KEY_WEIGHT_GRAD,
-           packed_weight_grad_partials(s, GradIn{nullptr, slot_in}, h->gk16, sh, R, D, F,
-                                       h->splits_key, h->gp_key + l * h->splits_key * F * D),
-           "key weight grad");
+    // CMix backward (src/model.rs:1145-1177): value input gradient (+ ReLU^2
+    // backward into gk16) with the value weight gradient, then the key input
+    // gradient with the key weight gradient
+    {
+      const GradIn gx{h->g_x, slot_in, h->gx16};
+      PROBED(ULLIS_HIP_PROBE_VALUE_BACKWARD,
+             fp16_backward_pair(s, Fp16DxArgs{gx, R, F, D, b.value, nullptr, key, h->gk16},
+                                WeightGradArgs{gx, nullptr, r2, R, F, D, h->splits_value,
+                                               h->gp_value + l * h->splits_value * D * F}),
+             "value backward");
+      const GradIn gk{nullptr, slot_in};
+      PROBED(ULLIS_HIP_PROBE_KEY_BACKWARD,
+             packed_backward_pair(s,
+                                  PackedDxArgs{gk, h->gk16, R, D, F, b.key.bits_t, b.key.scale,
+                                               h->g_a, nullptr, 0},
+                                  WeightGradArgs{gk, h->gk16, sh, R, D, F, h->splits_key,
+                                                 h->gp_key + l * h->splits_key * F * D}),
+             "key backward");
+    }
     STEP(time_shift_mix_backward(s, h->g_a, ln2, b.cx_k, R, T, D, h->g_b, h->pt_mix + l * pc, &nb),
          "mix bwd");
     if (nb != h->nb_col) return c->fail(ULLIS_HIP_ERR_RUNTIME, "mix backward partial count");
@@ -682,16 +685,20 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
          "o g_bias + g_x fp16");
     if (nb != h->nb_col) return c->fail(ULLIS_HIP_ERR_RUNTIME, "o bias partial count");
 
-    // ROSA O stop-grad backward (src/model.rs:1491-1522)
-    STEP(packed_backward_input(s, GradIn{h->g_x, slot_mid, h->gx16}, nullptr, R, D, D, b.o.bits_t,
-                               b.o.scale, h->g_a, nullptr, 0),
-         "o input grad");
+    // ROSA O stop-grad backward (src/model.rs:1491-1522): O input and weight
+    // gradients, then the e gradient from g_y
+    {
+      const GradIn gx{h->g_x, slot_mid, h->gx16};
+      PROBED(ULLIS_HIP_PROBE_O_BACKWARD,
+             packed_backward_pair(s,
+                                  PackedDxArgs{gx, nullptr, R, D, D, b.o.bits_t, b.o.scale, h->g_a,
+                                               nullptr, 0},
+                                  WeightGradArgs{gx, nullptr, h->y16 + l * nd, R, D, D, h->splits_o,
+                                                 h->gp_o + l * h->splits_o * D * D}),
+             "o backward");
+    }
     STEP(column_sum_partials(s, h->g_a, h->idx_rm + l * nd, R, D, h->pt_e + l * pc, &nb), "g_e");
     if (nb != h->nb_col) return c->fail(ULLIS_HIP_ERR_RUNTIME, "e gradient partial count");
-    STEP(packed_weight_grad_partials(s, GradIn{h->g_x, slot_mid, h->gx16}, nullptr,
-                                     h->y16 + l * nd, R, D, D, h->splits_o,
-                                     h->gp_o + l * h->splits_o * D * D),
-         "o weight grad");
 
     if (b.has_ln0) {  // (src/model.rs:2978-2982)
       STEP(layer_norm_backward_rows(s, x_emb, h->g_x, R, D, b.ln0.w, g_emb, 0, nullptr, h->pt_ln0,

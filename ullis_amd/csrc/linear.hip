@@ -426,19 +426,65 @@ hipError_t packed_forward_bits3(hipStream_t s, const uint16_t* const x[3], long 
   return hipSuccess;
 }
 
+namespace {
+
+// Streamed-LDS problems of the backward GEMMs: each calls f(problem) and
+// returns true when the operands allow the LDS kernels (false: f not called).
+template <class F>
+bool packed_dx_lds(const PackedDxArgs& d, hipError_t* err, F&& f) {
+  const uint16_t* g16 = d.gy16 ? d.gy16 : d.gy32.p16;
+  if (!lds::mk_ok(g16, d.out) || d.out > 8192) return false;
+  EpiStoreF32 epi{d.gx, d.gy32.amax, d.out_mul, d.accumulate};
+  return lds::with_lds(d.rows, d.in, d.out, 1, err, [&](auto t) {
+    using T = decltype(t);
+    lds::OpMK<T::bm, T::bk> a{reinterpret_cast<const half_t*>(g16), d.out, (int)d.rows};
+    lds::OpBits<T::bn, T::bk, true> b{d.bits_t, d.out / 32, (int)d.in, d.scale, 0};
+    return f(lds::lds_problem<T>(a, b, epi, d.rows, d.in, d.out, 1));
+  });
+}
+
+template <class F>
+bool weight_grad_lds(const WeightGradArgs& d, hipError_t* err, F&& f) {
+  // G[out][in]: M = out, N = in, K = rows; both operands are row-contiguous.
+  const uint16_t* g16 = d.gy16 ? d.gy16 : d.gy32.p16;
+  if (!lds::km_ok(g16, d.out, d.out) || !lds::km_ok(d.x16, d.in, d.in)) return false;
+  EpiPartial epi{d.part};
+  return lds::with_lds(d.out, d.in, d.rows, d.splits, err, [&](auto t) {
+    using T = decltype(t);
+    lds::OpKM<T::bm, T::bk> a{reinterpret_cast<const half_t*>(g16), d.out, (int)d.out};
+    lds::OpKM<T::bn, T::bk> b{reinterpret_cast<const half_t*>(d.x16), d.in, (int)d.in};
+    return f(lds::lds_problem<T>(a, b, epi, d.out, d.in, d.rows, d.splits));
+  });
+}
+
+template <class F>
+bool fp16_dx_lds(const Fp16DxArgs& d, hipError_t* err, F&& f) {
+  // gX[rows][in] = gY[rows][out] . W[out][in]: B(n = i, k = o) = W[o*in + i].
+  if (!lds::mk_ok(d.gy32.p16, d.out) || !lds::km_ok(d.w, d.in, d.in)) return false;
+  return lds::with_lds(d.rows, d.in, d.out, 1, err, [&](auto t) {
+    using T = decltype(t);
+    lds::OpMK<T::bm, T::bk> a{reinterpret_cast<const half_t*>(d.gy32.p16), d.out, (int)d.rows};
+    lds::OpKM<T::bn, T::bk> b{reinterpret_cast<const half_t*>(d.w), d.in, (int)d.in};
+    if (d.gk16)
+      return f(lds::lds_problem<T>(a, b, EpiRelu2Bwd{d.key16, d.gk16}, d.rows, d.in, d.out, 1));
+    return f(lds::lds_problem<T>(a, b, EpiStoreF32{d.gx, d.gy32.amax, nullptr, 0}, d.rows, d.in,
+                                 d.out, 1));
+  }, 240);
+}
+
+auto launch_one(hipStream_t s) {
+  return [s](const auto& p) { return lds::launch_lds_problem(s, p); };
+}
+
+}  // namespace
+
 hipError_t packed_backward_input(hipStream_t s, GradIn gy32, const uint16_t* gy16, long rows,
                                  long in, long out, const uint32_t* bits_t, const uint16_t* scale,
                                  float* gx, const float* out_mul, int accumulate) {
   EpiStoreF32 epi{gx, gy32.amax, out_mul, accumulate};
-  const uint16_t* g16 = gy16 ? gy16 : gy32.p16;
   hipError_t err = hipSuccess;
-  if (lds::mk_ok(g16, out) && out <= 8192 &&
-      lds::with_lds(rows, in, out, 1, &err, [&](auto t) {
-        using T = decltype(t);
-        lds::OpMK<T::bm, T::bk> a{reinterpret_cast<const half_t*>(g16), out, (int)rows};
-        lds::OpBits<T::bn, T::bk, true> b{bits_t, out / 32, (int)in, scale, 0};
-        return lds::launch_lds<T>(s, a, b, epi, rows, in, out, 1);
-      }))
+  if (packed_dx_lds(PackedDxArgs{gy32, gy16, rows, in, out, bits_t, scale, gx, out_mul, accumulate},
+                    &err, launch_one(s)))
     return err;
   return with_tile(rows, in, [&](auto t) {
     using T = decltype(t);
@@ -481,16 +527,9 @@ hipError_t packed_weight_grad_partials(hipStream_t s, GradIn gy32, const uint16_
                                        const uint16_t* x16, long rows, long in, long out,
                                        int splits, float* part) {
   EpiPartial epi{part};
-  // G[out][in]: M = out, N = in, K = rows; both operands are row-contiguous.
-  const uint16_t* g16 = gy16 ? gy16 : gy32.p16;
   hipError_t err = hipSuccess;
-  if (lds::km_ok(g16, out, out) && lds::km_ok(x16, in, in) &&
-      lds::with_lds(out, in, rows, splits, &err, [&](auto t) {
-        using T = decltype(t);
-        lds::OpKM<T::bm, T::bk> a{reinterpret_cast<const half_t*>(g16), out, (int)out};
-        lds::OpKM<T::bn, T::bk> b{reinterpret_cast<const half_t*>(x16), in, (int)in};
-        return lds::launch_lds<T>(s, a, b, epi, out, in, rows, splits);
-      }))
+  if (weight_grad_lds(WeightGradArgs{gy32, gy16, x16, rows, in, out, splits, part}, &err,
+                      launch_one(s)))
     return err;
   return with_tile(out, in, [&](auto t) {
     using T = decltype(t);
@@ -586,16 +625,8 @@ hipError_t fp16_forward(hipStream_t s, const void* x, int x_dtype, long rows, lo
 hipError_t fp16_backward_input(hipStream_t s, GradIn gy32, long rows, long in, long out,
                                const uint16_t* w, float* gx, const uint16_t* key16,
                                uint16_t* gk16) {
-  // gX[rows][in] = gY[rows][out] . W[out][in]: B(n = i, k = o) = W[o*in + i].
   hipError_t err = hipSuccess;
-  if (lds::mk_ok(gy32.p16, out) && lds::km_ok(w, in, in) &&
-      lds::with_lds(rows, in, out, 1, &err, [&](auto t) {
-        using T = decltype(t);
-        lds::OpMK<T::bm, T::bk> a{reinterpret_cast<const half_t*>(gy32.p16), out, (int)rows};
-        lds::OpKM<T::bn, T::bk> b{reinterpret_cast<const half_t*>(w), in, (int)in};
-        if (gk16) return lds::launch_lds<T>(s, a, b, EpiRelu2Bwd{key16, gk16}, rows, in, out, 1);
-        return lds::launch_lds<T>(s, a, b, EpiStoreF32{gx, gy32.amax, nullptr, 0}, rows, in, out, 1);
-      }, 240))
+  if (fp16_dx_lds(Fp16DxArgs{gy32, rows, in, out, w, gx, key16, gk16}, &err, launch_one(s)))
     return err;
   return with_tile(rows, in, [&](auto t) {
     using T = decltype(t);
@@ -613,6 +644,46 @@ hipError_t fp16_backward_input(hipStream_t s, GradIn gy32, long rows, long in, l
 hipError_t fp16_weight_grad_partials(hipStream_t s, GradIn gy32, const uint16_t* x16, long rows,
                                      long in, long out, int splits, float* part) {
   return packed_weight_grad_partials(s, gy32, nullptr, x16, rows, in, out, splits, part);
+}
+
+// Both GEMMs of a backward in one launch when both take the streamed-LDS path
+// (their blocks share the CUs); otherwise the two separate launches.
+hipError_t packed_backward_pair(hipStream_t s, const PackedDxArgs& dx, const WeightGradArgs& dw) {
+  hipError_t err = hipSuccess;
+  bool dw_ok = false;
+  if (packed_dx_lds(dx, &err, [&](const auto& p1) {
+        hipError_t e2 = hipSuccess;
+        dw_ok = weight_grad_lds(dw, &e2, [&](const auto& p2) {
+          return lds::launch_lds_pair(s, p1, p2);
+        });
+        return dw_ok ? e2 : hipSuccess;
+      }) &&
+      dw_ok)
+    return err;
+  if ((err = packed_backward_input(s, dx.gy32, dx.gy16, dx.rows, dx.in, dx.out, dx.bits_t,
+                                   dx.scale, dx.gx, dx.out_mul, dx.accumulate)) != hipSuccess)
+    return err;
+  return packed_weight_grad_partials(s, dw.gy32, dw.gy16, dw.x16, dw.rows, dw.in, dw.out,
+                                     dw.splits, dw.part);
+}
+
+hipError_t fp16_backward_pair(hipStream_t s, const Fp16DxArgs& dx, const WeightGradArgs& dw) {
+  hipError_t err = hipSuccess;
+  bool dw_ok = false;
+  if (fp16_dx_lds(dx, &err, [&](const auto& p1) {
+        hipError_t e2 = hipSuccess;
+        dw_ok = weight_grad_lds(dw, &e2, [&](const auto& p2) {
+          return lds::launch_lds_pair(s, p1, p2);
+        });
+        return dw_ok ? e2 : hipSuccess;
+      }) &&
+      dw_ok)
+    return err;
+  if ((err = fp16_backward_input(s, dx.gy32, dx.rows, dx.in, dx.out, dx.w, dx.gx, dx.key16,
+                                 dx.gk16)) != hipSuccess)
+    return err;
+  return packed_weight_grad_partials(s, dw.gy32, dw.gy16, dw.x16, dw.rows, dw.in, dw.out,
+                                     dw.splits, dw.part);
 }
 
 hipError_t fp16_weight_finish(hipStream_t s, const float* part, int splits, long out, long in,

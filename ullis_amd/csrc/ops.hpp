@@ -84,6 +84,40 @@ struct PackedFinish {
   uint32_t* bits_new = nullptr;
 };
 hipError_t packed_weight_finish(hipStream_t s, const PackedFinish& f);
+
+// Arguments of packed_backward_input / packed_weight_grad_partials /
+// fp16_backward_input, for the paired launches below.
+struct PackedDxArgs {
+  GradIn gy32;
+  const uint16_t* gy16;
+  long rows, in, out;
+  const uint32_t* bits_t;
+  const uint16_t* scale;
+  float* gx;
+  const float* out_mul;
+  int accumulate;
+};
+struct WeightGradArgs {
+  GradIn gy32;
+  const uint16_t* gy16;
+  const uint16_t* x16;
+  long rows, in, out;
+  int splits;
+  float* part;
+};
+struct Fp16DxArgs {
+  GradIn gy32;
+  long rows, in, out;
+  const uint16_t* w;
+  float* gx;
+  const uint16_t* key16;
+  uint16_t* gk16;
+};
+// Input and weight gradient of one layer in a single launch when both GEMMs
+// take the streamed-LDS kernels (the blocks of both share the CUs), else the
+// two launches of the functions above; same results either way.
+hipError_t packed_backward_pair(hipStream_t s, const PackedDxArgs& dx, const WeightGradArgs& dw);
+hipError_t fp16_backward_pair(hipStream_t s, const Fp16DxArgs& dx, const WeightGradArgs& dw);
 // in % 32 == 0 and 16-byte aligned part / latent / latent_res / g_w: the
 // finish runs one wave per row with vector loads.
 bool packed_finish_wave_ok(const PackedFinish& f);

@@ -9,6 +9,7 @@ and bench.py use. Shape rules and error texts come from the library.
 from __future__ import annotations
 
 import ctypes as C
+import weakref
 from dataclasses import dataclass
 
 import numpy as np
@@ -32,6 +33,7 @@ class DeviceBuffer:
         ptr = C.c_void_p()
         rt._check(rt.lib.ullis_hip_malloc(rt.ctx, max(self.nbytes, 4), C.byref(ptr)), "malloc")
         self.ptr = ptr.value
+        rt._own(self)
 
     def upload(self, arr: np.ndarray) -> "DeviceBuffer":
         a = np.ascontiguousarray(arr)
@@ -52,9 +54,12 @@ class DeviceBuffer:
         return out
 
     def free(self):
-        if self.ptr:
+        # after the runtime is closed the allocation is already gone
+        if self.ptr and self.rt.ctx:
             self.rt.lib.ullis_hip_free(self.rt.ctx, self.ptr)
-            self.ptr = None
+        self.ptr = None
+
+    close = free
 
     def __del__(self):
         try:
@@ -81,9 +86,17 @@ class HipRuntime:
         if rc != 0:
             raise HipError(f"ullis_hip_create failed ({rc}): no usable HIP device {device}")
         self.ctx = ctx.value
+        self._owned = weakref.WeakSet()  # live buffers and trainers on this context
+
+    def _own(self, obj):
+        self._owned.add(obj)
 
     def close(self):
+        """Frees every live buffer and trainer of this runtime, then the context;
+        objects that outlive it (e.g. held by a traceback) become inert."""
         if self.ctx:
+            for obj in list(self._owned):
+                obj.close()
             self.lib.ullis_hip_destroy(self.ctx)
             self.ctx = None
 
@@ -337,11 +350,12 @@ class HeronTrainer:
         self.arena_ptr, self.arena_bytes = ptr.value, nbytes.value
         self.layout, total = heron_layout(self._dims, rt.lib)
         assert total == self.arena_bytes
+        rt._own(self)
 
     def close(self):
-        if self.h:
+        if self.h and self.rt.ctx:
             self.rt.lib.ullis_hip_heron_destroy(self.h)
-            self.h = None
+        self.h = None
 
     def __del__(self):
         try:
@@ -357,9 +371,10 @@ class HeronTrainer:
             "key_forward": (1, "mfma", 2.0 * r * d * f, "packed +-1 GEMM: CMix key fwd + ReLU^2"),
             "value_forward": (2, "mfma", 2.0 * r * f * d, "fp16 GEMM: CMix value fwd + residual"),
             "head_ce": (3, "mfma", 3 * 2.0 * r * d * v, "head + streamed CE (whole op)"),
-            "value_input_grad": (4, "mfma", 2.0 * r * d * f, "fp16 GEMM: value dX + ReLU^2 bwd"),
-            "key_input_grad": (5, "mfma", 2.0 * r * f * d, "packed +-1 GEMM: key dX"),
-            "key_weight_grad": (6, "mfma", 2.0 * r * f * d, "key dW GEMM"),
+            "value_backward": (4, "mfma", 2 * 2.0 * r * d * f,
+                               "paired GEMMs: value dX + ReLU^2 bwd, value dW"),
+            "key_backward": (5, "mfma", 2 * 2.0 * r * f * d, "paired GEMMs: packed key dX, key dW"),
+            "o_backward": (6, "mfma", 2 * 2.0 * r * d * d, "paired GEMMs: packed O dX, O dW"),
             "ln_forward": (7, "hbm", r * d * (4 + 2) + 4.0 * d, "LayerNorm fwd (ln2)"),
             "ln_backward": (8, "hbm", r * d * 16 + 2.0 * d, "LayerNorm bwd rows (ln2, += g_x)"),
         }
