@@ -292,12 +292,11 @@ __global__ __launch_bounds__(1024) void ce_mean_kernel(const float* row_loss, lo
 }
 
 long chunk_cols(long vocab, long d) {
-  // Enough weight-gradient tiles (Vc x d, 64x64) to fill the GPU, multiple of 32.
-  long vc = 2048;
-  if (d < 512) vc = 4096;
-  if (vc > vocab) vc = vocab;
-  vc = cdiv(vc, 32) * 32;
-  return vc;
+  // The whole vocabulary up to 8192 columns (the scaled-bits operand of the
+  // input-gradient GEMM keeps the scales of its k range in LDS), multiple of 32.
+  (void)d;
+  const long vc = vocab < 8192 ? vocab : 8192;
+  return cdiv(vc, 32) * 32;
 }
 
 struct Ws {
@@ -408,16 +407,14 @@ hipError_t head_ce(hipStream_t s, const HeadCe& h, void* workspace) {
     EpiCeGrad gr{h.scale + c0, h.bias ? h.bias + c0 : nullptr, h.targets, h.ignore_id, h.time, c0,
                  V, w.lse, w.gy16, w.part_bias};
     if ((e = logits_gemm(s, h.hidden16, rows, d, bits_rows, n, gr)) != hipSuccess) return e;
-    // g_hidden (+)= gscale * gy_chunk . (scale * S)_chunk
-    if ((e = packed_backward_input_ex(s, w.gy16, n, rows, d, n, h.bits_t, V, c0, h.scale,
-                                      h.g_hidden, gscale, ci > 0)) != hipSuccess)
-      return e;
-    // G_chunk = gy_chunk^T . hidden, then the latent step for these head rows
+    // g_hidden (+)= gscale * gy_chunk . (scale * S)_chunk and G_chunk =
+    // gy_chunk^T . hidden in one launch, then the latent step for these rows
     const int sp = dw_splits(vc, d, rows);  // the workspace holds this many [vc][d] partials
     float* gp = h.gpart_all ? h.gpart_all + ci * sp * vc * d : w.gpart;
-    if ((e = packed_weight_grad_partials(s, GradIn{nullptr, nullptr}, w.gy16, h.hidden16, rows, d,
-                                         n, sp, gp)) != hipSuccess)
-      return e;
+    const PackedDxArgs dx{GradIn{nullptr, nullptr}, w.gy16, rows, d, n, h.bits_t, h.scale,
+                          h.g_hidden, gscale, ci > 0 ? 1 : 0, n, V, c0};
+    const WeightGradArgs dw{GradIn{nullptr, nullptr}, w.gy16, h.hidden16, rows, d, n, sp, gp};
+    if ((e = packed_backward_pair(s, dx, dw)) != hipSuccess) return e;
     if (h.gpart_all) continue;  // deferred: the caller runs the update
     PackedFinish f;
     f.part = w.gpart;

@@ -430,15 +430,20 @@ namespace {
 
 // Streamed-LDS problems of the backward GEMMs: each calls f(problem) and
 // returns true when the operands allow the LDS kernels (false: f not called).
+long ldgy_of(const PackedDxArgs& d) { return d.ldgy ? d.ldgy : d.out; }
+long ldb_of(const PackedDxArgs& d) { return d.ldb ? d.ldb : d.out; }
+
 template <class F>
 bool packed_dx_lds(const PackedDxArgs& d, hipError_t* err, F&& f) {
   const uint16_t* g16 = d.gy16 ? d.gy16 : d.gy32.p16;
-  if (!lds::mk_ok(g16, d.out) || d.out > 8192) return false;
+  const long ldgy = ldgy_of(d), ldb = ldb_of(d);
+  // the scaled-bits operand keeps the scales of the block's k range in LDS
+  if (!lds::mk_ok(g16, ldgy) || d.out > 8192 || ldb % 32 != 0 || d.kofs % 32 != 0) return false;
   EpiStoreF32 epi{d.gx, d.gy32.amax, d.out_mul, d.accumulate};
   return lds::with_lds(d.rows, d.in, d.out, 1, err, [&](auto t) {
     using T = decltype(t);
-    lds::OpMK<T::bm, T::bk> a{reinterpret_cast<const half_t*>(g16), d.out, (int)d.rows};
-    lds::OpBits<T::bn, T::bk, true> b{d.bits_t, d.out / 32, (int)d.in, d.scale, 0};
+    lds::OpMK<T::bm, T::bk> a{reinterpret_cast<const half_t*>(g16), ldgy, (int)d.rows};
+    lds::OpBits<T::bn, T::bk, true> b{d.bits_t, ldb / 32, (int)d.in, d.scale, (int)d.kofs};
     return f(lds::lds_problem<T>(a, b, epi, d.rows, d.in, d.out, 1));
   });
 }
@@ -478,24 +483,31 @@ auto launch_one(hipStream_t s) {
 
 }  // namespace
 
+// gx (+)= gy . (scale * S) over the window of PackedDxArgs.
+hipError_t packed_dx(hipStream_t s, const PackedDxArgs& d) {
+  hipError_t err = hipSuccess;
+  if (packed_dx_lds(d, &err, launch_one(s))) return err;
+  const long ldgy = ldgy_of(d), ldb = ldb_of(d);
+  EpiStoreF32 epi{d.gx, d.gy32.amax, d.out_mul, d.accumulate};
+  return with_tile(d.rows, d.in, [&](auto t) {
+    using T = decltype(t);
+    LoadBits<T::bn, T::bk, true> lb{d.bits_t, ldb, d.kofs, d.scale,
+                                    bits_aligned(ldb, d.kofs, d.scale)};
+    if (d.gy16) {
+      LoadF16K<T::bm, T::bk> la{reinterpret_cast<const half_t*>(d.gy16), ldgy,
+                                vec_ok_f16(d.gy16, ldgy)};
+      return launch_gemm<T>(s, la, lb, epi, d.rows, d.in, d.out, 1);
+    }
+    LoadF32K<T::bm, T::bk> la{d.gy32.p, ldgy, vec_ok_f32(d.gy32.p, ldgy), d.gy32.amax, 1.0f};
+    return launch_gemm<T>(s, la, lb, epi, d.rows, d.in, d.out, 1);
+  });
+}
+
 hipError_t packed_backward_input(hipStream_t s, GradIn gy32, const uint16_t* gy16, long rows,
                                  long in, long out, const uint32_t* bits_t, const uint16_t* scale,
                                  float* gx, const float* out_mul, int accumulate) {
-  EpiStoreF32 epi{gx, gy32.amax, out_mul, accumulate};
-  hipError_t err = hipSuccess;
-  if (packed_dx_lds(PackedDxArgs{gy32, gy16, rows, in, out, bits_t, scale, gx, out_mul, accumulate},
-                    &err, launch_one(s)))
-    return err;
-  return with_tile(rows, in, [&](auto t) {
-    using T = decltype(t);
-    LoadBits<T::bn, T::bk, true> lb{bits_t, out, 0, scale, bits_aligned(out, 0, scale)};
-    if (gy16) {
-      LoadF16K<T::bm, T::bk> la{reinterpret_cast<const half_t*>(gy16), out, vec_ok_f16(gy16, out)};
-      return launch_gemm<T>(s, la, lb, epi, rows, in, out, 1);
-    }
-    LoadF32K<T::bm, T::bk> la{gy32.p, out, vec_ok_f32(gy32.p, out), gy32.amax, 1.0f};
-    return launch_gemm<T>(s, la, lb, epi, rows, in, out, 1);
-  });
+  return packed_dx(s, PackedDxArgs{gy32, gy16, rows, in, out, bits_t, scale, gx, out_mul,
+                                   accumulate});
 }
 
 // Input gradient over a column window of the output features: contraction
@@ -505,22 +517,8 @@ hipError_t packed_backward_input_ex(hipStream_t s, const uint16_t* gy16, long ld
                                     long in, long k_len, const uint32_t* bits_t, long ldb,
                                     long kofs, const uint16_t* scale, float* gx,
                                     const float* out_mul, int accumulate) {
-  EpiStoreF32 epi{gx, nullptr, out_mul, accumulate};
-  hipError_t err = hipSuccess;
-  if (lds::mk_ok(gy16, ldgy) && ldb % 32 == 0 && kofs % 32 == 0 && k_len <= 8192 &&
-      lds::with_lds(rows, in, k_len, 1, &err, [&](auto t) {
-        using T = decltype(t);
-        lds::OpMK<T::bm, T::bk> a{reinterpret_cast<const half_t*>(gy16), ldgy, (int)rows};
-        lds::OpBits<T::bn, T::bk, true> b{bits_t, ldb / 32, (int)in, scale, (int)kofs};
-        return lds::launch_lds<T>(s, a, b, epi, rows, in, k_len, 1);
-      }))
-    return err;
-  return with_tile(rows, in, [&](auto t) {
-    using T = decltype(t);
-    LoadBits<T::bn, T::bk, true> lb{bits_t, ldb, kofs, scale, bits_aligned(ldb, kofs, scale)};
-    LoadF16K<T::bm, T::bk> la{reinterpret_cast<const half_t*>(gy16), ldgy, vec_ok_f16(gy16, ldgy)};
-    return launch_gemm<T>(s, la, lb, epi, rows, in, k_len, 1);
-  });
+  return packed_dx(s, PackedDxArgs{GradIn{nullptr, nullptr}, gy16, rows, in, k_len, bits_t, scale,
+                                   gx, out_mul, accumulate, ldgy, ldb, kofs});
 }
 
 hipError_t packed_weight_grad_partials(hipStream_t s, GradIn gy32, const uint16_t* gy16,
@@ -660,9 +658,7 @@ hipError_t packed_backward_pair(hipStream_t s, const PackedDxArgs& dx, const Wei
       }) &&
       dw_ok)
     return err;
-  if ((err = packed_backward_input(s, dx.gy32, dx.gy16, dx.rows, dx.in, dx.out, dx.bits_t,
-                                   dx.scale, dx.gx, dx.out_mul, dx.accumulate)) != hipSuccess)
-    return err;
+  if ((err = packed_dx(s, dx)) != hipSuccess) return err;
   return packed_weight_grad_partials(s, dw.gy32, dw.gy16, dw.x16, dw.rows, dw.in, dw.out,
                                      dw.splits, dw.part);
 }

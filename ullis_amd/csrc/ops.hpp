@@ -87,6 +87,9 @@ hipError_t packed_weight_finish(hipStream_t s, const PackedFinish& f);
 
 // Arguments of packed_backward_input / packed_weight_grad_partials /
 // fp16_backward_input, for the paired launches below.
+// out is the contraction length. A column window of a wider layer (the
+// streamed head): gy16 rows of ldgy halves, bits_t rows of ldb bits, k offset
+// kofs into bits_t columns and scale (0: ldgy = ldb = out, kofs = 0).
 struct PackedDxArgs {
   GradIn gy32;
   const uint16_t* gy16;
@@ -96,6 +99,7 @@ struct PackedDxArgs {
   float* gx;
   const float* out_mul;
   int accumulate;
+  long ldgy = 0, ldb = 0, kofs = 0;
 };
 struct WeightGradArgs {
   GradIn gy32;
