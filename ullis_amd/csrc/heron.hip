@@ -685,20 +685,21 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
          "o g_bias + g_x fp16");
     if (nb != h->nb_col) return c->fail(ULLIS_HIP_ERR_RUNTIME, "o bias partial count");
 
-    // ROSA O stop-grad backward (src/model.rs:1491-1522): O input and weight
-    // gradients, then the e gradient from g_y
+    // ROSA O stop-grad backward (src/model.rs:1491-1522): the O weight
+    // gradient, and the O input gradient g_y reduced straight to the e
+    // gradient partials (g_e = column sums of g_y * (2 idx - 1); with
+    // stop_grad_bits nothing else reads g_y)
     {
       const GradIn gx{h->g_x, slot_mid, h->gx16};
+      PackedDxArgs dx{gx, nullptr, R, D, D, b.o.bits_t, b.o.scale, h->g_a, nullptr, 0};
+      dx.sign_idx = h->idx_rm + l * nd;
+      dx.col_part = h->pt_e + l * pc;  // column_partial_blocks(R) groups of 16 rows
       PROBED(ULLIS_HIP_PROBE_O_BACKWARD,
-             packed_backward_pair(s,
-                                  PackedDxArgs{gx, nullptr, R, D, D, b.o.bits_t, b.o.scale, h->g_a,
-                                               nullptr, 0},
+             packed_backward_pair(s, dx,
                                   WeightGradArgs{gx, nullptr, h->y16 + l * nd, R, D, D, h->splits_o,
                                                  h->gp_o + l * h->splits_o * D * D}),
              "o backward");
     }
-    STEP(column_sum_partials(s, h->g_a, h->idx_rm + l * nd, R, D, h->pt_e + l * pc, &nb), "g_e");
-    if (nb != h->nb_col) return c->fail(ULLIS_HIP_ERR_RUNTIME, "e gradient partial count");
 
     if (b.has_ln0) {  // (src/model.rs:2978-2982)
       STEP(layer_norm_backward_rows(s, x_emb, h->g_x, R, D, b.ln0.w, g_emb, 0, nullptr, h->pt_ln0,

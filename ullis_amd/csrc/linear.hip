@@ -174,6 +174,47 @@ struct EpiPackedFwd {
   }
 };
 
+// The ROSA e gradient from the O input gradient g (never stored): column sums
+// of g * (2 idx - 1) over 16-row groups, with the same products and summation
+// order as column_sum_partials over the stored g (streamed-LDS kernels only).
+struct EpiSignedColSum {
+  const float* amax;  // operand scale to divide out
+  const uint8_t* idx;  // [M][N]
+  float* part;         // [ceil(M/16)][N]
+  __device__ void row16(int row, int col, float (&v)[16], int lane, int M, int N, float* buf,
+                        int brow, int bcol) {
+    const float m = unscale_of(amax);
+    float g[16];
+    if (row < M) {
+      const long i = (long)row * N + col;
+      if (col + 16 <= N && N % 16 == 0 && lds::al16(idx)) {
+        const u32x4 b = *reinterpret_cast<const u32x4*>(idx + i);
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+          g[k] = (v[k] * m) * (2.0f * (float)((b[k >> 2] >> (8 * (k & 3))) & 0xFFu) - 1.0f);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+          g[k] = col + k < N ? (v[k] * m) * (2.0f * (float)idx[i + k] - 1.0f) : 0.0f;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) g[k] = 0.0f;
+    }
+    float* rowp = buf + (lane >> 1) * lds::kBufPitch + (lane & 1) * 16;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) rowp[k] = g[k];
+    lds::lds_fence();
+    // half-wave h sums rows [16 h, 16 h + 16) of column lane % 32
+    const int c = lane & 31, h = lane >> 5;
+    float cs = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) cs += buf[(16 * h + r) * lds::kBufPitch + c];
+    const int prow = brow + 16 * h;
+    if (bcol + c < N && prow < M) part[(long)(prow / 16) * N + bcol + c] = cs;
+  }
+};
+
 struct EpiStoreF32 {
   float* out;
   const float* amax;  // operand scale to divide out
@@ -444,6 +485,9 @@ bool packed_dx_lds(const PackedDxArgs& d, hipError_t* err, F&& f) {
     using T = decltype(t);
     lds::OpMK<T::bm, T::bk> a{reinterpret_cast<const half_t*>(g16), ldgy, (int)d.rows};
     lds::OpBits<T::bn, T::bk, true> b{d.bits_t, ldb / 32, (int)d.in, d.scale, (int)d.kofs};
+    if (d.col_part)
+      return f(lds::lds_problem<T>(a, b, EpiSignedColSum{d.gy32.amax, d.sign_idx, d.col_part},
+                                   d.rows, d.in, d.out, 1));
     return f(lds::lds_problem<T>(a, b, epi, d.rows, d.in, d.out, 1));
   });
 }
@@ -485,8 +529,16 @@ auto launch_one(hipStream_t s) {
 
 // gx (+)= gy . (scale * S) over the window of PackedDxArgs.
 hipError_t packed_dx(hipStream_t s, const PackedDxArgs& d) {
+  if (d.col_part && (d.out_mul || d.accumulate || !d.sign_idx)) return hipErrorInvalidValue;
   hipError_t err = hipSuccess;
   if (packed_dx_lds(d, &err, launch_one(s))) return err;
+  if (d.col_part) {
+    // store gx, then the signed column sums over it
+    PackedDxArgs st = d;
+    st.col_part = nullptr;
+    if ((err = packed_dx(s, st)) != hipSuccess) return err;
+    return column_sum_partials(s, d.gx, d.sign_idx, d.rows, d.in, d.col_part, nullptr);
+  }
   const long ldgy = ldgy_of(d), ldb = ldb_of(d);
   EpiStoreF32 epi{d.gx, d.gy32.amax, d.out_mul, d.accumulate};
   return with_tile(d.rows, d.in, [&](auto t) {

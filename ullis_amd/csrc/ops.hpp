@@ -100,6 +100,12 @@ struct PackedDxArgs {
   const float* out_mul;
   int accumulate;
   long ldgy = 0, ldb = 0, kofs = 0;
+  // Signed column sums instead of gx (out_mul null, accumulate 0): with
+  // col_part set, part[r / 16][c] = sum over 16-row groups of
+  // gx[r][c] * (2 sign_idx[r][c] - 1) (sign_idx [rows][in] u8), exactly as
+  // column_sum_partials over gx; gx is then only scratch for the non-LDS path.
+  const uint8_t* sign_idx = nullptr;
+  float* col_part = nullptr;
 };
 struct WeightGradArgs {
   GradIn gy32;
