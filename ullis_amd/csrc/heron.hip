@@ -565,8 +565,9 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
       STEP(copy_device(s, x_l, x_emb, (long)sizeof(float) * nd), "copy x");
     }
     // ROSA block (src/model.rs:1354-1440)
-    STEP(layer_norm_forward(s, x_l, R, D, b.ln3.w, b.ln3.b, nullptr, h->ln16), "ln3");
-    STEP(time_shift_mix(s, h->ln16, R, T, D, b.x_q, h->q16, b.x_k, h->k16, b.x_v, h->v16), "mix3");
+    STEP(layer_norm_mix_forward(s, x_l, R, T, D, b.ln3.w, b.ln3.b, h->ln16, false, b.x_q, h->q16,
+                                b.x_k, h->k16, b.x_v, h->v16),
+         "ln3 + mix3");
     {
       const uint16_t* const xin[3] = {h->q16, h->k16, h->v16};
       const uint32_t* const wb[3] = {b.q.bits, b.k.bits, b.v.bits};
@@ -591,8 +592,9 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
     uint16_t* key = h->key16 + l * nf;
     uint16_t* r2 = h->relu2_16 + l * nf;
     PROBED(ULLIS_HIP_PROBE_LN_FORWARD,
-           layer_norm_forward(s, ar, R, D, b.ln2.w, b.ln2.b, nullptr, ln2), "ln2");
-    STEP(time_shift_mix(s, ln2, R, T, D, b.cx_k, sh, nullptr, nullptr, nullptr, nullptr), "mix");
+           layer_norm_mix_forward(s, ar, R, T, D, b.ln2.w, b.ln2.b, ln2, true, b.cx_k, sh, nullptr,
+                                  nullptr, nullptr, nullptr),
+           "ln2 + mix");
     {
       PackedFwdOut o;
       o.y16 = key;

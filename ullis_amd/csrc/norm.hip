@@ -20,17 +20,12 @@ namespace {
 
 constexpr int kRowsPerBlock = 4;
 
-// NV = float4 chunks per lane (ch <= 256 * NV, ch % 4 == 0).
+// LayerNorm of one row by one wave: lane holds channels [4 (lane + 64 j), +4)
+// of chunk j (NV float4 chunks per lane, ch <= 256 * NV, ch % 4 == 0).
 template <int NV>
-__global__ __launch_bounds__(256) void ln_fwd_vec_kernel(const float* __restrict__ x, long rows,
-                                                         int ch, const uint16_t* __restrict__ w,
-                                                         const uint16_t* __restrict__ b,
-                                                         float* __restrict__ y32,
-                                                         uint16_t* __restrict__ y16) {
-  const int lane = threadIdx.x & 63;
-  const long row = (long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const float* xr = x + row * ch;
+__device__ __forceinline__ void ln_row_vec(const float* __restrict__ xr, int ch, int lane,
+                                           const uint16_t* __restrict__ w,
+                                           const uint16_t* __restrict__ b, floatx4 (&out)[NV]) {
   floatx4 v[NV];
   float s = 0.0f;
 #pragma unroll
@@ -58,10 +53,29 @@ __global__ __launch_bounds__(256) void ln_fwd_vec_kernel(const float* __restrict
   for (int j = 0; j < NV; ++j) {
     const int c = (lane + 64 * j) * 4;
     if (c < ch) {
-      floatx4 o;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        o[e] = (v[j][e] - mean) * inv * f16_bits_to_f32(w[c + e]) + f16_bits_to_f32(b[c + e]);
+        out[j][e] = (v[j][e] - mean) * inv * f16_bits_to_f32(w[c + e]) + f16_bits_to_f32(b[c + e]);
+    }
+  }
+}
+
+template <int NV>
+__global__ __launch_bounds__(256) void ln_fwd_vec_kernel(const float* __restrict__ x, long rows,
+                                                         int ch, const uint16_t* __restrict__ w,
+                                                         const uint16_t* __restrict__ b,
+                                                         float* __restrict__ y32,
+                                                         uint16_t* __restrict__ y16) {
+  const int lane = threadIdx.x & 63;
+  const long row = (long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  floatx4 y[NV];
+  ln_row_vec<NV>(x + row * ch, ch, lane, w, b, y);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 4;
+    if (c < ch) {
+      const floatx4 o = y[j];
       if (y32) *reinterpret_cast<floatx4*>(y32 + row * ch + c) = o;
       if (y16) {
         half4 h;
@@ -69,6 +83,61 @@ __global__ __launch_bounds__(256) void ln_fwd_vec_kernel(const float* __restrict
         for (int e = 0; e < 4; ++e) h[e] = (half_t)o[e];
         *reinterpret_cast<half4*>(y16 + row * ch + c) = h;
       }
+    }
+  }
+}
+
+// mix one 4-channel chunk: out = f16(x + (prev - x) * mix), prev = 0 at t = 0
+// (time_shift_mix on the fp16 LayerNorm output).
+__device__ __forceinline__ void mix4_store(const half4& x, const half4& p, const uint16_t* mix,
+                                           uint16_t* out, int c, long idx) {
+  const half4 m = *reinterpret_cast<const half4*>(mix + c);
+  half4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float xt = (float)x[e];
+    const float xx = (float)p[e] - xt;
+    o[e] = (half_t)(xt + xx * (float)m[e]);
+  }
+  *reinterpret_cast<half4*>(out + idx) = o;
+}
+
+// LayerNorm fused with the time-shift mixes that read its fp16 output: each
+// wave normalises its row and the previous row of the same sequence (the
+// same per-row arithmetic as ln_fwd_vec_kernel), so out_i = mix_i of the
+// fp16 rows without the LayerNorm output making a round trip through HBM.
+// y16 (optional) also receives the fp16 LayerNorm output.
+template <int NV>
+__global__ __launch_bounds__(256) void ln_mix_kernel(const float* __restrict__ x, long rows,
+                                                     int time, int ch,
+                                                     const uint16_t* __restrict__ w,
+                                                     const uint16_t* __restrict__ b,
+                                                     uint16_t* __restrict__ y16,
+                                                     const uint16_t* mix0, uint16_t* out0,
+                                                     const uint16_t* mix1, uint16_t* out1,
+                                                     const uint16_t* mix2, uint16_t* out2) {
+  const int lane = threadIdx.x & 63;
+  const long row = (long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  floatx4 cur[NV], prev[NV];
+  ln_row_vec<NV>(x + row * ch, ch, lane, w, b, cur);
+  const bool has_prev = row % time != 0;  // uniform over the wave
+  if (has_prev) ln_row_vec<NV>(x + (row - 1) * ch, ch, lane, w, b, prev);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 4;
+    if (c < ch) {
+      half4 xh, ph;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xh[e] = (half_t)cur[j][e];
+        ph[e] = has_prev ? (half_t)prev[j][e] : (half_t)0.0f;
+      }
+      const long idx = row * ch + c;
+      if (y16) *reinterpret_cast<half4*>(y16 + idx) = xh;
+      if (out0) mix4_store(xh, ph, mix0, out0, c, idx);
+      if (out1) mix4_store(xh, ph, mix1, out1, c, idx);
+      if (out2) mix4_store(xh, ph, mix2, out2, c, idx);
     }
   }
 }
@@ -404,6 +473,28 @@ hipError_t layer_norm_forward(hipStream_t s, const float* x, long rows, long ch,
   }
   launch(ln_fwd_any_kernel, grid, dim3(256), 0, s, x, rows, (int)ch, w, b, y32, y16);
   return hipGetLastError();
+}
+
+hipError_t layer_norm_mix_forward(hipStream_t s, const float* x, long rows, long time, long ch,
+                                  const uint16_t* w, const uint16_t* b, uint16_t* y16, bool keep_y,
+                                  const uint16_t* mix0, uint16_t* out0, const uint16_t* mix1,
+                                  uint16_t* out1, const uint16_t* mix2, uint16_t* out2) {
+  if (rows <= 0 || ch <= 0 || time <= 0) return hipSuccess;
+  auto a8 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; };
+  const bool fused = ch % 4 == 0 && ch <= 4096 && time <= INT32_MAX && vec_ok(x) && a8(y16) &&
+                     (!out0 || (a8(out0) && a8(mix0))) && (!out1 || (a8(out1) && a8(mix1))) &&
+                     (!out2 || (a8(out2) && a8(mix2)));
+  if (fused) {
+    return by_nv(ch, [&](auto nv) {
+      launch(ln_mix_kernel<decltype(nv)::value>, dim3((unsigned)cdiv(rows, kRowsPerBlock)),
+             dim3(256), 0, s, x, rows, (int)time, (int)ch, w, b, keep_y ? y16 : nullptr, mix0,
+             out0, mix1, out1, mix2, out2);
+      return hipGetLastError();
+    });
+  }
+  hipError_t e = layer_norm_forward(s, x, rows, ch, w, b, nullptr, y16);
+  if (e != hipSuccess) return e;
+  return time_shift_mix(s, y16, rows, time, ch, mix0, out0, mix1, out1, mix2, out2);
 }
 
 static bool ln_bwd_vec_path(long ch) { return ch % 4 == 0 && ch <= 1024; }

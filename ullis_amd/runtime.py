@@ -375,7 +375,8 @@ class HeronTrainer:
                                "paired GEMMs: value dX + ReLU^2 bwd, value dW"),
             "key_backward": (5, "mfma", 2 * 2.0 * r * f * d, "paired GEMMs: packed key dX, key dW"),
             "o_backward": (6, "mfma", 2 * 2.0 * r * d * d, "paired GEMMs: packed O dX, O dW"),
-            "ln_forward": (7, "hbm", r * d * (4 + 2) + 4.0 * d, "LayerNorm fwd (ln2)"),
+            "ln_forward": (7, "hbm", r * d * (4 + 2 + 2) + 6.0 * d,
+                           "LayerNorm fwd (ln2) + time-shift mix"),
             "ln_backward": (8, "hbm", r * d * 16 + 2.0 * d, "LayerNorm bwd rows (ln2, += g_x)"),
         }
 
