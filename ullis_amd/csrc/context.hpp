@@ -63,14 +63,20 @@ struct Carver {
 
 // Split-K factor for a weight-gradient GEMM [out, in] over `rows`: enough
 // 64x64-tile blocks for two per CU (512), at least 256 rows per split, at most 8.
-inline int dw_splits(long out, long in, long rows) {
+inline int dw_splits(long out, long in, long rows, long target_blocks = 512) {
   const long tiles = cdiv(out, 64) * cdiv(in, 64);
-  long s = cdiv(512, tiles > 0 ? tiles : 1);
+  long s = cdiv(target_blocks, tiles > 0 ? tiles : 1);
   const long by_rows = rows / 256;
   if (s > by_rows) s = by_rows;
   if (s > 8) s = 8;
   if (s < 1) s = 1;
   return (int)s;
 }
+
+// Split-K factor of a weight gradient paired with its layer's input gradient
+// in one launch (packed_backward_pair / fp16_backward_pair): the input
+// gradient supplies blocks too, so one per CU (256) is enough, and fewer
+// splits mean fewer fp32 partials to write and reduce.
+inline int pair_dw_splits(long out, long in, long rows) { return dw_splits(out, in, rows, 256); }
 
 }  // namespace ullis

@@ -319,7 +319,7 @@ Ws carve(void* base, long rows, long d, long vocab) {
   w.tgt = reinterpret_cast<float*>(take(sizeof(float) * rows));
   w.lse = reinterpret_cast<float*>(take(sizeof(float) * rows));
   w.part_bias = reinterpret_cast<float*>(take(sizeof(float) * cdiv(rows, 32) * vocab));
-  w.gpart = reinterpret_cast<float*>(take(sizeof(float) * dw_splits(vc, d, rows) * vc * d));
+  w.gpart = reinterpret_cast<float*>(take(sizeof(float) * pair_dw_splits(vc, d, rows) * vc * d));
   w.g_scale = reinterpret_cast<float*>(take(sizeof(float) * vocab));
   w.g_bias = reinterpret_cast<float*>(take(sizeof(float) * vocab));
   w.gy16 = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * rows * vc));
@@ -363,13 +363,13 @@ size_t head_ce_workspace_bytes(long rows, long d, long vocab) {
   const long vc = chunk_cols(vocab, d);
   auto al = [](size_t b) { return (b + 255) / 256 * 256; };
   return al(4 * nb32 * rows) * 2 + al(4 * rows) * 2 + al(4 * cdiv(rows, 32) * vocab) +
-         al(4 * dw_splits(vc, d, rows) * vc * d) + al(4 * vocab) * 2 + al(2 * rows * vc) + 256;
+         al(4 * pair_dw_splits(vc, d, rows) * vc * d) + al(4 * vocab) * 2 + al(2 * rows * vc) + 256;
 }
 
 long head_ce_chunk_cols(long vocab, long d) { return chunk_cols(vocab, d); }
 
 int head_ce_splits(long rows, long d, long vocab) {
-  return dw_splits(chunk_cols(vocab, d), d, rows);
+  return pair_dw_splits(chunk_cols(vocab, d), d, rows);
 }
 
 float* head_ce_bias_partials(void* workspace, long rows, long d, long vocab) {
@@ -409,7 +409,7 @@ hipError_t head_ce(hipStream_t s, const HeadCe& h, void* workspace) {
     if ((e = logits_gemm(s, h.hidden16, rows, d, bits_rows, n, gr)) != hipSuccess) return e;
     // g_hidden (+)= gscale * gy_chunk . (scale * S)_chunk and G_chunk =
     // gy_chunk^T . hidden in one launch, then the latent step for these rows
-    const int sp = dw_splits(vc, d, rows);  // the workspace holds this many [vc][d] partials
+    const int sp = pair_dw_splits(vc, d, rows);  // the workspace holds this many [vc][d] partials
     float* gp = h.gpart_all ? h.gpart_all + ci * sp * vc * d : w.gpart;
     const PackedDxArgs dx{GradIn{nullptr, nullptr}, w.gy16, rows, d, n, h.bits_t, h.scale,
                           h.g_hidden, gscale, ci > 0 ? 1 : 0, n, V, c0};

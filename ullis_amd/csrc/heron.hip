@@ -380,9 +380,9 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
   const long R = h->rows, D = h->D, F = h->F, L = h->L, V = h->V;
   const long nd = R * D, nf = R * F;
   const long words = cdiv(nd, 32);
-  h->splits_o = dw_splits(D, D, R);
-  h->splits_key = dw_splits(F, D, R);
-  h->splits_value = dw_splits(D, F, R);
+  h->splits_o = pair_dw_splits(D, D, R);
+  h->splits_key = pair_dw_splits(F, D, R);
+  h->splits_value = pair_dw_splits(D, F, R);
   h->nb_col = (int)column_partial_blocks(R);
   h->nb_ln = layer_norm_backward_nblk(R, D);
   const long nb_ln0 = layer_norm_backward_blocks(R);  // any LN backward path fits
