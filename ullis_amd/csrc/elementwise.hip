@@ -300,12 +300,24 @@ __global__ void rosa_expand_kernel(const uint8_t* idx_cm, const uint16_t* e, lon
 
 // Channel-major [B][C][T] bits -> row-major [B*T][C] through a 64 x 64 LDS
 // tile (coalesced 16-byte reads along T and writes along C).
-// grid (T / 64, C / 64, B); requires T % 64 == 0, C % 64 == 0.
+// grid (T / 64, C / 64, B * layers); requires T % 64 == 0, C % 64 == 0.
+// Layer l = blockIdx.z / B reads idx_cm and writes y16 / idx_rm at offset
+// l * B * T * C, with e = e_tab[l] (e_tab null: one layer, e).
 __global__ __launch_bounds__(256) void rosa_expand_tile_kernel(const uint8_t* idx_cm,
-                                                               const uint16_t* e, int time, int ch,
+                                                               const uint16_t* e,
+                                                               const uint16_t* const* e_tab,
+                                                               int batch, int time, int ch,
                                                                uint16_t* y16, uint8_t* idx_rm) {
   __shared__ uint8_t tile[64][64 + 16];
-  const int t0 = blockIdx.x * 64, c0 = blockIdx.y * 64, b = blockIdx.z;
+  const int t0 = blockIdx.x * 64, c0 = blockIdx.y * 64, b = blockIdx.z % batch;
+  const int l = blockIdx.z / batch;
+  if (e_tab) {
+    const long lofs = (long)l * batch * time * ch;
+    e = e_tab[l];
+    idx_cm += lofs;
+    y16 += lofs;
+    if (idx_rm) idx_rm += lofs;
+  }
   {
     const int cl = threadIdx.x >> 2, tl = (threadIdx.x & 3) * 16;
     const u32x4 v = *reinterpret_cast<const u32x4*>(
@@ -477,12 +489,37 @@ hipError_t rosa_expand(hipStream_t s, const uint8_t* idx_cm, const uint16_t* e, 
   if (time % 64 == 0 && ch % 64 == 0 && time * ch < (1L << 31) && a16(idx_cm) && a16(e) &&
       a16(y16) && (!idx_rm || a16(idx_rm))) {
     launch(rosa_expand_tile_kernel, dim3((unsigned)(time / 64), (unsigned)(ch / 64), (unsigned)batch),
-           dim3(256), 0, s, idx_cm, e, (int)time, (int)ch, y16, idx_rm);
+           dim3(256), 0, s, idx_cm, e, (const uint16_t* const*)nullptr, (int)batch, (int)time,
+           (int)ch, y16, idx_rm);
     return hipGetLastError();
   }
   launch(rosa_expand_kernel, grid1d(n), dim3(256), 0, s, idx_cm, e, batch, time, ch,
                      y16, idx_rm);
   return hipGetLastError();
+}
+
+hipError_t rosa_expand_layers(hipStream_t s, const uint8_t* idx_cm, const uint16_t* const* e_host,
+                              const uint16_t* const* e_dev, long layers, long batch, long time,
+                              long ch, uint16_t* y16, uint8_t* idx_rm) {
+  const long nd = batch * time * ch;
+  if (nd <= 0 || layers <= 0) return hipSuccess;
+  bool tile = time % 64 == 0 && ch % 64 == 0 && time * ch < (1L << 31) &&
+              batch * layers <= 65535 && a16(idx_cm) && a16(y16) && (!idx_rm || a16(idx_rm)) &&
+              e_dev != nullptr;
+  for (long l = 0; l < layers && tile; ++l) tile = a16(e_host[l]);
+  if (tile) {
+    launch(rosa_expand_tile_kernel,
+           dim3((unsigned)(time / 64), (unsigned)(ch / 64), (unsigned)(batch * layers)), dim3(256),
+           0, s, idx_cm, (const uint16_t*)nullptr, e_dev, (int)batch, (int)time, (int)ch, y16,
+           idx_rm);
+    return hipGetLastError();
+  }
+  for (long l = 0; l < layers; ++l) {
+    hipError_t e = rosa_expand(s, idx_cm + l * nd, e_host[l], batch, time, ch, y16 + l * nd,
+                               idx_rm ? idx_rm + l * nd : nullptr);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 }  // namespace ullis

@@ -99,6 +99,10 @@ struct ullis_hip_heron {
   int vec_blocks = 0, f16_blocks = 0, fin_blocks = 0, trans_blocks = 0;
   int ln0_job_blocks = 0;  // blocks of the trailing LN0 job (0: none)
   std::vector<const Packed*> trans_generic;  // bits_t rebuilt by the generic transpose
+  // ROSA e of every layer (host array and a device copy) for the expand of all
+  // layers' ROSA outputs in one launch
+  std::vector<const uint16_t*> e_host;
+  const uint16_t* const* e_dev = nullptr;
   uint32_t* qkv = nullptr;
   void* head_ws = nullptr;
   int splits_o = 1, splits_key = 1, splits_value = 1;
@@ -289,6 +293,8 @@ int build_update_jobs(ullis_hip_heron* h) {
   add(sizeof(F16Job) * fj.size());
   add(sizeof(FinishJob) * pj.size());
   add(sizeof(TransJob) * tj.size());
+  for (const Block& b : h->blocks) h->e_host.push_back(b.e);
+  add(sizeof(const uint16_t*) * h->e_host.size());
   if (int rc = c->hip(hipMalloc(&h->job_mem, bytes), "heron update job tables")) return rc;
   Carver cv(h->job_mem);
   auto up = [&](auto& v, auto*& dst, int& n) -> int {
@@ -304,6 +310,8 @@ int build_update_jobs(ullis_hip_heron* h) {
   if (int rc = up(fj, h->f16_jobs, h->n_f16)) return rc;
   if (int rc = up(pj, h->fin_jobs, h->n_fin)) return rc;
   if (int rc = up(tj, h->trans_jobs, h->n_trans)) return rc;
+  int n_e = 0;
+  if (int rc = up(h->e_host, h->e_dev, n_e)) return rc;
   h->vec_blocks = vb;
   h->f16_blocks = fb;
   h->fin_blocks = pb;
@@ -554,6 +562,9 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
   bool ln0_now = false;
 
   STEP(fill_f32(s, h->slots, L + 2, 0.0f), "clear amax slots");
+  // y = (2 idx - 1) e of every layer (e is not updated before the step's end)
+  STEP(rosa_expand_layers(s, rosa_idx, h->e_host.data(), h->e_dev, L, B, T, D, h->y16, h->idx_rm),
+       "rosa y");
 
   // ------------------------------------------------------------- forward
   for (long l = 0; l < L; ++l) {
@@ -578,7 +589,6 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
       STEP(packed_forward_bits3(s, xin, R, D, D, wb, sc, bi, planes), "qkv");
     }
     uint16_t* y16 = h->y16 + l * nd;
-    STEP(rosa_expand(s, rosa_idx + l * nd, b.e, B, T, D, y16, h->idx_rm + l * nd), "rosa y");
     float* ar = h->after_rosa + l * nd;
     {
       PackedFwdOut o;

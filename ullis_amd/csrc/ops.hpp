@@ -251,6 +251,12 @@ hipError_t partial_reduce(hipStream_t s, const float* part, int nblk, long ncols
 // and the row-major idx tape.
 hipError_t rosa_expand(hipStream_t s, const uint8_t* idx_cm, const uint16_t* e, long batch,
                        long time, long ch, uint16_t* y16, uint8_t* idx_rm);
+// rosa_expand of `layers` consecutive layers in one launch: idx_cm, y16 and
+// idx_rm advance by batch*time*ch per layer, layer l uses e_host[l] (host
+// array) / e_dev[l] (the same pointers in device memory).
+hipError_t rosa_expand_layers(hipStream_t s, const uint8_t* idx_cm, const uint16_t* const* e_host,
+                              const uint16_t* const* e_dev, long layers, long batch, long time,
+                              long ch, uint16_t* y16, uint8_t* idx_rm);
 
 // --------------------------------------------------------------- head + CE
 
