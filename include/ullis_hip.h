@@ -186,7 +186,7 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
 #define ULLIS_HIP_PROBE_KEY_BACKWARD 5      /* key dX (packed) and dW in one launch */
 #define ULLIS_HIP_PROBE_O_BACKWARD 6        /* ROSA O dX (packed) and dW in one launch */
 #define ULLIS_HIP_PROBE_LN_FORWARD 7        /* ln2 forward fused with the CMix time-shift mix */
-#define ULLIS_HIP_PROBE_LN_BACKWARD 8       /* ln2 backward rows */
+#define ULLIS_HIP_PROBE_LN_BACKWARD 8       /* CMix mix backward fused with the ln2 backward */
 #define ULLIS_HIP_PROBE_COUNT 9
 int ullis_hip_heron_probe(ullis_hip_heron* h, int probe_id);
 int ullis_hip_heron_probe_read(ullis_hip_heron* h, float* total_ms, int* launches);

@@ -86,7 +86,7 @@ struct ullis_hip_heron {
   float *gp_value = nullptr, *gp_key = nullptr, *gp_o = nullptr, *gp_head = nullptr;
   float *pt_mix = nullptr, *pt_ln2 = nullptr, *pt_ob = nullptr, *pt_e = nullptr;
   float *pt_lnout = nullptr, *pt_ln0 = nullptr;
-  int nb_col = 0, nb_ln = 0;
+  int nb_col = 0, nb_ln = 0, nb_mix = 0;
   // batched update job tables (device memory) and their grid sizes; the LN0
   // job is the last vector job so that it can be left out when LN0 backward
   // took a path with another partial count (unaligned x_emb)
@@ -250,7 +250,8 @@ int build_update_jobs(ullis_hip_heron* h) {
   for (long l = 0; l < L; ++l) {
     Block& b = h->blocks[l];
     const long pc = (long)h->nb_col * D;
-    vec2(h->pt_mix + l * pc, h->nb_col, D, false, sgd(b.cx_k, b.cx_k_res, 1.0f, nullptr), {});
+    vec2(h->pt_mix + l * h->nb_mix * D, h->nb_mix, D, false, sgd(b.cx_k, b.cx_k_res, 1.0f, nullptr),
+         {});
     ln(b.ln2, h->pt_ln2 + l * 2L * h->nb_ln * D, h->nb_ln);
     vec2(h->pt_ob + l * pc, h->nb_col, D, false, sgd(b.o.bias, b.o.bias_res, 1.0f, nullptr), {});
     vec2(h->pt_e + l * pc, h->nb_col, D, false, sgd(b.e, b.e_res, 1.0f, nullptr), {});
@@ -393,6 +394,7 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
   h->splits_value = pair_dw_splits(D, F, R);
   h->nb_col = (int)column_partial_blocks(R);
   h->nb_ln = layer_norm_backward_nblk(R, D);
+  h->nb_mix = layer_norm_mix_backward_mix_nblk(R, D);
   const long nb_ln0 = layer_norm_backward_blocks(R);  // any LN backward path fits
   const long head_vc = head_ce_chunk_cols(V, D);
   const long head_sp = head_ce_splits(R, D, V);
@@ -400,6 +402,7 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
   const long gp_value = (long)h->splits_value * D * F, gp_key = (long)h->splits_key * F * D;
   const long gp_o = (long)h->splits_o * D * D, gp_head = head_chunks * head_sp * head_vc * D;
   const long pt_col = (long)h->nb_col * D, pt_ln = 2L * h->nb_ln * D;
+  const long pt_mix = (long)h->nb_mix * D;
   const size_t head_ws = head_ce_workspace_bytes(R, D, V);
 
   size_t bytes = 0;
@@ -420,7 +423,8 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
   add(4ul * gp_key * L);
   add(4ul * gp_o * L);
   add(4ul * gp_head);
-  for (int i = 0; i < 3; ++i) add(4ul * pt_col * L);  // pt_mix pt_ob pt_e
+  add(4ul * pt_mix * L);
+  for (int i = 0; i < 2; ++i) add(4ul * pt_col * L);  // pt_ob pt_e
   add(4ul * pt_ln * L);      // pt_ln2
   add(4ul * pt_ln);          // pt_lnout
   add(4ul * 2 * nb_ln0 * D); // pt_ln0
@@ -457,7 +461,7 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
   h->gp_key = cv.take<float>(gp_key * L);
   h->gp_o = cv.take<float>(gp_o * L);
   h->gp_head = cv.take<float>(gp_head);
-  h->pt_mix = cv.take<float>(pt_col * L);
+  h->pt_mix = cv.take<float>(pt_mix * L);
   h->pt_ob = cv.take<float>(pt_col * L);
   h->pt_e = cv.take<float>(pt_col * L);
   h->pt_ln2 = cv.take<float>(pt_ln * L);
@@ -681,16 +685,18 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
                                                  h->gp_key + l * h->splits_key * F * D}),
              "key backward");
     }
-    STEP(time_shift_mix_backward(s, h->g_a, ln2, b.cx_k, R, T, D, h->g_b, h->pt_mix + l * pc, &nb),
-         "mix bwd");
-    if (nb != h->nb_col) return c->fail(ULLIS_HIP_ERR_RUNTIME, "mix backward partial count");
-
-    // LN2 backward, += into g_x (src/model.rs:2958-2963)
-    PROBED(ULLIS_HIP_PROBE_LN_BACKWARD,
-           layer_norm_backward_rows(s, ar, h->g_b, R, D, b.ln2.w, h->g_x, 1, slot_mid,
-                                    h->pt_ln2 + l * 2L * h->nb_ln * D, &nb),
-           "ln2 bwd");
-    if (nb != h->nb_ln) return c->fail(ULLIS_HIP_ERR_RUNTIME, "ln2 backward partial count");
+    // CMix time-shift mix backward (x_k gradient) fused with the LN2
+    // backward, += into g_x (src/model.rs:2958-2963)
+    {
+      int nb_mix = 0;
+      PROBED(ULLIS_HIP_PROBE_LN_BACKWARD,
+             layer_norm_mix_backward_rows(s, ar, h->g_a, ln2, b.cx_k, R, T, D, b.ln2.w, h->g_x, 1,
+                                          slot_mid, h->pt_ln2 + l * 2L * h->nb_ln * D,
+                                          h->pt_mix + l * h->nb_mix * D, h->g_b, &nb, &nb_mix),
+             "mix + ln2 bwd");
+      if (nb != h->nb_ln || nb_mix != h->nb_mix)
+        return c->fail(ULLIS_HIP_ERR_RUNTIME, "mix / ln2 backward partial count");
+    }
     // O bias gradient (column sums of g_x) and the fp16 copy of g_x for the
     // O GEMMs here and the CMix GEMMs of the block below.
     STEP(column_sum_partials(s, h->g_x, nullptr, R, D, h->pt_ob + l * pc, &nb, h->gx16, slot_mid),

@@ -287,24 +287,59 @@ __global__ __launch_bounds__(256) void ln_bwd_vec_kernel(const float* __restrict
 // of a row's loads (x, gy and, when accumulating, the old gx) are issued
 // before the first reduction, and the grid has one wave per row, so the
 // memory latency of every row overlaps. Column partials per block as above.
-template <int NV>
+// MIX: the output gradient gy is that of a time-shift mix's input, computed
+// here from the mix's output gradient g_s (rows t, t + 1), its fp16 input
+// x16 = this LayerNorm's output (rows t, t - 1) and the mix vector, with the
+// arithmetic of time_shift_mix_bwd4_kernel; the mix-vector gradient goes to
+// part_mix[block][ch] (the block's rows summed in order).
+template <int NV, bool MIX = false>
 __global__ __launch_bounds__(256) void ln_bwd_row_kernel(const float* __restrict__ x,
                                                          const float* __restrict__ gy, long rows,
                                                          int ch, const uint16_t* __restrict__ w,
                                                          float* gx, int accumulate, float* amax,
-                                                         float* __restrict__ part) {
-  __shared__ float red[kRowsPerBlock][2][1024];
+                                                         float* __restrict__ part,
+                                                         const uint16_t* __restrict__ x16 = nullptr,
+                                                         const uint16_t* __restrict__ mix = nullptr,
+                                                         int time = 1,
+                                                         float* __restrict__ part_mix = nullptr) {
+  constexpr int kParts = MIX ? 3 : 2;
+  __shared__ float red[kRowsPerBlock][kParts][1024];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const long row = (long)blockIdx.x * kRowsPerBlock + wave;
   const bool live = row < rows;
-  floatx4 v[NV], g[NV], old[NV], wv[NV];
+  floatx4 v[NV], g[NV], old[NV], wv[NV], gmix[NV];
+  const int t = MIX ? (int)(row % time) : 0;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int c = (lane + 64 * j) * 4;
     const bool ok = live && c < ch;
     v[j] = ok ? *reinterpret_cast<const floatx4*>(x + row * ch + c) : (floatx4){};
-    g[j] = ok ? *reinterpret_cast<const floatx4*>(gy + row * ch + c) : (floatx4){};
+    if constexpr (MIX) {
+      floatx4 gs = {}, gn = {};
+      half4 xh = {}, ph = {}, m = {};
+      const bool has_next = t + 1 < time;
+      if (ok) {
+        const long idx = row * ch + c;
+        gs = *reinterpret_cast<const floatx4*>(gy + idx);
+        xh = *reinterpret_cast<const half4*>(x16 + idx);
+        if (t > 0) ph = *reinterpret_cast<const half4*>(x16 + idx - ch);
+        if (has_next) gn = *reinterpret_cast<const floatx4*>(gy + idx + ch);
+        m = *reinterpret_cast<const half4*>(mix + c);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float xt = (float)xh[e];
+        const float xx = (t == 0 ? 0.0f : (float)ph[e]) - xt;
+        const float mm = (float)m[e];
+        gmix[j][e] = gs[e] * xx;
+        float gb = gs[e] - gs[e] * mm;
+        if (has_next) gb = gb + gn[e] * mm;
+        g[j][e] = gb;
+      }
+    } else {
+      g[j] = ok ? *reinterpret_cast<const floatx4*>(gy + row * ch + c) : (floatx4){};
+    }
     old[j] = ok && accumulate ? *reinterpret_cast<const floatx4*>(gx + row * ch + c) : (floatx4){};
     const half4 wh = c < ch ? *reinterpret_cast<const half4*>(w + c) : (half4){};
 #pragma unroll
@@ -366,6 +401,7 @@ __global__ __launch_bounds__(256) void ln_bwd_row_kernel(const float* __restrict
       if (c < ch) {
         red[wave][0][c + e] = pw[j][e];
         red[wave][1][c + e] = pb[j][e];
+        if constexpr (MIX) red[wave][kParts - 1][c + e] = live ? gmix[j][e] : 0.0f;
       }
   }
   __shared__ float wmax[kRowsPerBlock];
@@ -389,6 +425,12 @@ __global__ __launch_bounds__(256) void ln_bwd_row_kernel(const float* __restrict
     }
     part[((long)blockIdx.x * 2 + 0) * ch + c] = a;
     part[((long)blockIdx.x * 2 + 1) * ch + c] = bsum;
+    if constexpr (MIX) {
+      float mg = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kRowsPerBlock; ++k) mg += red[k][kParts - 1][c];
+      part_mix[(long)blockIdx.x * ch + c] = mg;
+    }
   }
 }
 
@@ -534,7 +576,8 @@ hipError_t layer_norm_backward_rows(hipStream_t s, const float* x, const float* 
     if (nblk_out) *nblk_out = nblk;
     return by_nv(ch, [&](auto nv) {
       launch(ln_bwd_row_kernel<decltype(nv)::value>, dim3(nblk), dim3(256), 0, s, x, gy, rows,
-             (int)ch, w, gx, accumulate, amax, part);
+             (int)ch, w, gx, accumulate, amax, part, (const uint16_t*)nullptr,
+             (const uint16_t*)nullptr, 1, (float*)nullptr);
       return hipGetLastError();
     });
   }
@@ -550,6 +593,39 @@ hipError_t layer_norm_backward_rows(hipStream_t s, const float* x, const float* 
   launch(ln_bwd_any_kernel, dim3(nblk), dim3(64), 0, s, x, gy, rows, (int)ch, w, gx,
                      accumulate, amax, part);
   return hipGetLastError();
+}
+
+int layer_norm_mix_backward_mix_nblk(long rows, long ch) {
+  return ln_bwd_row_path(rows, ch) ? (int)cdiv(rows, kRowsPerBlock) : (int)cdiv(rows, 16);
+}
+
+hipError_t layer_norm_mix_backward_rows(hipStream_t s, const float* x, const float* g_s,
+                                        const uint16_t* x16, const uint16_t* mix, long rows,
+                                        long time, long ch, const uint16_t* w, float* gx,
+                                        int accumulate, float* amax, float* part, float* part_mix,
+                                        float* g_scratch, int* nblk_out, int* nblk_mix_out) {
+  if (rows <= 0 || ch <= 0 || time <= 0) {
+    if (nblk_out) *nblk_out = 0;
+    if (nblk_mix_out) *nblk_mix_out = 0;
+    return hipSuccess;
+  }
+  auto a8 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; };
+  if (ln_bwd_row_path(rows, ch) && time <= INT32_MAX && vec_ok(x) && vec_ok(g_s) && vec_ok(gx) &&
+      a8(w) && a8(x16) && a8(mix)) {
+    const int nblk = (int)cdiv(rows, kRowsPerBlock);
+    if (nblk_out) *nblk_out = nblk;
+    if (nblk_mix_out) *nblk_mix_out = nblk;
+    return by_nv(ch, [&](auto nv) {
+      launch(ln_bwd_row_kernel<decltype(nv)::value, true>, dim3(nblk), dim3(256), 0, s, x, g_s,
+             rows, (int)ch, w, gx, accumulate, amax, part, x16, mix, (int)time, part_mix);
+      return hipGetLastError();
+    });
+  }
+  hipError_t e = time_shift_mix_backward(s, g_s, x16, mix, rows, time, ch, g_scratch, part_mix,
+                                         nblk_mix_out);
+  if (e != hipSuccess) return e;
+  return layer_norm_backward_rows(s, x, g_scratch, rows, ch, w, gx, accumulate, amax, part,
+                                  nblk_out);
 }
 
 hipError_t layer_norm_param_finish(hipStream_t s, const float* part, int nblk, long ch, float* gw,

@@ -184,6 +184,18 @@ hipError_t layer_norm_backward_rows(hipStream_t s, const float* x, const float* 
 int layer_norm_backward_blocks(long rows);
 // Partial blocks layer_norm_backward_rows uses for 16-byte aligned x / gy / gx.
 int layer_norm_backward_nblk(long rows, long ch);
+// LayerNorm backward fed by the backward of the time-shift mix that read its
+// fp16 output x16: gy = time_shift_mix_backward(g_s, x16, mix) is formed in
+// the same kernel (same values), the mix gradient partials go to
+// part_mix[*nblk_mix_out][ch]; g_scratch [rows][ch] is used when the fused
+// kernel does not apply. With aligned operands the partial counts are
+// layer_norm_backward_nblk and layer_norm_mix_backward_mix_nblk.
+hipError_t layer_norm_mix_backward_rows(hipStream_t s, const float* x, const float* g_s,
+                                        const uint16_t* x16, const uint16_t* mix, long rows,
+                                        long time, long ch, const uint16_t* w, float* gx,
+                                        int accumulate, float* amax, float* part, float* part_mix,
+                                        float* g_scratch, int* nblk_out, int* nblk_mix_out);
+int layer_norm_mix_backward_mix_nblk(long rows, long ch);
 
 // Sums part[nblk][2][ch] -> gw, gb (optional outputs) and, when lr > 0,
 // clipped SGD on (w, b) with their carries.

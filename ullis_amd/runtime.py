@@ -377,7 +377,8 @@ class HeronTrainer:
             "o_backward": (6, "mfma", 2 * 2.0 * r * d * d, "paired GEMMs: packed O dX, O dW"),
             "ln_forward": (7, "hbm", r * d * (4 + 2 + 2) + 6.0 * d,
                            "LayerNorm fwd (ln2) + time-shift mix"),
-            "ln_backward": (8, "hbm", r * d * 16 + 2.0 * d, "LayerNorm bwd rows (ln2, += g_x)"),
+            "ln_backward": (8, "hbm", r * d * (4 + 4 + 2 + 8) + 4.0 * d,
+                            "mix bwd + LayerNorm bwd rows (ln2, += g_x)"),
         }
 
     def probe_begin(self, name: str = "key_forward") -> str:
