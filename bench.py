@@ -92,7 +92,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-rows", type=int, default=64,
                     help="rows of the CPU-baseline sample (0 disables it)")
-    ap.add_argument("--probe", default="key_forward",
+    ap.add_argument("--probe", default="value_backward",
                     help="launch class timed for the roofline object")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after the timed region, run one plain device copy kernel of this many "

@@ -316,6 +316,64 @@ __device__ __forceinline__ void get16h(const uint16_t* p, int col, int n, bool v
   }
 }
 
+// XCD-aware tile order. Blocks are dealt round-robin to the 8 XCDs
+// (bid % 8), each with its own L2, and the blocks of one XCD run together. XCD
+// x takes one rectangle of gm x gn output tiles (gm | tiles_m, gn | tiles_n,
+// gm * gn = tiles / 8, all powers of two) that minimises the operand bytes
+// its L2 streams, gm * wa + gn * wb (wa / wb: bytes of one tile row of A /
+// one tile column of B per K step); row-major inside the rectangle. The
+// host picks the rectangle (tile_map); other tile counts keep the row-major
+// order.
+struct TileMap {
+  int log_gm = -1;  // < 0: row-major order
+  int log_gn = 0, log_groups_n = 0;
+};
+
+inline int log2_exact(long v) {  // log2 of a power of two, else -1
+  if (v <= 0 || (v & (v - 1)) != 0) return -1;
+  int l = 0;
+  while ((1L << l) < v) ++l;
+  return l;
+}
+
+inline TileMap tile_map(long tiles_m, long tiles_n, long wa, long wb) {
+  TileMap m;
+  const long total = tiles_m * tiles_n;
+  if (total % 8 != 0) return m;
+  const long per = total / 8;
+  long best = -1;
+  for (long gm = 1; gm <= tiles_m && gm <= per; gm *= 2) {
+    if (tiles_m % gm != 0 || per % gm != 0) continue;
+    const long gn = per / gm;
+    if (tiles_n % gn != 0 || log2_exact(gn) < 0 || log2_exact(tiles_n / gn) < 0) continue;
+    const long cost = gm * wa + gn * wb;
+    if (best < 0 || cost < best) {
+      best = cost;
+      m.log_gm = log2_exact(gm);
+      m.log_gn = log2_exact(gn);
+      m.log_groups_n = log2_exact(tiles_n / gn);
+    }
+  }
+  return m;
+}
+
+__device__ __forceinline__ void tile_of_block_map(int bid, int tiles_n, const TileMap& map,
+                                                  int& tm, int& tn) {
+  if (map.log_gm >= 0) {
+    const int xcd = bid & 7, local = bid >> 3;
+    tm = ((xcd >> map.log_groups_n) << map.log_gm) + (local >> map.log_gn);
+    tn = ((xcd & ((1 << map.log_groups_n) - 1)) << map.log_gn) + (local & ((1 << map.log_gn) - 1));
+  } else {
+    tm = bid / tiles_n;
+    tn = bid - tm * tiles_n;
+  }
+}
+
+template <class T, class OA, class OB>
+TileMap tile_map_for(long M, long N) {
+  return tile_map(cdiv(M, T::bm), cdiv(N, T::bn), OA::kBytes, OB::kBytes);
+}
+
 // Epilogues of split-K outputs take the block's K split through set_split(kz).
 template <class E, class = void>
 inline constexpr bool kHasSplit = false;
@@ -343,7 +401,7 @@ constexpr int lds_smem_bytes() {
 template <int BM, int BN, int BK, int NS, class OA, class OB, class Epi>
 __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const OA& a,
                                               const OB& b, Epi& epi, int M, int N, int K,
-                                              int k_split) {
+                                              int k_split, const TileMap& map) {
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int STAGE = OA::kBytes + OB::kBytes;
@@ -359,7 +417,8 @@ __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const
   const int wm = wave >> 1, wn = wave & 1;
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   int tm, tn;
-  tile_of_block(bid, tiles_m, tiles_n, tm, tn);
+  tile_of_block_map(bid, tiles_n, map, tm, tn);
+  (void)tiles_m;
   const int m0 = tm * BM, n0 = tn * BN;
   const int kbeg = kz * k_split;
   const int kend = min(K, kbeg + k_split);
@@ -492,9 +551,9 @@ __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const
 
 template <int BM, int BN, int BK, int NS, class OA, class OB, class Epi>
 __global__ __launch_bounds__(256) void gemm_lds_kernel(OA a, OB b, Epi epi, int M, int N, int K,
-                                                       int k_split) {
+                                                       int k_split, TileMap map) {
   __shared__ __attribute__((aligned(1024))) char smem[lds_smem_bytes<BM, BN, BK, NS, OA, OB>()];
-  gemm_lds_body<BM, BN, BK, NS>(smem, blockIdx.x, blockIdx.z, a, b, epi, M, N, K, k_split);
+  gemm_lds_body<BM, BN, BK, NS>(smem, blockIdx.x, blockIdx.z, a, b, epi, M, N, K, k_split, map);
 }
 
 template <class T, int G>
@@ -506,11 +565,11 @@ struct Group {
 template <int BM, int BN, int BK, int NS, class OA, class OB, class Epi, int G>
 __global__ __launch_bounds__(256) void gemm_lds_group_kernel(Group<OA, G> a, Group<OB, G> b,
                                                              Group<Epi, G> epi, int M, int N,
-                                                             int K, int k_split) {
+                                                             int K, int k_split, TileMap map) {
   __shared__ __attribute__((aligned(1024))) char smem[lds_smem_bytes<BM, BN, BK, NS, OA, OB>()];
   const int g = blockIdx.y;
   gemm_lds_body<BM, BN, BK, NS>(smem, blockIdx.x, blockIdx.z, a.v[g], b.v[g], epi.v[g], M, N, K,
-                                k_split);
+                                k_split, map);
 }
 
 // One GEMM of a pair launch: tile config T, operands, epilogue and shape;
@@ -521,6 +580,7 @@ struct LdsProblem {
   OB b;
   Epi epi;
   int M, N, K, k_split, tiles, blocks;
+  TileMap map;
 };
 
 // Two independent GEMMs (possibly of different tile configs and operand
@@ -534,12 +594,14 @@ __global__ __launch_bounds__(256) void gemm_lds_pair_kernel(LdsProblem<T1, OA1, 
   __shared__ __attribute__((aligned(1024))) char smem[S1 > S2 ? S1 : S2];
   const int bid = blockIdx.x;
   if (bid < p1.blocks) {
-    gemm_lds_body<T1::bm, T1::bn, T1::bk, T1::ns>(smem, bid % p1.tiles, bid / p1.tiles, p1.a, p1.b,
-                                                  p1.epi, p1.M, p1.N, p1.K, p1.k_split);
+    const int z = p1.blocks == p1.tiles ? 0 : bid / p1.tiles;
+    gemm_lds_body<T1::bm, T1::bn, T1::bk, T1::ns>(smem, bid - z * p1.tiles, z, p1.a, p1.b, p1.epi,
+                                                  p1.M, p1.N, p1.K, p1.k_split, p1.map);
   } else {
     const int b2 = bid - p1.blocks;
-    gemm_lds_body<T2::bm, T2::bn, T2::bk, T2::ns>(smem, b2 % p2.tiles, b2 / p2.tiles, p2.a, p2.b,
-                                                  p2.epi, p2.M, p2.N, p2.K, p2.k_split);
+    const int z = p2.blocks == p2.tiles ? 0 : b2 / p2.tiles;
+    gemm_lds_body<T2::bm, T2::bn, T2::bk, T2::ns>(smem, b2 - z * p2.tiles, z, p2.a, p2.b, p2.epi,
+                                                  p2.M, p2.N, p2.K, p2.k_split, p2.map);
   }
 }
 
@@ -584,7 +646,8 @@ hipError_t launch_lds_group(hipStream_t s, const Group<OA, G>& a, const Group<OB
   const long tiles = cdiv(M, T::bm) * cdiv(N, T::bn);
   const int ks = (int)(cdiv(K, T::bk) * T::bk);
   launch((gemm_lds_group_kernel<T::bm, T::bn, T::bk, T::ns, OA, OB, Epi, G>),
-         dim3((unsigned)tiles, G, 1), dim3(kThreads), 0, s, a, b, epi, (int)M, (int)N, (int)K, ks);
+         dim3((unsigned)tiles, G, 1), dim3(kThreads), 0, s, a, b, epi, (int)M, (int)N, (int)K, ks,
+         tile_map_for<T, OA, OB>(M, N));
   return hipGetLastError();
 }
 
@@ -597,7 +660,7 @@ hipError_t launch_lds(hipStream_t s, const OA& a, const OB& b, const Epi& epi, l
   const int ks = (int)(cdiv(cdiv(K, splits), T::bk) * T::bk);
   launch((gemm_lds_kernel<T::bm, T::bn, T::bk, T::ns, OA, OB, Epi>),
          dim3((unsigned)tiles, 1, splits), dim3(kThreads), 0, s, a, b, epi, (int)M, (int)N, (int)K,
-         ks);
+         ks, tile_map_for<T, OA, OB>(M, N));
   return hipGetLastError();
 }
 
@@ -607,14 +670,15 @@ LdsProblem<T, OA, OB, Epi> lds_problem(const OA& a, const OB& b, const Epi& epi,
   if (splits < 1) splits = 1;
   const int tiles = (int)(cdiv(M, T::bm) * cdiv(N, T::bn));
   const int ks = (int)(cdiv(cdiv(K, splits), T::bk) * T::bk);
-  return LdsProblem<T, OA, OB, Epi>{a, b, epi, (int)M, (int)N, (int)K, ks, tiles, tiles * splits};
+  return LdsProblem<T, OA, OB, Epi>{a,  b,     epi,          (int)M, (int)N, (int)K,
+                                    ks, tiles, tiles * splits, tile_map_for<T, OA, OB>(M, N)};
 }
 
 template <class T, class OA, class OB, class Epi>
 hipError_t launch_lds_problem(hipStream_t s, const LdsProblem<T, OA, OB, Epi>& p) {
   launch((gemm_lds_kernel<T::bm, T::bn, T::bk, T::ns, OA, OB, Epi>),
          dim3((unsigned)p.tiles, 1, (unsigned)(p.blocks / p.tiles)), dim3(kThreads), 0, s, p.a, p.b,
-         p.epi, p.M, p.N, p.K, p.k_split);
+         p.epi, p.M, p.N, p.K, p.k_split, p.map);
   return hipGetLastError();
 }
 

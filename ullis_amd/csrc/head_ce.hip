@@ -51,7 +51,7 @@ struct EpiCeStats {
   const uint32_t* targets;
   uint32_t ignore_id;
   long time;
-  float* part_m;  // [nb32][M]
+  float* part_m;  // [M][nb32], nb32 = ceil(N / 32): one row's blocks contiguous
   float* part_s;
   float* tgt;     // [M]
   template <int TM, int TN>
@@ -75,8 +75,9 @@ struct EpiCeStats {
           const float ssum = halfwave_sum(e);
           if (row < M && cbase < N) {
             if ((lane & 31) == 0) {
-              part_m[cb * M + row] = m;
-              part_s[cb * M + row] = ssum;
+              const long nb = (N + 31) / 32;
+              part_m[(long)row * nb + cb] = m;
+              part_s[(long)row * nb + cb] = ssum;
             }
             if (colok && ce_row_valid(row, M, time, targets, ignore_id) &&
                 (long)targets[row + 1] == (long)col)
@@ -119,8 +120,9 @@ struct EpiCeStats {
     }
     if (row >= M) return;
     if ((lane & 1) == 0 && col < N) {
-      part_m[(long)(col >> 5) * M + row] = mm;
-      part_s[(long)(col >> 5) * M + row] = ss;
+      const long nb = (N + 31) / 32;
+      part_m[(long)row * nb + (col >> 5)] = mm;
+      part_s[(long)row * nb + (col >> 5)] = ss;
     }
     if (ce_row_valid(row, M, time, targets, ignore_id)) {
       const long t = (long)targets[row + 1] - col;
@@ -237,12 +239,14 @@ __global__ __launch_bounds__(256) void ce_combine_kernel(const float* part_m, co
   const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   float m = -INFINITY;
-  for (long b = lane; b < nb; b += 64) m = __builtin_fmaxf(m, part_m[b * rows + row]);
+  const float* pm = part_m + row * nb;
+  const float* ps = part_s + row * nb;
+  for (long b = lane; b < nb; b += 64) m = __builtin_fmaxf(m, pm[b]);
   m = wave_max(m);
   float s = 0.0f;
   for (long b = lane; b < nb; b += 64) {
-    const float mb = part_m[b * rows + row];
-    if (mb > -INFINITY) s += part_s[b * rows + row] * expf(mb - m);
+    const float mb = pm[b];
+    if (mb > -INFINITY) s += ps[b] * expf(mb - m);
   }
   s = wave_sum(s);
   if (lane == 0) {
