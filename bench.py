@@ -38,9 +38,9 @@ FP16_PEAK_TFLOPS = 2516.6  # dense fp16 MFMA, MI355X
 # (FETCH_SIZE, WRITE_SIZE; KiB per dispatch) over this script with
 # --copy-mib 256, scaled by what the same counters read for the 256 MiB copy
 # kernel (FETCH_SIZE reads half the bytes copied: x2.0; WRITE_SIZE x1.0).
-# Summary: profiles/key_forward_hbm_traffic.txt. Re-measure when the kernel changes.
+# Summary: profiles/value_backward_hbm_traffic.txt. Re-measure when the kernel changes.
 TRAFFIC_BYTES = {
-    "key_forward": (1664.5 * 2.0 + 16384.0 * 1.0) * 1024,
+    "value_backward": (21703.0 * 2.0 + 12536.3 * 1.0) * 1024,
 }
 
 
