@@ -77,13 +77,16 @@ struct OpMK {
   static_assert(kBytes % 4096 == 0, "a stage must be whole wave-loads for 4 waves");
   static constexpr int kInst = kBytes / 4096;  // loads per wave per stage
   static constexpr int kExtra = 0;
-  static_assert(CPR == 4 || CPR == 8, "BK 32 or 64");
+  static_assert(CPR == 4 || CPR == 8 || CPR == 16 || CPR == 32, "BK 32, 64, 128 or 256");
   // LDS serves 16 lanes of a ds_read_b128 per cycle from a 256-byte bank
   // window: 16 consecutive rows must land in 16 distinct 16-byte slots.
-  // Rows are 64 B (BK 32: 4 rows per window) or 128 B (BK 64: 2 per window),
-  // so the chunk index is XORed with the row bits above those.
+  // Rows are 64 B (BK 32: 4 rows per window), 128 B (BK 64: 2 per window) or
+  // whole windows (BK 128 / 256), so the chunk index is XORed with the row
+  // bits above those.
   __device__ static int swz(int row) {
-    if constexpr (CPR == 8)
+    if constexpr (CPR >= 16)
+      return row & 15;
+    else if constexpr (CPR == 8)
       return (row >> 1) & 7;
     else
       return (row >> 2) & 3;
@@ -165,10 +168,11 @@ struct OpBits {
   int kofs;               // k offset into the rows (multiple of 32)
   static constexpr int WPR = BK / 32;  // words per row per stage
   static constexpr int kWords = ROWS * WPR;
-  static_assert(kWords % 4 == 0 && kWords / 4 <= 64, "bit tile must split into 4 wave loads");
+  static constexpr int kInst = kWords <= 256 ? 1 : kWords / 256;  // one word per lane per load
+  static_assert(kWords % 4 == 0 && (kInst == 1 || kWords % 256 == 0),
+                "bit tile must split into whole wave loads");
   static constexpr int kWordsPerWave = kWords / 4;
   static constexpr int kBytes = ((kWords * 4 + 255) / 256) * 256;
-  static constexpr int kInst = 1;
   static constexpr int kMaxScaleK = 8192;
   // extra: 16-entry sign table (128 B), then the scale range when SCALED.
   static constexpr int kLut = 128;
@@ -188,11 +192,15 @@ struct OpBits {
     }
   }
   __device__ __forceinline__ void issue(char* stage, int row0, int k0, int wave, int lane) const {
-    if (lane < kWordsPerWave) {
-      const int id = wave * kWordsPerWave + lane;
-      const int row = id / WPR, w = id % WPR;
-      const int r = min(row0 + row, rows - 1);
-      dma4(p + (long)r * ldw + ((kofs + k0) >> 5) + w, stage + wave * kWordsPerWave * 4);
+#pragma unroll
+    for (int t = 0; t < kInst; ++t) {
+      const int base = (wave * kInst + t) * (kWordsPerWave / kInst);
+      if (lane < kWordsPerWave / kInst) {
+        const int id = base + lane;
+        const int row = id / WPR, w = id % WPR;
+        const int r = min(row0 + row, rows - 1);
+        dma4(p + (long)r * ldw + ((kofs + k0) >> 5) + w, stage + base * 4);
+      }
     }
   }
   // k0rel: the stage's first k relative to the block's kbeg (scale index).
@@ -380,10 +388,6 @@ inline constexpr bool kHasSplit = false;
 template <class E>
 inline constexpr bool kHasSplit<E, decltype(std::declval<E&>().set_split(0))> = true;
 
-#ifndef ULLIS_LDS_SCHED
-#define ULLIS_LDS_SCHED 0
-#endif
-
 // LDS bytes of one block of the streamed-LDS GEMM: the stage ring (which the
 // epilogue reuses) and the operands' extra tables.
 template <int BM, int BN, int BK, int NS, class OA, class OB>
@@ -423,16 +427,6 @@ __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const
   const int kbeg = kz * k_split;
   const int kend = min(K, kbeg + k_split);
   const int nk = kend > kbeg ? (kend - kbeg) / BK : 0;
-#ifndef ULLIS_LDS_ROT
-#define ULLIS_LDS_ROT 0
-#endif
-#if ULLIS_LDS_ROT
-  const int rot = nk > 0 ? (bid >> 3) % nk : 0;
-#else
-  const int rot = 0;
-#endif
-  // K step of iteration kt
-  auto kstep = [&](int kt) { return kt + rot < nk ? kt + rot : kt + rot - nk; };
 
   floatx16 acc[TM][TN];
 #pragma unroll
@@ -444,72 +438,9 @@ __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const
   b.prepare(extra_b, kbeg, kend);
   auto issue = [&](int kt) {
     char* st = smem + (kt % NS) * STAGE;
-    a.issue(st, m0, kbeg + kstep(kt) * BK, wave, lane);
-    b.issue(st + OA::kBytes, n0, kbeg + kstep(kt) * BK, wave, lane);
+    a.issue(st, m0, kbeg + kt * BK, wave, lane);
+    b.issue(st + OA::kBytes, n0, kbeg + kt * BK, wave, lane);
   };
-  constexpr int KS = BK / 16;
-  // all MFMA operand fragments of stage kt (LDS -> registers)
-  auto read = [&](int kt, half8 (&xa)[KS][TM], half8 (&xb)[KS][TN]) {
-    const char* st = smem + (kt % NS) * STAGE;
-    const int k0rel = kstep(kt) * BK;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-        xa[ks][i] = a.frag(st, extra_a, wm * WM + i * 32, ks * 16, lane, k0rel);
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        xb[ks][j] = b.frag(st + OA::kBytes, extra_b, wn * WN + j * 32, ks * 16, lane, k0rel);
-    }
-  };
-  auto math = [&](const half8 (&xa)[KS][TM], const half8 (&xb)[KS][TN]) {
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa[ks][i], xb[ks][j], acc[i][j], 0, 0, 0);
-  };
-#if ULLIS_LDS_SCHED == 2
-  static_assert(IPS * (NS - 1) < 64, "pipeline depth");
-  // Register double buffer: the fragments of stage kt + 1 are read from LDS
-  // while the MFMAs of stage kt run. Once a stage's fragments are in
-  // registers its ring slot is free, so NS stages of global loads are issued
-  // ahead of the fragment reads. The K loop is unrolled twice so that the two
-  // fragment sets swap roles without register copies or branches around the
-  // reads (either would make the MFMAs wait for the reads just issued).
-#pragma unroll
-  for (int s = 0; s < NS; ++s)
-    if (s < nk) issue(s);
-  // stage kt (kt + 1 < nk): fragments of kt in (ca, cb), read kt + 1 into (na, nb)
-  auto step = [&](int kt, const half8 (&ca)[KS][TM], const half8 (&cb)[KS][TN],
-                  half8 (&na)[KS][TM], half8 (&nb)[KS][TN]) {
-    // stage kt + 1 has landed and every wave holds its stage-kt fragments
-    wait_stages<IPS, NS - 2>(nk - 2 - kt);
-    if (kt + NS < nk) issue(kt + NS);  // into the slot of stage kt
-    read(kt + 1, na, nb);
-    __builtin_amdgcn_sched_barrier(0);
-    math(ca, cb);
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  half8 fa[KS][TM], fb[KS][TN], ga[KS][TM], gb[KS][TN];
-  if (nk > 0) {
-    wait_stages<IPS, NS - 1>(nk - 1);  // stage 0 has landed
-    read(0, fa, fb);
-  }
-  int kt = 0;
-  for (; kt + 2 < nk; kt += 2) {
-    step(kt, fa, fb, ga, gb);
-    step(kt + 1, ga, gb, fa, fb);
-  }
-  if (kt + 1 < nk) {
-    step(kt, fa, fb, ga, gb);
-    math(ga, gb);
-  } else if (kt < nk) {
-    math(fa, fb);
-  }
-#else
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
     if (s < nk) issue(s);
@@ -518,14 +449,8 @@ __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const
     // Stage kt is complete once at most the later stages' loads are in flight.
     wait_stages<IPS, NS - 2>(nk - 1 - kt);
     if (kt + NS - 1 < nk) issue(kt + NS - 1);
-#if ULLIS_LDS_SCHED == 1
-    half8 fa[KS][TM], fb[KS][TN];
-    read(kt, fa, fb);
-    __builtin_amdgcn_sched_barrier(0);
-    math(fa, fb);
-#else
     const char* st = smem + (kt % NS) * STAGE;
-    const int k0rel = kstep(kt) * BK;
+    const int k0rel = kt * BK;
 #pragma unroll
     for (int ks = 0; ks < BK; ks += 16) {
       half8 af[TM], bf[TN];
@@ -540,9 +465,7 @@ __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const
         for (int j = 0; j < TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
-#endif
   }
-#endif
   wait_barrier<0>();  // every wave is done reading the ring
   if constexpr (kHasSplit<Epi>) epi.set_split(kz);
   epilogue_rows(epi, acc, reinterpret_cast<float*>(smem) + wave * kBufFloats, m0 + wm * WM,
@@ -610,12 +533,28 @@ __global__ __launch_bounds__(256) void gemm_lds_pair_kernel(LdsProblem<T1, OA1, 
 // beat 128x128 tiles (one block per CU) everywhere except very wide outputs
 // (the vocab head), where 128x128 tiles win; a 4-stage ring was best inside
 // the train step (2, 3 and 6 stages were slower).
+// Tile configs: 64x64 output tiles (one 32x32 MFMA block per wave). A
+// two-stage ring of BK = 128 halves the barrier round trips per MFMA of a
+// four-stage ring of BK = 64 in the same 64 KiB of LDS (two blocks per CU),
+// and measured faster at every heron shape (value fwd 12.7 -> 11.8 us, value
+// dW 16.7 -> 13.7 us, head dW 46.7 -> 36.8 us); 128x128 tiles were slower or
+// equal. BK = 64 serves contraction lengths that are not multiples of 128.
+struct LdsMid {
+  static constexpr int bm = 64, bn = 64, bk = 128, ns = 2;
+};
+struct LdsShort {
+  static constexpr int bm = 64, bn = 64, bk = 64, ns = 4;
+};
+struct LdsDeep {
+  static constexpr int bm = 64, bn = 64, bk = 128, ns = 4;
+};
 struct LdsBig {
   static constexpr int bm = 128, bn = 128, bk = 32, ns = 4;
 };
-struct LdsMid {
-  static constexpr int bm = 64, bn = 64, bk = 64, ns = 4;
-};
+// Per-call-site choice (with_lds): kAuto = LdsMid / LdsShort by K; kDeep =
+// the four-stage BK 128 ring for launches of one block per CU whose operands
+// come from HBM; kBig = 128x128 tiles.
+enum class LdsPolicy { kAuto, kDeep, kBig };
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool mk_ok(const void* p, long ld) { return p && aligned16(p) && ld % 8 == 0; }
@@ -625,18 +564,27 @@ inline bool km_ok(const void* p, long ld, long rows) {
 
 // Runs f(T) with the streamed-LDS tile config for an M x N output when K
 // splits into whole BK steps; returns false (and runs nothing) otherwise.
-// big_tiles: number of 128x128 tiles from which the 128x128 config is used.
 template <class F>
-bool with_lds(long M, long N, long K, int splits, hipError_t* err, F&& f, long big_tiles = 960) {
+bool with_lds(long M, long N, long K, int splits, hipError_t* err, F&& f,
+              LdsPolicy policy = LdsPolicy::kAuto) {
   if (M <= 0 || N <= 0 || K <= 0 || splits < 1) return false;
-  auto go = [&](auto t) {
-    using T = decltype(t);
-    if (K % T::bk != 0) return false;
-    *err = f(t);
+  if (policy == LdsPolicy::kDeep && K % LdsDeep::bk == 0) {
+    *err = f(LdsDeep{});
     return true;
-  };
-  if (cdiv(M, 128) * cdiv(N, 128) >= big_tiles) return go(LdsBig{});
-  return go(LdsMid{});
+  }
+  if (policy == LdsPolicy::kBig && K % LdsBig::bk == 0 && M % 128 == 0 && N % 128 == 0) {
+    *err = f(LdsBig{});
+    return true;
+  }
+  if (K % LdsMid::bk == 0) {
+    *err = f(LdsMid{});
+    return true;
+  }
+  if (K % LdsShort::bk == 0) {
+    *err = f(LdsShort{});
+    return true;
+  }
+  return false;
 }
 
 template <class T, class OA, class OB, class Epi, int G>
