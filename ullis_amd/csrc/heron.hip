@@ -13,6 +13,17 @@
 // gradients), LN0 backward at block 0.
 // Tapes stay resident in HBM between the forward and the backward.
 //
+// Two streams. With the automaton's indices given and rosa_grad =
+// stop_grad_bits, two parts of the step feed nothing else in it: the ROSA
+// Q/K/V branch (LN3, its mixes and the Q/K/V GEMMs, whose sign bit-planes are
+// an output only) and the O backward (O weight gradient and the e gradient;
+// ROSA passes no gradient to x). They run on a second stream (default
+// priority), ordered after their inputs by events, while the main stream
+// carries the residual chain; the main stream waits for the second one before
+// the end-of-step updates. Every buffer the second stream reads is final when
+// its event is recorded (x_l, the per-boundary fp16 gradient gx16_b[l], the
+// layer's amax slot), and it writes only buffers of its own.
+//
 // Parameter updates: each tensor is read only by its own layer's forward and
 // backward, and the reference updates it after its last read, so no kernel
 // later in the step reads an updated parameter. Every update is therefore
@@ -78,7 +89,16 @@ struct ullis_hip_heron {
   uint16_t *ln16 = nullptr, *q16 = nullptr, *k16 = nullptr, *v16 = nullptr;
   uint16_t *y16 = nullptr, *ln2_16 = nullptr, *shifted16 = nullptr;
   uint8_t* idx_rm = nullptr;
-  uint16_t *key16 = nullptr, *relu2_16 = nullptr, *gk16 = nullptr, *gx16 = nullptr;
+  uint16_t *key16 = nullptr, *relu2_16 = nullptr, *gk16 = nullptr;
+  // fp16 copy of the (scaled) gradient at each layer boundary x_l, l = 0..L:
+  // read by layer l's O backward and layer l-1's CMix backward
+  uint16_t* gx16_b = nullptr;
+  float* g_side = nullptr;       // O input-gradient scratch of the second stream's fallback path
+  uint16_t* ln3_16 = nullptr;    // LN3 output scratch of the second stream's fallback path
+  // second stream and its ordering events
+  hipStream_t side = nullptr;
+  std::vector<hipEvent_t> ev_fwd, ev_bwd;
+  hipEvent_t ev_join = nullptr;
   float *g_x = nullptr, *g_a = nullptr, *g_b = nullptr;
   float *slots = nullptr, *stats = nullptr;
   float* row_loss = nullptr;
@@ -417,7 +437,9 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
   add(2ul * nf * L);         // key16
   add(2ul * nf * L);         // relu2_16
   add(2ul * nf);             // gk16
-  add(2ul * nd);             // gx16
+  add(2ul * nd * (L + 1));   // gx16_b
+  add(4ul * nd);             // g_side
+  add(2ul * nd);             // ln3_16
   add(4ul * nd * 3);         // g_x g_a g_b
   add(4ul * gp_value * L);
   add(4ul * gp_key * L);
@@ -453,7 +475,9 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
   h->key16 = cv.take<uint16_t>(nf * L);
   h->relu2_16 = cv.take<uint16_t>(nf * L);
   h->gk16 = cv.take<uint16_t>(nf);
-  h->gx16 = cv.take<uint16_t>(nd);
+  h->gx16_b = cv.take<uint16_t>(nd * (L + 1));
+  h->g_side = cv.take<float>(nd);
+  h->ln3_16 = cv.take<uint16_t>(nd);
   h->g_x = cv.take<float>(nd);
   h->g_a = cv.take<float>(nd);
   h->g_b = cv.take<float>(nd);
@@ -476,6 +500,18 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
     ullis_hip_heron_destroy(h);
     return rc;
   }
+  {
+    bool ok2 = hipStreamCreateWithFlags(&h->side, hipStreamNonBlocking) == hipSuccess;
+    h->ev_fwd.assign(L, nullptr);
+    h->ev_bwd.assign(L, nullptr);
+    for (auto* v : {&h->ev_fwd, &h->ev_bwd})
+      for (auto& e : *v) ok2 = ok2 && hipEventCreateWithFlags(&e, hipEventDisableTiming) == hipSuccess;
+    ok2 = ok2 && hipEventCreateWithFlags(&h->ev_join, hipEventDisableTiming) == hipSuccess;
+    if (!ok2) {
+      ullis_hip_heron_destroy(h);
+      return c->fail(ULLIS_HIP_ERR_RUNTIME, "heron stream / event creation failed");
+    }
+  }
   h->probe_events.resize(2 * kProbeMax);
   for (auto& e : h->probe_events) {
     if (hipEventCreate(&e) != hipSuccess) {
@@ -496,6 +532,12 @@ void ullis_hip_heron_destroy(ullis_hip_heron* h) {
   if (!h) return;
   if (h->ctx) (void)hipStreamSynchronize(h->ctx->stream);
   for (auto& e : h->probe_events) (void)hipEventDestroy(e);
+  if (h->side) (void)hipStreamSynchronize(h->side);
+  for (auto* v : {&h->ev_fwd, &h->ev_bwd})
+    for (auto& e : *v)
+      if (e) (void)hipEventDestroy(e);
+  if (h->ev_join) (void)hipEventDestroy(h->ev_join);
+  if (h->side) (void)hipStreamDestroy(h->side);
   if (h->arena) (void)hipFree(h->arena);
   if (h->act) (void)hipFree(h->act);
   if (h->job_mem) (void)hipFree(h->job_mem);
@@ -579,9 +621,12 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
     } else if (l == 0) {
       STEP(copy_device(s, x_l, x_emb, (long)sizeof(float) * nd), "copy x");
     }
-    // ROSA block (src/model.rs:1354-1440)
-    STEP(layer_norm_mix_forward(s, x_l, R, T, D, b.ln3.w, b.ln3.b, h->ln16, false, b.x_q, h->q16,
-                                b.x_k, h->k16, b.x_v, h->v16),
+    // ROSA block (src/model.rs:1354-1440). The Q/K/V branch runs on the
+    // second stream once x_l is complete.
+    STEP(hipEventRecord(h->ev_fwd[l], s), "event");
+    STEP(hipStreamWaitEvent(h->side, h->ev_fwd[l], 0), "event wait");
+    STEP(layer_norm_mix_forward(h->side, x_l, R, T, D, b.ln3.w, b.ln3.b, h->ln3_16, false, b.x_q,
+                                h->q16, b.x_k, h->k16, b.x_v, h->v16),
          "ln3 + mix3");
     {
       const uint16_t* const xin[3] = {h->q16, h->k16, h->v16};
@@ -590,7 +635,7 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
       const uint16_t* const bi[3] = {b.q.bias, b.k.bias, b.v.bias};
       uint32_t* const planes[3] = {qkv + (l * 3 + 0) * words, qkv + (l * 3 + 1) * words,
                                    qkv + (l * 3 + 2) * words};
-      STEP(packed_forward_bits3(s, xin, R, D, D, wb, sc, bi, planes), "qkv");
+      STEP(packed_forward_bits3(h->side, xin, R, D, D, wb, sc, bi, planes), "qkv");
     }
     uint16_t* y16 = h->y16 + l * nd;
     float* ar = h->after_rosa + l * nd;
@@ -652,7 +697,7 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
                                 h->pt_lnout, &nb),
        "ln_out bwd");
   if (nb != h->nb_ln) return c->fail(ULLIS_HIP_ERR_RUNTIME, "ln_out backward partial count");
-  STEP(scale_to_f16(s, h->g_x, nd, h->slots + L, h->gx16), "g_x fp16");
+  STEP(scale_to_f16(s, h->g_x, nd, h->slots + L, h->gx16_b + L * nd), "g_x fp16");
 
   // ------------------------------------------------------------ backward
   for (long l = L - 1; l >= 0; --l) {
@@ -670,7 +715,7 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
     // backward into gk16) with the value weight gradient, then the key input
     // gradient with the key weight gradient
     {
-      const GradIn gx{h->g_x, slot_in, h->gx16};
+      const GradIn gx{h->g_x, slot_in, h->gx16_b + (l + 1) * nd};
       PROBED(ULLIS_HIP_PROBE_VALUE_BACKWARD,
              fp16_backward_pair(s, Fp16DxArgs{gx, R, F, D, b.value, nullptr, key, h->gk16},
                                 WeightGradArgs{gx, nullptr, r2, R, F, D, h->splits_value,
@@ -699,23 +744,28 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
     }
     // O bias gradient (column sums of g_x) and the fp16 copy of g_x for the
     // O GEMMs here and the CMix GEMMs of the block below.
-    STEP(column_sum_partials(s, h->g_x, nullptr, R, D, h->pt_ob + l * pc, &nb, h->gx16, slot_mid),
+    uint16_t* gx16_l = h->gx16_b + l * nd;
+    STEP(column_sum_partials(s, h->g_x, nullptr, R, D, h->pt_ob + l * pc, &nb, gx16_l, slot_mid),
          "o g_bias + g_x fp16");
     if (nb != h->nb_col) return c->fail(ULLIS_HIP_ERR_RUNTIME, "o bias partial count");
 
-    // ROSA O stop-grad backward (src/model.rs:1491-1522): the O weight
-    // gradient, and the O input gradient g_y reduced straight to the e
-    // gradient partials (g_e = column sums of g_y * (2 idx - 1); with
-    // stop_grad_bits nothing else reads g_y)
+    // ROSA O stop-grad backward (src/model.rs:1491-1522) on the second
+    // stream: the O weight gradient, and the O input gradient g_y reduced
+    // straight to the e gradient partials (g_e = column sums of
+    // g_y * (2 idx - 1); with stop_grad_bits nothing else reads g_y). It reads
+    // only the fp16 gradient copy of this boundary and this layer's amax slot,
+    // both final here.
+    STEP(hipEventRecord(h->ev_bwd[l], s), "event");
+    STEP(hipStreamWaitEvent(h->side, h->ev_bwd[l], 0), "event wait");
     {
-      const GradIn gx{h->g_x, slot_mid, h->gx16};
-      PackedDxArgs dx{gx, nullptr, R, D, D, b.o.bits_t, b.o.scale, h->g_a, nullptr, 0};
+      const GradIn g16_only{nullptr, slot_mid};
+      PackedDxArgs dx{g16_only, gx16_l, R, D, D, b.o.bits_t, b.o.scale, h->g_side, nullptr, 0};
       dx.sign_idx = h->idx_rm + l * nd;
       dx.col_part = h->pt_e + l * pc;  // column_partial_blocks(R) groups of 16 rows
       PROBED(ULLIS_HIP_PROBE_O_BACKWARD,
-             packed_backward_pair(s, dx,
-                                  WeightGradArgs{gx, nullptr, h->y16 + l * nd, R, D, D, h->splits_o,
-                                                 h->gp_o + l * h->splits_o * D * D}),
+             packed_backward_pair(h->side, dx,
+                                  WeightGradArgs{g16_only, gx16_l, h->y16 + l * nd, R, D, D,
+                                                 h->splits_o, h->gp_o + l * h->splits_o * D * D}),
              "o backward");
     }
 
@@ -735,6 +785,10 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
       STEP(copy_device(s, g_emb, h->g_x, (long)sizeof(float) * nd), "copy g_emb");
     }
   }
+
+  // the second stream's work is done before the updates and the step's end
+  STEP(hipEventRecord(h->ev_join, h->side), "event");
+  STEP(hipStreamWaitEvent(s, h->ev_join, 0), "event wait");
 
   // ------------------------------------------------ end-of-step updates
   // vector steps (LN gamma / beta, x_k, O bias, e, head bias at 8 lr)
