@@ -115,9 +115,18 @@ struct ullis_hip_heron {
   const F16Job* f16_jobs = nullptr;
   const FinishJob* fin_jobs = nullptr;
   const TransJob* trans_jobs = nullptr;
-  int n_vec = 0, n_f16 = 0, n_fin = 0, n_trans = 0;
-  int vec_blocks = 0, f16_blocks = 0, fin_blocks = 0, trans_blocks = 0;
-  int ln0_job_blocks = 0;  // blocks of the trailing LN0 job (0: none)
+  // The tables are cut into L + 1 segments: segment l holds layer l's jobs
+  // (run on the second stream once its O backward is done), segment L the
+  // LN_out, head and LN0 jobs (run at the step's end); block0 values start at
+  // 0 in every segment.
+  struct JobRange {
+    int j0 = 0, n = 0, blocks = 0;
+  };
+  struct UpdateSeg {
+    JobRange vec, f16, fin, trans;
+  };
+  std::vector<UpdateSeg> seg;
+  int ln0_job_blocks = 0;  // blocks of the tail's trailing LN0 job (0: none)
   std::vector<const Packed*> trans_generic;  // bits_t rebuilt by the generic transpose
   // ROSA e of every layer (host array and a device copy) for the expand of all
   // layers' ROSA outputs in one launch
@@ -208,6 +217,10 @@ constexpr int kProbeMax = 512;
     }                                                                              \
   } while (0)
 
+struct HeronSegStart {
+  int v, f, p, t;
+};
+
 // Job tables of the end-of-step updates (every pointer in them is fixed for
 // the life of the trainer), uploaded once.
 int build_update_jobs(ullis_hip_heron* h) {
@@ -218,8 +231,21 @@ int build_update_jobs(ullis_hip_heron* h) {
   std::vector<F16Job> fj;
   std::vector<FinishJob> pj;
   std::vector<TransJob> tj;
-  int vb = 0, fb = 0, pb = 0, tb = 0;
+  int vb = 0, fb = 0, pb = 0, tb = 0;  // blocks of the open segment
   bool vec_ok = true;
+  auto open_seg = [&] {
+    HeronSegStart st{(int)vj.size(), (int)fj.size(), (int)pj.size(), (int)tj.size()};
+    vb = fb = pb = tb = 0;
+    return st;
+  };
+  auto close_seg = [&](const HeronSegStart& st) {
+    ullis_hip_heron::UpdateSeg g;
+    g.vec = {st.v, (int)vj.size() - st.v, vb};
+    g.f16 = {st.f, (int)fj.size() - st.f, fb};
+    g.fin = {st.p, (int)pj.size() - st.p, pb};
+    g.trans = {st.t, (int)tj.size() - st.t, tb};
+    h->seg.push_back(g);
+  };
   auto vec2 = [&](const float* part, int nblk, long ch, bool two, VecTarget a, VecTarget b) {
     VecJob j{part, nblk, two ? 2 * ch : ch, ch, a, two ? b : a, vb};
     vb += vec_job_blocks(j.ncols);
@@ -268,6 +294,7 @@ int build_update_jobs(ullis_hip_heron* h) {
   };
 
   for (long l = 0; l < L; ++l) {
+    const HeronSegStart st = open_seg();
     Block& b = h->blocks[l];
     const long pc = (long)h->nb_col * D;
     vec2(h->pt_mix + l * h->nb_mix * D, h->nb_mix, D, false, sgd(b.cx_k, b.cx_k_res, 1.0f, nullptr),
@@ -283,7 +310,11 @@ int build_update_jobs(ullis_hip_heron* h) {
     packed(b.key, 0, F, h->gp_key + l * h->splits_key * F * D, h->splits_key, h->slots + l + 1,
            nullptr);
     packed(b.o, 0, D, h->gp_o + l * h->splits_o * D * D, h->splits_o, h->slots + l, nullptr);
+    rebuild(b.key);
+    rebuild(b.o);
+    close_seg(st);
   }
+  const HeronSegStart tail = open_seg();
   ln(h->ln_out, h->pt_lnout, h->nb_ln);
   // head bias: g_bias = gscale * column sums, step at 8 lr (src/model.rs:3118-3130)
   vec2(head_ce_bias_partials(h->head_ws, R, D, V), (int)cdiv(R, 32), V, false,
@@ -300,11 +331,8 @@ int build_update_jobs(ullis_hip_heron* h) {
     ln(h->blocks[0].ln0, h->pt_ln0, h->nb_ln);
     h->ln0_job_blocks = vb - before;
   }
-  for (const Block& b : h->blocks) {
-    rebuild(b.key);
-    rebuild(b.o);
-  }
   rebuild(h->head);
+  close_seg(tail);
   if (!vec_ok)
     return c->fail(ULLIS_HIP_ERR_INVALID, "heron update tensors are not 16-byte aligned");
 
@@ -327,16 +355,28 @@ int build_update_jobs(ullis_hip_heron* h) {
     return c->hip(hipMemcpy(d, v.data(), sizeof(J) * v.size(), hipMemcpyHostToDevice),
                   "heron update job upload");
   };
-  if (int rc = up(vj, h->vec_jobs, h->n_vec)) return rc;
-  if (int rc = up(fj, h->f16_jobs, h->n_f16)) return rc;
-  if (int rc = up(pj, h->fin_jobs, h->n_fin)) return rc;
-  if (int rc = up(tj, h->trans_jobs, h->n_trans)) return rc;
-  int n_e = 0;
-  if (int rc = up(h->e_host, h->e_dev, n_e)) return rc;
-  h->vec_blocks = vb;
-  h->f16_blocks = fb;
-  h->fin_blocks = pb;
-  h->trans_blocks = tb;
+  int n = 0;
+  if (int rc = up(vj, h->vec_jobs, n)) return rc;
+  if (int rc = up(fj, h->f16_jobs, n)) return rc;
+  if (int rc = up(pj, h->fin_jobs, n)) return rc;
+  if (int rc = up(tj, h->trans_jobs, n)) return rc;
+  if (int rc = up(h->e_host, h->e_dev, n)) return rc;
+  return 0;
+}
+
+// The update launches of one segment (drop_last_vec: leave out its last vector
+// job and that job's blocks).
+int run_update_seg(ullis_hip_heron* h, hipStream_t s, int l, float lr, bool drop_last_vec) {
+  ullis_hip_ctx* c = h->ctx;
+  const ullis_hip_heron::UpdateSeg& g = h->seg[l];
+  const int nv = g.vec.n - (drop_last_vec && h->ln0_job_blocks ? 1 : 0);
+  const int bv = g.vec.blocks - (drop_last_vec ? h->ln0_job_blocks : 0);
+  // vector steps (LN gamma / beta, x_k, O bias, e, head bias at 8 lr)
+  STEP(run_vec_jobs(s, h->vec_jobs + g.vec.j0, nv, bv, lr), "vector steps");
+  STEP(run_f16_jobs(s, h->f16_jobs + g.f16.j0, g.f16.n, g.f16.blocks, lr), "value steps");
+  STEP(run_finish_jobs(s, h->fin_jobs + g.fin.j0, g.fin.n, g.fin.blocks, lr),
+       "latent / scale steps");
+  STEP(run_trans_jobs(s, h->trans_jobs + g.trans.j0, g.trans.n, g.trans.blocks), "bits_t");
   return 0;
 }
 
@@ -768,6 +808,9 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
                                                  h->splits_o, h->gp_o + l * h->splits_o * D * D}),
              "o backward");
     }
+    // every gradient of layer l is complete: its updates run on the second
+    // stream too (nothing later in the step reads layer l's parameters)
+    if (int rc = run_update_seg(h, h->side, (int)l, lr, false)) return rc;
 
     if (b.has_ln0) {  // (src/model.rs:2978-2982)
       STEP(layer_norm_backward_rows(s, x_emb, h->g_x, R, D, b.ln0.w, g_emb, 0, nullptr, h->pt_ln0,
@@ -791,13 +834,8 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
   STEP(hipStreamWaitEvent(s, h->ev_join, 0), "event wait");
 
   // ------------------------------------------------ end-of-step updates
-  // vector steps (LN gamma / beta, x_k, O bias, e, head bias at 8 lr)
-  STEP(run_vec_jobs(s, h->vec_jobs, h->n_vec - (ln0_now && h->ln0_job_blocks ? 1 : 0),
-                    h->vec_blocks - (ln0_now ? h->ln0_job_blocks : 0), lr),
-       "vector steps");
-  STEP(run_f16_jobs(s, h->f16_jobs, h->n_f16, h->f16_blocks, lr), "value steps");
-  STEP(run_finish_jobs(s, h->fin_jobs, h->n_fin, h->fin_blocks, lr), "latent / scale steps");
-  STEP(run_trans_jobs(s, h->trans_jobs, h->n_trans, h->trans_blocks), "bits_t");
+  // LN_out, head and LN0 (the layers' own ran on the second stream)
+  if (int rc = run_update_seg(h, s, (int)L, lr, ln0_now)) return rc;
   for (const Packed* k : h->trans_generic)
     STEP(transpose_bits(s, k->bits, k->out, k->in, k->bits_t), "bits_t");
   return 0;
