@@ -755,19 +755,22 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
     // backward into gk16) with the value weight gradient, then the key input
     // gradient with the key weight gradient
     {
-      const GradIn gx{h->g_x, slot_in, h->gx16_b + (l + 1) * nd};
+      uint16_t* gx16_in = h->gx16_b + (l + 1) * nd;
+      uint16_t* gk16 = h->gk16;
+      const GradIn gx{h->g_x, slot_in, gx16_in};
+      const GradIn g16_only{nullptr, slot_in};
+      const WeightGradArgs vdw{g16_only, gx16_in, r2, R, F, D, h->splits_value,
+                               h->gp_value + l * h->splits_value * D * F};
+      const WeightGradArgs kdw{g16_only, gk16, sh, R, D, F, h->splits_key,
+                               h->gp_key + l * h->splits_key * F * D};
       PROBED(ULLIS_HIP_PROBE_VALUE_BACKWARD,
-             fp16_backward_pair(s, Fp16DxArgs{gx, R, F, D, b.value, nullptr, key, h->gk16},
-                                WeightGradArgs{gx, nullptr, r2, R, F, D, h->splits_value,
-                                               h->gp_value + l * h->splits_value * D * F}),
+             fp16_backward_pair(s, Fp16DxArgs{gx, R, F, D, b.value, nullptr, key, gk16}, vdw),
              "value backward");
-      const GradIn gk{nullptr, slot_in};
       PROBED(ULLIS_HIP_PROBE_KEY_BACKWARD,
              packed_backward_pair(s,
-                                  PackedDxArgs{gk, h->gk16, R, D, F, b.key.bits_t, b.key.scale,
+                                  PackedDxArgs{g16_only, gk16, R, D, F, b.key.bits_t, b.key.scale,
                                                h->g_a, nullptr, 0},
-                                  WeightGradArgs{gk, h->gk16, sh, R, D, F, h->splits_key,
-                                                 h->gp_key + l * h->splits_key * F * D}),
+                                  kdw),
              "key backward");
     }
     // CMix time-shift mix backward (x_k gradient) fused with the LN2
