@@ -506,26 +506,48 @@ struct LdsProblem {
   TileMap map;
 };
 
-// Two independent GEMMs (possibly of different tile configs and operand
-// kinds) in one launch: blocks [0, p1.blocks) run p1, the rest p2, so the
-// blocks of both share the CUs and their operand streams overlap.
-template <class T1, class OA1, class OB1, class E1, class T2, class OA2, class OB2, class E2>
-__global__ __launch_bounds__(256) void gemm_lds_pair_kernel(LdsProblem<T1, OA1, OB1, E1> p1,
-                                                            LdsProblem<T2, OA2, OB2, E2> p2) {
-  constexpr int S1 = lds_smem_bytes<T1::bm, T1::bn, T1::bk, T1::ns, OA1, OB1>();
-  constexpr int S2 = lds_smem_bytes<T2::bm, T2::bn, T2::bk, T2::ns, OA2, OB2>();
-  __shared__ __attribute__((aligned(1024))) char smem[S1 > S2 ? S1 : S2];
-  const int bid = blockIdx.x;
-  if (bid < p1.blocks) {
-    const int z = p1.blocks == p1.tiles ? 0 : bid / p1.tiles;
-    gemm_lds_body<T1::bm, T1::bn, T1::bk, T1::ns>(smem, bid - z * p1.tiles, z, p1.a, p1.b, p1.epi,
-                                                  p1.M, p1.N, p1.K, p1.k_split, p1.map);
-  } else {
-    const int b2 = bid - p1.blocks;
-    const int z = p2.blocks == p2.tiles ? 0 : b2 / p2.tiles;
-    gemm_lds_body<T2::bm, T2::bn, T2::bk, T2::ns>(smem, b2 - z * p2.tiles, z, p2.a, p2.b, p2.epi,
-                                                  p2.M, p2.N, p2.K, p2.k_split, p2.map);
-  }
+constexpr int max_of(int a) { return a; }
+template <class... R>
+constexpr int max_of(int a, R... r) {
+  const int m = max_of(r...);
+  return a > m ? a : m;
+}
+
+template <class P>
+struct LdsProblemSmem;
+template <class T, class OA, class OB, class Epi>
+struct LdsProblemSmem<LdsProblem<T, OA, OB, Epi>> {
+  static constexpr int value = lds_smem_bytes<T::bm, T::bn, T::bk, T::ns, OA, OB>();
+};
+
+template <class T, class OA, class OB, class Epi>
+__device__ __forceinline__ void run_lds_problem(char* smem, const LdsProblem<T, OA, OB, Epi>& p,
+                                                int bid) {
+  const int z = p.blocks == p.tiles ? 0 : bid / p.tiles;
+  Epi epi = p.epi;
+  gemm_lds_body<T::bm, T::bn, T::bk, T::ns>(smem, bid - z * p.tiles, z, p.a, p.b, epi, p.M, p.N,
+                                            p.K, p.k_split, p.map);
+}
+
+// Independent GEMMs (possibly of different tile configs, operand kinds and
+// epilogues) in one launch: the first ps[0].blocks blocks run ps[0], the next
+// ps[1].blocks run ps[1], ..., so the blocks of all of them share the CUs.
+template <class... Ps>
+__global__ __launch_bounds__(256) void gemm_lds_multi_kernel(Ps... ps) {
+  constexpr int S = max_of(LdsProblemSmem<Ps>::value...);
+  __shared__ __attribute__((aligned(1024))) char smem[S];
+  int bid = blockIdx.x;
+  bool done = false;
+  auto one = [&](const auto& p) {
+    if (done) return;
+    if (bid < p.blocks) {
+      run_lds_problem(smem, p, bid);
+      done = true;
+    } else {
+      bid -= p.blocks;
+    }
+  };
+  (one(ps), ...);
 }
 
 // ------------------------------------------------------------ host dispatch
@@ -631,12 +653,16 @@ hipError_t launch_lds_problem(hipStream_t s, const LdsProblem<T, OA, OB, Epi>& p
 }
 
 // Shapes must fit int32 (lds_problem's callers check M, N, K).
-template <class T1, class OA1, class OB1, class E1, class T2, class OA2, class OB2, class E2>
-hipError_t launch_lds_pair(hipStream_t s, const LdsProblem<T1, OA1, OB1, E1>& p1,
-                           const LdsProblem<T2, OA2, OB2, E2>& p2) {
-  launch((gemm_lds_pair_kernel<T1, OA1, OB1, E1, T2, OA2, OB2, E2>),
-         dim3((unsigned)(p1.blocks + p2.blocks)), dim3(kThreads), 0, s, p1, p2);
+template <class... Ps>
+hipError_t launch_lds_multi(hipStream_t s, const Ps&... ps) {
+  launch((gemm_lds_multi_kernel<Ps...>), dim3((unsigned)(0 + ... + ps.blocks)), dim3(kThreads), 0,
+         s, ps...);
   return hipGetLastError();
+}
+
+template <class P1, class P2>
+hipError_t launch_lds_pair(hipStream_t s, const P1& p1, const P2& p2) {
+  return launch_lds_multi(s, p1, p2);
 }
 
 }  // namespace lds
