@@ -98,7 +98,7 @@ struct ullis_hip_heron {
   // second stream and its ordering events
   hipStream_t side = nullptr;
   std::vector<hipEvent_t> ev_fwd, ev_bwd;
-  hipEvent_t ev_join = nullptr;
+  hipEvent_t ev_join = nullptr, ev_head = nullptr;
   float *g_x = nullptr, *g_a = nullptr, *g_b = nullptr;
   float *slots = nullptr, *stats = nullptr;
   float* row_loss = nullptr;
@@ -115,10 +115,11 @@ struct ullis_hip_heron {
   const F16Job* f16_jobs = nullptr;
   const FinishJob* fin_jobs = nullptr;
   const TransJob* trans_jobs = nullptr;
-  // The tables are cut into L + 1 segments: segment l holds layer l's jobs
+  // The tables are cut into L + 2 segments: segment l holds layer l's jobs
   // (run on the second stream once its O backward is done), segment L the
-  // LN_out, head and LN0 jobs (run at the step's end); block0 values start at
-  // 0 in every segment.
+  // LN_out and head jobs (on the second stream once LN_out's backward is
+  // done), segment L + 1 the LN0 job (at the step's end); block0 values start
+  // at 0 in every segment.
   struct JobRange {
     int j0 = 0, n = 0, blocks = 0;
   };
@@ -126,7 +127,6 @@ struct ullis_hip_heron {
     JobRange vec, f16, fin, trans;
   };
   std::vector<UpdateSeg> seg;
-  int ln0_job_blocks = 0;  // blocks of the tail's trailing LN0 job (0: none)
   std::vector<const Packed*> trans_generic;  // bits_t rebuilt by the generic transpose
   // ROSA e of every layer (host array and a device copy) for the expand of all
   // layers' ROSA outputs in one launch
@@ -326,13 +326,11 @@ int build_update_jobs(ullis_hip_heron* h) {
       packed(h->head, c0, V - c0 < vc ? V - c0 : vc, h->gp_head + ci * sp * vc * D, sp, nullptr,
              h->stats + 2);
   }
-  if (h->blocks[0].has_ln0) {
-    const int before = vb;
-    ln(h->blocks[0].ln0, h->pt_ln0, h->nb_ln);
-    h->ln0_job_blocks = vb - before;
-  }
   rebuild(h->head);
   close_seg(tail);
+  const HeronSegStart last = open_seg();
+  if (h->blocks[0].has_ln0) ln(h->blocks[0].ln0, h->pt_ln0, h->nb_ln);
+  close_seg(last);
   if (!vec_ok)
     return c->fail(ULLIS_HIP_ERR_INVALID, "heron update tensors are not 16-byte aligned");
 
@@ -364,15 +362,12 @@ int build_update_jobs(ullis_hip_heron* h) {
   return 0;
 }
 
-// The update launches of one segment (drop_last_vec: leave out its last vector
-// job and that job's blocks).
-int run_update_seg(ullis_hip_heron* h, hipStream_t s, int l, float lr, bool drop_last_vec) {
+// The update launches of one segment.
+int run_update_seg(ullis_hip_heron* h, hipStream_t s, int l, float lr) {
   ullis_hip_ctx* c = h->ctx;
   const ullis_hip_heron::UpdateSeg& g = h->seg[l];
-  const int nv = g.vec.n - (drop_last_vec && h->ln0_job_blocks ? 1 : 0);
-  const int bv = g.vec.blocks - (drop_last_vec ? h->ln0_job_blocks : 0);
   // vector steps (LN gamma / beta, x_k, O bias, e, head bias at 8 lr)
-  STEP(run_vec_jobs(s, h->vec_jobs + g.vec.j0, nv, bv, lr), "vector steps");
+  STEP(run_vec_jobs(s, h->vec_jobs + g.vec.j0, g.vec.n, g.vec.blocks, lr), "vector steps");
   STEP(run_f16_jobs(s, h->f16_jobs + g.f16.j0, g.f16.n, g.f16.blocks, lr), "value steps");
   STEP(run_finish_jobs(s, h->fin_jobs + g.fin.j0, g.fin.n, g.fin.blocks, lr),
        "latent / scale steps");
@@ -547,6 +542,7 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
     for (auto* v : {&h->ev_fwd, &h->ev_bwd})
       for (auto& e : *v) ok2 = ok2 && hipEventCreateWithFlags(&e, hipEventDisableTiming) == hipSuccess;
     ok2 = ok2 && hipEventCreateWithFlags(&h->ev_join, hipEventDisableTiming) == hipSuccess;
+    ok2 = ok2 && hipEventCreateWithFlags(&h->ev_head, hipEventDisableTiming) == hipSuccess;
     if (!ok2) {
       ullis_hip_heron_destroy(h);
       return c->fail(ULLIS_HIP_ERR_RUNTIME, "heron stream / event creation failed");
@@ -577,6 +573,7 @@ void ullis_hip_heron_destroy(ullis_hip_heron* h) {
     for (auto& e : *v)
       if (e) (void)hipEventDestroy(e);
   if (h->ev_join) (void)hipEventDestroy(h->ev_join);
+  if (h->ev_head) (void)hipEventDestroy(h->ev_head);
   if (h->side) (void)hipStreamDestroy(h->side);
   if (h->arena) (void)hipFree(h->arena);
   if (h->act) (void)hipFree(h->act);
@@ -737,6 +734,11 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
                                 h->pt_lnout, &nb),
        "ln_out bwd");
   if (nb != h->nb_ln) return c->fail(ULLIS_HIP_ERR_RUNTIME, "ln_out backward partial count");
+  // the head and LN_out gradients are complete: their updates run on the
+  // second stream (nothing later in the step reads those parameters)
+  STEP(hipEventRecord(h->ev_head, s), "event");
+  STEP(hipStreamWaitEvent(h->side, h->ev_head, 0), "event wait");
+  if (int rc = run_update_seg(h, h->side, (int)L, lr)) return rc;
   STEP(scale_to_f16(s, h->g_x, nd, h->slots + L, h->gx16_b + L * nd), "g_x fp16");
 
   // ------------------------------------------------------------ backward
@@ -813,7 +815,7 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
     }
     // every gradient of layer l is complete: its updates run on the second
     // stream too (nothing later in the step reads layer l's parameters)
-    if (int rc = run_update_seg(h, h->side, (int)l, lr, false)) return rc;
+    if (int rc = run_update_seg(h, h->side, (int)l, lr)) return rc;
 
     if (b.has_ln0) {  // (src/model.rs:2978-2982)
       STEP(layer_norm_backward_rows(s, x_emb, h->g_x, R, D, b.ln0.w, g_emb, 0, nullptr, h->pt_ln0,
@@ -837,8 +839,9 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
   STEP(hipStreamWaitEvent(s, h->ev_join, 0), "event wait");
 
   // ------------------------------------------------ end-of-step updates
-  // LN_out, head and LN0 (the layers' own ran on the second stream)
-  if (int rc = run_update_seg(h, s, (int)L, lr, ln0_now)) return rc;
+  // LN0 (unless LN0 backward took the other path and stepped it already)
+  if (!ln0_now)
+    if (int rc = run_update_seg(h, s, (int)L + 1, lr)) return rc;
   for (const Packed* k : h->trans_generic)
     STEP(transpose_bits(s, k->bits, k->out, k->in, k->bits_t), "bits_t");
   return 0;
