@@ -10,10 +10,11 @@ region is bracketed by stream synchronisation; HIP events on the library's
 stream give the step time.
 
 Prints ONE JSON line. `roofline` is for the kernel that dominates the step,
-timed by the kernel timestamps of its own launches (ullis_hip_heron_probe)
-over a second pass of the same number of steps right after the reported
-one: arming the probe orders the step's second stream around the probed
-launches and slows the step, so it stays out of the reported steps.
+timed over a second pass of the same number of steps right after the
+reported one (ullis_hip_heron_probe): every workgroup of a probed launch
+writes its start and end on the device wall clock, and a launch lasts from
+the earliest start to the latest end. The probe pass is kept out of the
+reported steps because the stamps themselves cost a little.
 `cpu_baseline` times the CPU oracle (a port of the
 reference's CPU backend) single-threaded on a bounded sample of the same
 workload (fewer rows, same widths and depth), scaled per token.
@@ -43,7 +44,7 @@ FP16_PEAK_TFLOPS = 2516.6  # dense fp16 MFMA, MI355X
 # kernel (FETCH_SIZE reads half the bytes copied: x2.0; WRITE_SIZE x1.0).
 # Summary: profiles/value_backward_hbm_traffic.txt. Re-measure when the kernel changes.
 TRAFFIC_BYTES = {
-    "value_backward": (21703.0 * 2.0 + 12536.3 * 1.0) * 1024,
+    "value_backward": (21648.5 * 2.0 + 12649.5 * 1.0) * 1024,
 }
 
 
@@ -155,9 +156,8 @@ def main() -> int:
     tokens = shape.rows * args.steps
     value = tokens / (total_ms / 1e3)
     loss = float(st.download(np.float32, 4)[0])
-    # the roofline object: K more steps with the probe armed (the probe's
-    # timestamped launches order the step's second stream around the probed
-    # kernel, so they are kept out of the reported steps)
+    # the roofline object: K more steps with the probe armed (the stamping
+    # launches are kept out of the reported steps)
     kernel, probe_ms = None, None
     if args.probe != "none":
         probe = trainer.probe_begin(args.probe)

@@ -150,19 +150,29 @@ def test_full_heron_step_properties(rt):
     x, labels, idx = step_inputs(shape.rows, 512, 8192, 12, 1, 2048)
     dx, dl, di = rt.put(x), rt.put(labels), rt.put(idx)
     outs = []
-    for _ in range(2):  # same start state twice: bit-identical (deterministic reductions)
+    # same start state each time: bit-identical (deterministic reductions),
+    # also with a launch probe armed (stamped GEMM launches, event-timed
+    # LayerNorm launches)
+    for probe in (None, None, "value_backward", "ln_backward"):
         trainer.upload_arena(arena)
         g = rt.zeros(np.float32, shape.rows * 512)
         rl = rt.zeros(np.float32, shape.rows)
         st = rt.zeros(np.float32, 4)
+        if probe:
+            trainer.probe_begin(probe)
         trainer.step(dx, dl, NO_IGNORE, 0.01, di, g, rl, st)
         rt.sync()
+        if probe:
+            k = trainer.probe_end(probe)
+            assert k["count"] == 12, (probe, k)
+            assert 1e-3 < k["total_ms"] / k["count"] < 5.0, (probe, k)
         outs.append((trainer.download_arena(), g.download(np.float32), rl.download(np.float32),
                      st.download(np.float32)))
-    (a0, g0, r0, s0), (a1, g1, r1, s1) = outs
-    np.testing.assert_array_equal(a0, a1)
-    np.testing.assert_array_equal(g0.view(np.uint32), g1.view(np.uint32))
-    np.testing.assert_array_equal(r0.view(np.uint32), r1.view(np.uint32))
+    a0, g0, r0, s0 = outs[0]
+    for a1, g1, r1, _ in outs[1:]:
+        np.testing.assert_array_equal(a0, a1)
+        np.testing.assert_array_equal(g0.view(np.uint32), g1.view(np.uint32))
+        np.testing.assert_array_equal(r0.view(np.uint32), r1.view(np.uint32))
     assert s0[1] == 2047 and r0[2047] == 0.0
     # random init: logits are small, so the CE is close to ln(V)
     assert abs(s0[0] - np.log(8192)) < 0.05

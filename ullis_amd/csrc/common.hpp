@@ -131,16 +131,54 @@ __device__ __forceinline__ int mfma32_row(int r, int lane) {
 }
 
 // ------------------------------------------------------------ launching
-// Kernel-timestamp probe: when armed on the launching thread, the next
-// launch() records its kernel's start and end into these events
-// (hipExtLaunchKernelGGL), i.e. the execution time of the dispatch itself,
-// without the latency of separate event packets around it. launch() disarms
-// the probe when it consumes it.
+// Launch probe, armed on the launching thread for the next launch:
+//  - kernels that take a stamps slot (the streamed-LDS GEMMs) get `stamps`
+//    as an argument: every block records the device wall clock
+//    (s_memrealtime) at its start (atomic min into stamps[0]) and end
+//    (atomic max into stamps[1]), i.e. the launch's execution interval, which
+//    waiting for CUs held by another stream's kernels does not inflate; the
+//    launcher sets used_stamps;
+//  - any other launch() records its kernel into the events
+//    (hipExtLaunchKernelGGL).
+// The launcher that consumes the probe disarms it.
 struct LaunchProbe {
   hipEvent_t start = nullptr;
   hipEvent_t stop = nullptr;
+  unsigned long long* stamps = nullptr;  // [stamp_cap][2]: per block (start, end)
+  long stamp_cap = 0;                    // blocks the stamps slot holds
+  long blocks = 0;                       // blocks of the launch that took the slot
+  bool used_stamps = false;
 };
 inline thread_local LaunchProbe* t_launch_probe = nullptr;
+
+// The stamps slot for the next launch, of `blocks` workgroups, of a kernel
+// that records them (the probe is consumed), or null: no probe, or a grid
+// larger than the slot (the launch is then timed by the probe's events).
+inline unsigned long long* take_probe_stamps(long blocks) {
+  LaunchProbe* p = t_launch_probe;
+  if (!p || !p->stamps || blocks > p->stamp_cap) return nullptr;
+  t_launch_probe = nullptr;
+  p->used_stamps = true;
+  p->blocks = blocks;
+  return p->stamps;
+}
+
+// Each block writes its own (start, end) pair of the device wall clock, so
+// stamping adds no contended atomics; the kernel's interval is the earliest
+// start to the latest end.
+__device__ __forceinline__ long stamp_slot() {
+  return blockIdx.x + (long)gridDim.x * (blockIdx.y + (long)gridDim.y * blockIdx.z);
+}
+__device__ __forceinline__ void stamp_block_start(unsigned long long* stamps) {
+  if (stamps && threadIdx.x == 0) stamps[2 * stamp_slot()] = __builtin_amdgcn_s_memrealtime();
+}
+// Call from every thread after the block's last store.
+__device__ __forceinline__ void stamp_block_end(unsigned long long* stamps) {
+  if (stamps) {
+    __syncthreads();
+    if (threadIdx.x == 0) stamps[2 * stamp_slot() + 1] = __builtin_amdgcn_s_memrealtime();
+  }
+}
 
 template <typename... KArgs, typename... Args>
 inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds_bytes,

@@ -474,9 +474,12 @@ __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const
 
 template <int BM, int BN, int BK, int NS, class OA, class OB, class Epi>
 __global__ __launch_bounds__(256) void gemm_lds_kernel(OA a, OB b, Epi epi, int M, int N, int K,
-                                                       int k_split, TileMap map) {
+                                                       int k_split, TileMap map,
+                                                       unsigned long long* stamps) {
   __shared__ __attribute__((aligned(1024))) char smem[lds_smem_bytes<BM, BN, BK, NS, OA, OB>()];
+  stamp_block_start(stamps);
   gemm_lds_body<BM, BN, BK, NS>(smem, blockIdx.x, blockIdx.z, a, b, epi, M, N, K, k_split, map);
+  stamp_block_end(stamps);
 }
 
 template <class T, int G>
@@ -488,11 +491,14 @@ struct Group {
 template <int BM, int BN, int BK, int NS, class OA, class OB, class Epi, int G>
 __global__ __launch_bounds__(256) void gemm_lds_group_kernel(Group<OA, G> a, Group<OB, G> b,
                                                              Group<Epi, G> epi, int M, int N,
-                                                             int K, int k_split, TileMap map) {
+                                                             int K, int k_split, TileMap map,
+                                                             unsigned long long* stamps) {
   __shared__ __attribute__((aligned(1024))) char smem[lds_smem_bytes<BM, BN, BK, NS, OA, OB>()];
   const int g = blockIdx.y;
+  stamp_block_start(stamps);
   gemm_lds_body<BM, BN, BK, NS>(smem, blockIdx.x, blockIdx.z, a.v[g], b.v[g], epi.v[g], M, N, K,
                                 k_split, map);
+  stamp_block_end(stamps);
 }
 
 // One GEMM of a pair launch: tile config T, operands, epilogue and shape;
@@ -533,11 +539,12 @@ __device__ __forceinline__ void run_lds_problem(char* smem, const LdsProblem<T, 
 // epilogues) in one launch: the first ps[0].blocks blocks run ps[0], the next
 // ps[1].blocks run ps[1], ..., so the blocks of all of them share the CUs.
 template <class... Ps>
-__global__ __launch_bounds__(256) void gemm_lds_multi_kernel(Ps... ps) {
+__global__ __launch_bounds__(256) void gemm_lds_multi_kernel(unsigned long long* stamps, Ps... ps) {
   constexpr int S = max_of(LdsProblemSmem<Ps>::value...);
   __shared__ __attribute__((aligned(1024))) char smem[S];
   int bid = blockIdx.x;
   bool done = false;
+  stamp_block_start(stamps);
   auto one = [&](const auto& p) {
     if (done) return;
     if (bid < p.blocks) {
@@ -548,6 +555,7 @@ __global__ __launch_bounds__(256) void gemm_lds_multi_kernel(Ps... ps) {
     }
   };
   (one(ps), ...);
+  stamp_block_end(stamps);
 }
 
 // ------------------------------------------------------------ host dispatch
@@ -615,9 +623,10 @@ hipError_t launch_lds_group(hipStream_t s, const Group<OA, G>& a, const Group<OB
   if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return hipErrorInvalidValue;
   const long tiles = cdiv(M, T::bm) * cdiv(N, T::bn);
   const int ks = (int)(cdiv(K, T::bk) * T::bk);
+  unsigned long long* stamps = take_probe_stamps(tiles * G);
   launch((gemm_lds_group_kernel<T::bm, T::bn, T::bk, T::ns, OA, OB, Epi, G>),
          dim3((unsigned)tiles, G, 1), dim3(kThreads), 0, s, a, b, epi, (int)M, (int)N, (int)K, ks,
-         tile_map_for<T, OA, OB>(M, N));
+         tile_map_for<T, OA, OB>(M, N), stamps);
   return hipGetLastError();
 }
 
@@ -628,9 +637,10 @@ hipError_t launch_lds(hipStream_t s, const OA& a, const OB& b, const Epi& epi, l
   if (splits < 1) splits = 1;
   const long tiles = cdiv(M, T::bm) * cdiv(N, T::bn);
   const int ks = (int)(cdiv(cdiv(K, splits), T::bk) * T::bk);
+  unsigned long long* stamps = take_probe_stamps(tiles * splits);
   launch((gemm_lds_kernel<T::bm, T::bn, T::bk, T::ns, OA, OB, Epi>),
          dim3((unsigned)tiles, 1, splits), dim3(kThreads), 0, s, a, b, epi, (int)M, (int)N, (int)K,
-         ks, tile_map_for<T, OA, OB>(M, N));
+         ks, tile_map_for<T, OA, OB>(M, N), stamps);
   return hipGetLastError();
 }
 
@@ -646,17 +656,19 @@ LdsProblem<T, OA, OB, Epi> lds_problem(const OA& a, const OB& b, const Epi& epi,
 
 template <class T, class OA, class OB, class Epi>
 hipError_t launch_lds_problem(hipStream_t s, const LdsProblem<T, OA, OB, Epi>& p) {
+  unsigned long long* stamps = take_probe_stamps(p.blocks);
   launch((gemm_lds_kernel<T::bm, T::bn, T::bk, T::ns, OA, OB, Epi>),
          dim3((unsigned)p.tiles, 1, (unsigned)(p.blocks / p.tiles)), dim3(kThreads), 0, s, p.a, p.b,
-         p.epi, p.M, p.N, p.K, p.k_split, p.map);
+         p.epi, p.M, p.N, p.K, p.k_split, p.map, stamps);
   return hipGetLastError();
 }
 
 // Shapes must fit int32 (lds_problem's callers check M, N, K).
 template <class... Ps>
 hipError_t launch_lds_multi(hipStream_t s, const Ps&... ps) {
+  unsigned long long* stamps = take_probe_stamps(0L + (0L + ... + ps.blocks));
   launch((gemm_lds_multi_kernel<Ps...>), dim3((unsigned)(0 + ... + ps.blocks)), dim3(kThreads), 0,
-         s, ps...);
+         s, stamps, ps...);
   return hipGetLastError();
 }
 

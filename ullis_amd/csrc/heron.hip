@@ -139,6 +139,9 @@ struct ullis_hip_heron {
   int probe = 0;
   int probe_used = 0;
   std::vector<hipEvent_t> probe_events;
+  unsigned long long* probe_stamps = nullptr;  // device [kProbeMax][kStampCap][2], lazily
+  std::vector<long> probe_blocks;              // per probed launch: stamped blocks, 0 = events
+  double wall_khz = 0.0;                       // device wall-clock rate (s_memrealtime)
 
   template <class T>
   T* tensor(const std::string& name) {
@@ -182,10 +185,17 @@ bool bind_packed(ullis_hip_heron* h, const std::string& p, long out, long in, bo
   } while (0)
 
 constexpr int kProbeMax = 512;
+constexpr long kStampCap = 8192;  // blocks per stamped launch (larger grids use events)
+
+__global__ void probe_stamps_clear_kernel(unsigned long long* st, long n) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) st[i] = 0ull;
+}
 
 // When `id` is the probed launch class, the kernel that `expr` launches
-// records its own start and end timestamps into the next event pair
-// (LaunchProbe). `expr` must launch exactly one kernel.
+// records its execution interval (LaunchProbe: device wall-clock stamps for
+// the streamed-LDS GEMMs, kernel-timestamp events for other kernels). `expr`
+// must launch exactly one kernel.
 #define PROBED(id, expr, what)                                                     \
   do {                                                                             \
     const bool on_ = h->probe == (id) && h->probe_used < kProbeMax;                \
@@ -193,6 +203,8 @@ constexpr int kProbeMax = 512;
     if (on_) {                                                                     \
       lp_.start = h->probe_events[2 * h->probe_used];                              \
       lp_.stop = h->probe_events[2 * h->probe_used + 1];                           \
+      lp_.stamps = h->probe_stamps + 2 * kStampCap * h->probe_used;                \
+      lp_.stamp_cap = kStampCap;                                                   \
       t_launch_probe = &lp_;                                                       \
     }                                                                              \
     const int rc_ = c->hip((expr), (what));                                        \
@@ -201,6 +213,7 @@ constexpr int kProbeMax = 512;
     if (rc_) return rc_;                                                           \
     if (on_) {                                                                     \
       if (!consumed_) return c->fail(ULLIS_HIP_ERR_RUNTIME, "probe: no kernel launched"); \
+      h->probe_blocks[h->probe_used] = lp_.used_stamps ? lp_.blocks : 0;           \
       ++h->probe_used;                                                             \
     }                                                                              \
   } while (0)
@@ -213,6 +226,7 @@ constexpr int kProbeMax = 512;
     STEP(expr, what);                                                              \
     if (on_) {                                                                     \
       STEP(hipEventRecord(h->probe_events[2 * h->probe_used + 1], s), "probe");    \
+      h->probe_blocks[h->probe_used] = 0;                                          \
       ++h->probe_used;                                                             \
     }                                                                              \
   } while (0)
@@ -548,6 +562,17 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
       return c->fail(ULLIS_HIP_ERR_RUNTIME, "heron stream / event creation failed");
     }
   }
+  h->probe_blocks.assign(kProbeMax, 0);
+  {
+    int dev = 0, khz = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess ||
+        khz <= 0) {
+      ullis_hip_heron_destroy(h);
+      return c->fail(ULLIS_HIP_ERR_RUNTIME, "device wall-clock rate unavailable");
+    }
+    h->wall_khz = (double)khz;
+  }
   h->probe_events.resize(2 * kProbeMax);
   for (auto& e : h->probe_events) {
     if (hipEventCreate(&e) != hipSuccess) {
@@ -578,6 +603,7 @@ void ullis_hip_heron_destroy(ullis_hip_heron* h) {
   if (h->arena) (void)hipFree(h->arena);
   if (h->act) (void)hipFree(h->act);
   if (h->job_mem) (void)hipFree(h->job_mem);
+  if (h->probe_stamps) (void)hipFree(h->probe_stamps);
   delete h;
 }
 
@@ -592,14 +618,41 @@ int ullis_hip_heron_probe(ullis_hip_heron* h, int probe_id) {
   if (!h || probe_id < 0 || probe_id >= ULLIS_HIP_PROBE_COUNT) return ULLIS_HIP_ERR_INVALID;
   h->probe = probe_id;
   h->probe_used = 0;
+  if (probe_id != ULLIS_HIP_PROBE_NONE) {
+    ullis_hip_ctx* c = h->ctx;
+    const long n = 2 * kStampCap * kProbeMax;
+    if (!h->probe_stamps)
+      STEP(hipMalloc(&h->probe_stamps, sizeof(unsigned long long) * n), "probe stamps alloc");
+    launch(probe_stamps_clear_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, c->stream,
+           h->probe_stamps, n);
+    STEP(hipGetLastError(), "probe stamps clear");
+  }
   return 0;
 }
 
 int ullis_hip_heron_probe_read(ullis_hip_heron* h, float* total_ms, int* launches) {
   if (!h || !total_ms || !launches) return ULLIS_HIP_ERR_INVALID;
   ullis_hip_ctx* c = h->ctx;
+  STEP(hipStreamSynchronize(c->stream), "probe sync");
+  STEP(hipStreamSynchronize(h->side), "probe sync");
+  std::vector<unsigned long long> st;
   double sum = 0.0;
   for (int i = 0; i < h->probe_used; ++i) {
+    if (const long nb = h->probe_blocks[i]) {
+      st.resize(2 * (size_t)nb);
+      STEP(hipMemcpy(st.data(), h->probe_stamps + 2 * kStampCap * i,
+                     sizeof(unsigned long long) * st.size(), hipMemcpyDeviceToHost),
+           "probe stamps");
+      unsigned long long t0 = ~0ull, t1 = 0;
+      for (long b = 0; b < nb; ++b) {
+        if (st[2 * b] == 0 || st[2 * b + 1] < st[2 * b])
+          return c->fail(ULLIS_HIP_ERR_RUNTIME, "probe stamps unset");
+        t0 = std::min(t0, st[2 * b]);
+        t1 = std::max(t1, st[2 * b + 1]);
+      }
+      sum += (double)(t1 - t0) / h->wall_khz;
+      continue;
+    }
     float ms = 0.0f;
     STEP(hipEventSynchronize(h->probe_events[2 * i + 1]), "probe sync");
     STEP(hipEventElapsedTime(&ms, h->probe_events[2 * i], h->probe_events[2 * i + 1]),
