@@ -140,6 +140,84 @@ int ullis_hip_packed_head_train_sgd(ullis_hip_ctx* ctx, const uint16_t* hidden16
                                     float ste_scale, float* row_loss, float* stats4,
                                     float* g_hidden, float* g_scale, float* g_bias, float* g_w);
 
+/* ---- block-level methods of the Metal train step ----
+ * The reference moves train tapes as MetalBuffers from a block's forward to
+ * its backward (src/model.rs:1242-1256, 1525-1535); here the caller owns the
+ * tape: a device buffer of *_tape_bytes() bytes, 256-byte aligned, filled by
+ * the forward and read by the backward of the same block. GEMM operands
+ * (block inputs, tapes) are fp16; an fp32 x is rounded to fp16 first. The
+ * parameter updates the reference runs on the GPU inside these methods run
+ * here too, in place (latent, residual, bits, and bits_t when non-NULL;
+ * NULL bits_t is rebuilt in scratch for the input gradient); the small
+ * vectors the reference steps on the host (key / O scale, O bias, e, the mix
+ * vectors) are returned as gradients, for ullis_hip_clipped_sgd_fp16. */
+size_t ullis_hip_cmix_tape_bytes(size_t rows, size_t d_model, size_t dim_ffn);
+size_t ullis_hip_rosa_tape_bytes(size_t rows, size_t channels);
+
+/* MetalRuntime::cmix_block_forward, src/metal.rs:1891 (CMix forward_tape,
+ * src/model.rs:1018-1078): s = x + (x[t-1] - x) * mix, k = key(s) (packed,
+ * no bias), r = max(k, 0)^2, out = r . value_weight^T (value_weight f16
+ * [d_model, dim_ffn]). x [batch*time, d_model] of x_dtype; out fp32, the
+ * block's contribution without the residual. */
+int ullis_hip_cmix_block_forward(ullis_hip_ctx* ctx, const void* x, int x_dtype,
+                                 const uint16_t* mix, const uint32_t* key_bits,
+                                 const uint16_t* key_scale, const uint16_t* value_weight,
+                                 size_t batch, size_t time, size_t d_model, size_t dim_ffn,
+                                 float* out, void* tape);
+
+/* MetalRuntime::cmix_block_backward_sgd, src/metal.rs:2165 (driven by CMix
+ * backward_update, src/model.rs:1080-1143): from gy (fp32 [batch*time,
+ * d_model], gradient of out) on the pre-update weights: g_x (overwritten),
+ * g_mix [d_model], g_key_scale [dim_ffn]; then the value weight clipped SGD
+ * and the key BinaryConnect step (gradient x ste_scale) with the repack. */
+int ullis_hip_cmix_block_backward_sgd(ullis_hip_ctx* ctx, const void* tape, const float* gy,
+                                      const uint16_t* mix, uint32_t* key_bits,
+                                      uint32_t* key_bits_t, const uint16_t* key_scale,
+                                      uint16_t* key_latent, float* key_residual,
+                                      uint16_t* value_weight, float* value_residual,
+                                      size_t batch, size_t time, size_t d_model, size_t dim_ffn,
+                                      float learning_rate, float ste_scale, float* g_x,
+                                      float* g_mix, float* g_key_scale);
+
+/* MetalRuntime::rosa_block_forward, src/metal.rs:1334-1484, up to the
+ * suffix automaton: q/k/v inputs x + (x[t-1] - x) * mix_{q,k,v}, the three
+ * packed projections with bias, and their sign bit-planes (bit
+ * row*channels + c = projection > 0, LSB-first u32, ceil(batch*time*
+ * channels / 32) words each) for rosa_qkv_batch_packed_channel_major
+ * (src/rosa.rs:486-513), which stays with the caller. */
+int ullis_hip_rosa_qkv_forward(ullis_hip_ctx* ctx, const void* x, int x_dtype,
+                               const uint16_t* mix_q, const uint16_t* mix_k,
+                               const uint16_t* mix_v, const uint32_t* q_bits,
+                               const uint16_t* q_scale, const uint16_t* q_bias,
+                               const uint32_t* k_bits, const uint16_t* k_scale,
+                               const uint16_t* k_bias, const uint32_t* v_bits,
+                               const uint16_t* v_scale, const uint16_t* v_bias, size_t batch,
+                               size_t time, size_t channels, uint32_t* q_plane,
+                               uint32_t* k_plane, uint32_t* v_plane);
+
+/* The rest of MetalRuntime::rosa_block_forward (src/metal.rs:1485-1511):
+ * y = (2 idx - 1) * e (rosa_qkv_out_batched_channel_major, src/rosa.rs:
+ * 614-639) from the automaton's output idx (u8, channel-major [batch]
+ * [channels][time]), out = O(y) with bias, fp32 [batch*time, channels].
+ * The tape keeps y (fp16) and idx (row-major). */
+int ullis_hip_rosa_out_forward(ullis_hip_ctx* ctx, const uint8_t* idx, const uint16_t* e,
+                               const uint32_t* o_bits, const uint16_t* o_scale,
+                               const uint16_t* o_bias, size_t batch, size_t time,
+                               size_t channels, float* out, void* tape);
+
+/* MetalRuntime::rosa_o_stop_grad_sgd, src/metal.rs:2409 (RwkvRosaQkv1Bit::
+ * backward_stop_grad, src/model.rs:1442-1490): from gy (fp32 [rows,
+ * channels], gradient of out): g_e[c] = sum_r g_y[r,c] (2 idx - 1) with g_y
+ * the O input gradient (never stored), g_scale, g_bias [channels]; then the
+ * O BinaryConnect step (gradient x ste_scale) with the repack. The
+ * reference's y / out / bias arguments are the tape here (its scale
+ * gradient from outputs is sum_i sign * G, the same quantity). */
+int ullis_hip_rosa_o_stop_grad_sgd(ullis_hip_ctx* ctx, const void* tape, const float* gy,
+                                   uint32_t* o_bits, uint32_t* o_bits_t, const uint16_t* o_scale,
+                                   uint16_t* o_latent, float* o_residual, size_t rows,
+                                   size_t channels, float learning_rate, float ste_scale,
+                                   float* g_e, float* g_scale, float* g_bias);
+
 /* ---- one Heron train step on the device (UllisHeron::train_step_on,
  *      src/model.rs:2827-3025, metal branch; rosa_grad = stop_grad_bits) ---- */
 
@@ -171,12 +249,13 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
 /*
  * Kernel probe, the device-side counterpart of the reference's per-phase
  * TrainStepProfile (src/model.rs:101-124): while a probe id is set, every
- * launch of that class inside ullis_hip_heron_step records the start and end
- * timestamps of its kernel into HIP events (hipExtLaunchKernel), so the time
- * is the kernel's own execution time; HEAD_CE, which is several kernels, is
- * instead bracketed by event records on the step's stream. At most 512
- * launches are recorded. probe_read waits for the recorded events and returns
- * the summed time and the number of launches, then restarts the count.
+ * launch of that class inside ullis_hip_heron_step records its execution
+ * interval: a streamed-LDS GEMM launch has each workgroup write its start and
+ * end on the device wall clock (earliest start to latest end), other kernels
+ * use kernel-timestamp events (hipExtLaunchKernel); HEAD_CE, which is several
+ * kernels, is bracketed by event records on the step's stream. At most 512
+ * launches are recorded. probe_read waits for the step and returns the summed
+ * time and the number of launches, then restarts the count.
  */
 #define ULLIS_HIP_PROBE_NONE 0
 #define ULLIS_HIP_PROBE_KEY_FORWARD 1       /* CMix key packed GEMM + ReLU^2, per layer */

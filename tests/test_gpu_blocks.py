@@ -1,0 +1,261 @@
+"""GPU parity of the block-level methods (ullis_hip_cmix_block_*,
+ullis_hip_rosa_*), through HipRuntime's MetalRuntime-shaped mirror, against
+the oracle's CPU composition of the same block (the non-Metal branches of
+src/model.rs:1018-1177 and 1354-1523), and of the block-by-block Heron step
+(HeronBlockStep) against the fused device step (ullis_hip_heron_step),
+which it must match bit for bit.
+
+Bounds: a block chains GEMMs through fp16 operands where the oracle keeps
+fp32 (the mixed input, ReLU^2, the scaled gradient), so composed outputs and
+gradients are compared as max|gpu - ref| / max|ref| <= BLOCK_REL (two fp16
+roundings of ~2^-11 each, with margin); updates are compared as the change of
+the effective parameter (f16 value + fp32 carry), which is -lr * clip(g);
+sign bits as mismatch fractions (an output or latent within rounding of zero
+may land on either side).
+"""
+import numpy as np
+import pytest
+
+from oracle import cpu_ref as o
+from ullis_amd.heron_blocks import HeronBlockStep
+from ullis_amd.runtime import HeronShape, HeronTrainer
+from ullis_amd.synth import f16, heron_arena, pack_bits, step_inputs, tensor_view, unpack_bits
+
+pytestmark = pytest.mark.gpu
+
+NO_IGNORE = 0xFFFFFFFF
+BLOCK_REL = 2e-3
+UPDATE_REL = 5e-3
+BITS_FRAC = 2e-3
+
+
+def h2f(bits):
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float32)
+
+
+def rel(a, r):
+    a = np.asarray(a, np.float64)
+    r = np.asarray(r, np.float64)
+    assert a.shape == r.shape and np.isfinite(a).all()
+    return float(np.max(np.abs(a - r))) / max(float(np.max(np.abs(r))), 1e-30)
+
+
+def bit_frac(a, b, n):
+    return float(np.mean(unpack_bits(a, n) != unpack_bits(b, n)))
+
+
+def effective(values16, residual):
+    return h2f(values16).astype(np.float64) + np.asarray(residual, np.float64)
+
+
+def cm_to_rm(idx_cm, batch, time, ch):
+    return np.ascontiguousarray(
+        np.asarray(idx_cm, np.uint8).reshape(batch, ch, time).transpose(0, 2, 1)).reshape(-1)
+
+
+def mixed(x, mix16, batch, time, ch):
+    xx = o.time_shift_delta(x, batch, time, ch)
+    return (x.reshape(-1, ch) + xx.reshape(-1, ch) * h2f(mix16)[None, :]).reshape(-1)
+
+
+def cmix_case(rng, batch, time, d, f):
+    rows = batch * time
+    return dict(
+        x16=f16(rng.standard_normal(rows * d)),
+        mix=f16(rng.uniform(0.0, 1.0, d)),
+        key_latent=f16(rng.uniform(-0.01, 0.01, f * d)),
+        key_residual=rng.uniform(-1e-4, 1e-4, f * d).astype(np.float32),
+        key_scale=f16(rng.uniform(0.02, 0.06, f)),
+        value=f16(rng.normal(0, 0.05, d * f)),
+        value_residual=rng.uniform(-1e-4, 1e-4, d * f).astype(np.float32),
+        gy=(rng.standard_normal(rows * d) * 1e-3).astype(np.float32),
+    )
+
+
+@pytest.mark.parametrize("batch,time,d,f", [(1, 64, 64, 128), (2, 32, 64, 192), (1, 256, 128, 512)])
+def test_cmix_block_forward_backward_match_oracle(rt, batch, time, d, f):
+    rng = np.random.default_rng(11 + d + f)
+    c = cmix_case(rng, batch, time, d, f)
+    rows = batch * time
+    key_bits = o.pack_latent_bits(c["key_latent"])
+    fwd = rt.cmix_block_forward(c["x16"], c["mix"], key_bits, c["key_scale"], c["value"], batch,
+                                time, d, f)
+    # oracle: CMix forward_tape CPU branch (src/model.rs:1051-1061)
+    x = h2f(c["x16"])
+    shifted = mixed(x, c["mix"], batch, time, d)
+    key = o.packed_forward(shifted, rows, d, f, key_bits, c["key_scale"])
+    relu2 = np.maximum(key, 0.0) ** 2
+    out = o.fp16_forward(relu2, rows, f, d, c["value"])
+    assert rel(fwd["out"], out) <= BLOCK_REL
+
+    lr, ste = 0.01, float(time - 1)
+    bwd = rt.cmix_block_backward_sgd(fwd["gpu_tape"], c["gy"], c["mix"], key_bits, c["key_scale"],
+                                     c["key_latent"], c["key_residual"], c["value"],
+                                     c["value_residual"], batch, time, d, f, lr, ste)
+    # oracle: CMix backward_update CPU branch (src/model.rs:1145-1177)
+    g_relu2, g_value = o.fp16_backward(relu2, c["gy"], rows, f, d, c["value"])
+    v_new, v_res = o.clipped_sgd(c["value"], c["value_residual"], g_value, lr)
+    g_key = g_relu2 * 2.0 * np.maximum(key, 0.0)
+    pb = o.packed_backward_ste(shifted, g_key, rows, d, f, key_bits, c["key_scale"], want_gb=False)
+    lat, lat_res, _, _, _, _, bits_new = o.packed_apply_sgd(
+        d, f, c["key_latent"], c["key_residual"], c["key_scale"], np.zeros(f, np.float32), None,
+        None, pb["weight_gradient"], pb["scale_gradient"], None, lr, ste)
+    g_x, g_mix = o.lerp_shift_backward(o.time_shift_delta(x, batch, time, d), c["mix"],
+                                       pb["input_gradient"], batch, time, d)
+    assert rel(bwd["g_x"], g_x) <= BLOCK_REL
+    assert rel(bwd["g_mix"], g_mix) <= BLOCK_REL
+    assert rel(bwd["g_key_scale"], pb["scale_gradient"]) <= BLOCK_REL
+    v0 = effective(c["value"], c["value_residual"])
+    assert rel(effective(bwd["next_value_weight"], bwd["next_value_residual"]) - v0,
+               effective(v_new, v_res) - v0) <= UPDATE_REL
+    k0 = effective(c["key_latent"], c["key_residual"])
+    assert rel(effective(bwd["next_key_latent"], bwd["next_key_residual"]) - k0,
+               effective(lat, lat_res) - k0) <= UPDATE_REL
+    # bits are the repack of the updated latent; bits_t their transpose
+    np.testing.assert_array_equal(bwd["next_key_bits"], o.pack_latent_bits(bwd["next_key_latent"]))
+    np.testing.assert_array_equal(bwd["next_key_bits_t"],
+                                  o.transpose_bits(bwd["next_key_bits"], f, d))
+    assert bit_frac(bwd["next_key_bits"], bits_new, f * d) <= BITS_FRAC
+
+
+def rosa_case(rng, batch, time, d):
+    rows = batch * time
+
+    def proj():
+        return dict(bits=pack_bits(rng.uniform(-1, 1, d * d) >= 0),
+                    scale=f16(rng.uniform(0.02, 0.06, d)), bias=f16(rng.normal(0, 0.01, d)))
+    return dict(
+        x16=f16(rng.standard_normal(rows * d)),
+        mix=[f16(rng.uniform(0.0, 1.0, d)) for _ in range(3)],
+        q=proj(), k=proj(), v=proj(), o=proj(),
+        e=f16(rng.normal(0, 0.5, d)),
+        idx=rng.integers(0, 2, rows * d, dtype=np.uint8),  # channel-major [B][D][T]
+        latent=f16(rng.uniform(-0.01, 0.01, d * d)),
+        residual=rng.uniform(-1e-4, 1e-4, d * d).astype(np.float32),
+        gy=(rng.standard_normal(rows * d) * 1e-3).astype(np.float32),
+    )
+
+
+@pytest.mark.parametrize("batch,time,d", [(1, 64, 64), (2, 64, 96), (1, 128, 128)])
+def test_rosa_block_forward_and_o_stop_grad_match_oracle(rt, batch, time, d):
+    rng = np.random.default_rng(5 + d + time)
+    c = rosa_case(rng, batch, time, d)
+    rows = batch * time
+    seen = []
+
+    def sam(qp, kp, vp):  # the suffix automaton's seat: hand back the fixed idx
+        seen.append((qp, kp, vp))
+        return c["idx"]
+
+    q, k, v, op = c["q"], c["k"], c["v"], c["o"]
+    fwd = rt.rosa_block_forward(c["x16"], *c["mix"], q["bits"], q["scale"], q["bias"], k["bits"],
+                                k["scale"], k["bias"], v["bits"], v["scale"], v["bias"], c["e"],
+                                op["bits"], op["scale"], op["bias"], batch, time, d, sam)
+    assert len(seen) == 1
+    # oracle: forward_tape CPU branch (src/model.rs:1412-1425) up to the planes
+    x = h2f(c["x16"])
+    words = (rows * d + 31) // 32
+    for j, (p, m) in enumerate(zip((q, k, v), c["mix"])):
+        y = o.packed_forward(mixed(x, m, batch, time, d), rows, d, d, p["bits"], p["scale"],
+                             p["bias"])
+        want = o.sign_pack_bits(y)
+        assert fwd["planes"][j].shape == (words,)
+        assert bit_frac(fwd["planes"][j], want, rows * d) <= BITS_FRAC, j
+    idx_rm = cm_to_rm(c["idx"], batch, time, d)
+    yv = o.rosa_y_from_idx(idx_rm, c["e"], rows, d)
+    out = o.packed_forward(yv, rows, d, d, op["bits"], op["scale"], op["bias"])
+    assert rel(fwd["out"], out) <= 1e-4  # y = +-e is exact in fp16
+
+    lr, ste = 0.01, float(time - 1)
+    bwd = rt.rosa_o_stop_grad_sgd(fwd["gpu_tape"], c["gy"], op["bits"], op["scale"], c["latent"],
+                                  c["residual"], rows, d, lr, ste)
+    # oracle: backward_stop_grad CPU branch (src/model.rs:1491-1522)
+    pb = o.packed_backward_ste(yv, c["gy"], rows, d, d, op["bits"], op["scale"])
+    g_e = o.rosa_e_grad(pb["input_gradient"], idx_rm, rows, d)
+    lat, lat_res, _, _, _, _, bits_new = o.packed_apply_sgd(
+        d, d, c["latent"], c["residual"], op["scale"], np.zeros(d, np.float32), None, None,
+        pb["weight_gradient"], pb["scale_gradient"], None, lr, ste)
+    assert rel(bwd["e_gradient"], g_e) <= BLOCK_REL
+    assert rel(bwd["scale_gradient"], pb["scale_gradient"]) <= BLOCK_REL
+    assert rel(bwd["bias_gradient"], pb["bias_gradient"]) <= 1e-5  # fp32 column sums
+    l0 = effective(c["latent"], c["residual"])
+    assert rel(effective(bwd["next_latent"], bwd["next_residual"]) - l0,
+               effective(lat, lat_res) - l0) <= UPDATE_REL
+    np.testing.assert_array_equal(bwd["next_bits"], o.pack_latent_bits(bwd["next_latent"]))
+    np.testing.assert_array_equal(bwd["next_bits_t"], o.transpose_bits(bwd["next_bits"], d, d))
+    assert bit_frac(bwd["next_bits"], bits_new, d * d) <= BITS_FRAC
+
+
+def test_block_methods_reject_bad_arguments(rt):
+    lib = rt.lib
+    d, f, b, t = 64, 128, 1, 64
+    tape = rt.buffer(lib.ullis_hip_cmix_tape_bytes(b * t, d, f) + 256)
+    x = rt.buffer(4 * b * t * d)
+    small = rt.buffer(4096)
+    args = [small.ptr] * 4
+    # zero-sized shape, NULL tape, misaligned tape
+    assert lib.ullis_hip_cmix_block_forward(rt.ctx, x.ptr, 2, *args, 0, t, d, f, x.ptr,
+                                            tape.ptr) == -1
+    assert lib.ullis_hip_cmix_block_forward(rt.ctx, x.ptr, 2, *args, b, t, d, f, x.ptr,
+                                            None) == -1
+    assert lib.ullis_hip_cmix_block_forward(rt.ctx, x.ptr, 2, *args, b, t, d, f, x.ptr,
+                                            tape.ptr + 16) == -1
+    assert b"aligned" in lib.ullis_hip_last_error(rt.ctx)
+    assert lib.ullis_hip_cmix_block_forward(rt.ctx, x.ptr, 7, *args, b, t, d, f, x.ptr,
+                                            tape.ptr) == -1
+    assert lib.ullis_hip_rosa_o_stop_grad_sgd(rt.ctx, tape.ptr, x.ptr, small.ptr, None, small.ptr,
+                                              small.ptr, small.ptr, t, d, -1.0, 1.0, small.ptr,
+                                              small.ptr, small.ptr) == -1
+    assert lib.ullis_hip_cmix_tape_bytes(0, d, f) == 0
+    assert lib.ullis_hip_rosa_tape_bytes(t, 0) == 0
+
+
+@pytest.mark.parametrize("d,layers,f,vocab,time",
+                         [(64, 2, 128, 256, 64), (128, 3, 256, 512, 128),
+                          (512, 2, 2048, 8192, 2048)])
+def test_block_step_matches_fused_step(rt, d, layers, f, vocab, time):
+    """HeronBlockStep (block methods, host residual adds, the automaton
+    handed the Q/K/V planes between the projections and O) against the fused
+    step on the same arena and inputs: bit-identical, since both run the same
+    kernels with the same reductions and the same update arithmetic (the
+    last case has config 4's widths at two layers)."""
+    shape = HeronShape(d_model=d, n_layers=layers, dim_ffn=f, vocab=vocab, batch=1, time=time)
+    fused = HeronTrainer(rt, shape)
+    blocks = HeronBlockStep(rt, shape)
+    arena = heron_arena(fused.layout, fused.arena_bytes, shape.dims(), seed=3, random_ln=True)
+    x, labels, idx = step_inputs(shape.rows, d, vocab, layers, 1, time, seed=3)
+    nd = shape.rows * d
+    words = (nd + 31) // 32
+
+    fused.upload_arena(arena)
+    dx, dl, di = rt.put(x), rt.put(labels), rt.put(idx)
+    g = rt.zeros(np.float32, nd)
+    rl = rt.zeros(np.float32, shape.rows)
+    st = rt.zeros(np.float32, 4)
+    qkv = rt.zeros(np.uint32, layers * 3 * words)
+    fused.step(dx, dl, NO_IGNORE, 0.01, di, g, rl, st, qkv)
+    rt.sync()
+    fa, fg, frl = fused.download_arena(), g.download(np.float32), rl.download(np.float32)
+    fst, fq = st.download(np.float32), qkv.download(np.uint32).reshape(layers, 3, words)
+
+    blocks.upload_arena(arena)
+    handed = []
+
+    def sam(layer, qp, kp, vp):
+        handed.append(layer)
+        return idx[layer * nd:(layer + 1) * nd]
+
+    out = blocks.step(x, labels, NO_IGNORE, 0.01, sam)
+    ba = blocks.download_arena()
+    assert handed == list(range(layers))
+    for l in range(layers):
+        for j in range(3):
+            np.testing.assert_array_equal(out["qkv_planes"][l][j], fq[l, j], err_msg=f"{l}/{j}")
+    np.testing.assert_array_equal(out["stats"][:3], fst[:3])
+    np.testing.assert_array_equal(out["row_loss"].view(np.uint32), frl.view(np.uint32))
+    np.testing.assert_array_equal(out["g_emb"].view(np.uint32), fg.view(np.uint32))
+    for name, _dt, _count, _off, _derived in fused.layout:
+        np.testing.assert_array_equal(tensor_view(ba, fused.layout, name),
+                                      tensor_view(fa, fused.layout, name), err_msg=name)
+    blocks.close()
+    fused.close()

@@ -72,6 +72,17 @@ SIGNATURES = {
         i32,
         [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, u32, f32, f32,
          vp, vp, vp, vp, vp, vp]),
+    "ullis_hip_cmix_tape_bytes": (sz, [sz, sz, sz]),
+    "ullis_hip_rosa_tape_bytes": (sz, [sz, sz]),
+    "ullis_hip_cmix_block_forward": (i32, [vp, vp, i32, vp, vp, vp, vp, sz, sz, sz, sz, vp, vp]),
+    "ullis_hip_cmix_block_backward_sgd": (
+        i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, f32, f32, vp, vp, vp]),
+    "ullis_hip_rosa_qkv_forward": (
+        i32, [vp, vp, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, vp, vp,
+              vp]),
+    "ullis_hip_rosa_out_forward": (i32, [vp, vp, vp, vp, vp, vp, sz, sz, sz, vp, vp]),
+    "ullis_hip_rosa_o_stop_grad_sgd": (
+        i32, [vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, f32, f32, vp, vp, vp]),
     "ullis_hip_heron_layout": (sz, [C.POINTER(HeronDims), C.POINTER(TensorDesc), sz,
                                     C.POINTER(C.c_uint64)]),
     "ullis_hip_heron_create": (i32, [vp, C.POINTER(HeronDims), sz, sz, C.POINTER(vp)]),

@@ -277,6 +277,11 @@ __global__ void scale_to_f16_kernel(const float* v, long n, const float* amax, u
 // Sums part[nblk][ncols] over nblk: 16 columns per block, 64 partial subsets
 // per column summed in a fixed order (strided, then an LDS tree), so the result
 // does not depend on scheduling. Columns < split go to target a, the rest to b.
+__global__ void f32_to_f16_kernel(const float* v, long n, uint16_t* out16) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out16[i] = f32_to_f16_bits(v[i]);
+}
+
 __global__ __launch_bounds__(1024) void partial_reduce_kernel(const float* part, int nblk,
                                                               long ncols, long split, VecTarget a,
                                                               VecTarget b) {
@@ -465,6 +470,12 @@ hipError_t scale_to_f16(hipStream_t s, const float* v, long n, const float* amax
     return hipErrorInvalidValue;
   launch(scale_to_f16_kernel, dim3((unsigned)cdiv(cdiv(n, 4), 256)), dim3(256), 0, s, v, n, amax,
          out16);
+  return hipGetLastError();
+}
+
+hipError_t f32_to_f16(hipStream_t s, const float* v, long n, uint16_t* out16) {
+  if (n <= 0) return hipSuccess;
+  launch(f32_to_f16_kernel, grid1d(n), dim3(256), 0, s, v, n, out16);
   return hipGetLastError();
 }
 

@@ -241,6 +241,8 @@ hipError_t column_sum_partials(hipStream_t s, const float* v, const uint8_t* idx
 // copy when out16 / amax are given.
 hipError_t scale_to_f16(hipStream_t s, const float* v, long n, const float* amax,
                         uint16_t* out16);
+// out16 = f16 RNE of v (overflow to +-Inf, Fp16::from_f32).
+hipError_t f32_to_f16(hipStream_t s, const float* v, long n, uint16_t* out16);
 // Sums part[nblk][ch] -> out (optional) and optional clipped SGD with lr.
 hipError_t vector_finish(hipStream_t s, const float* part, int nblk, long ch, float* out,
                          float lr, uint16_t* values, float* residual);

@@ -305,6 +305,131 @@ class HipRuntime:
             out["weight_gradient"] = g_w.download(np.float32, vocab * d)
         return out
 
+    # --------------------------------------------------- block-level methods
+    def _x16_or_f32(self, x):
+        xa = np.asarray(x)
+        if xa.dtype == np.uint16:
+            return self.put(xa), F16
+        return self.put(xa.astype(np.float32)), F32
+
+    def cmix_block_forward(self, x, mix, key_bits, key_scale, value_weight, batch, time,
+                           d_model, dim_ffn):
+        """MetalRuntime::cmix_block_forward (src/metal.rs:1891). x: fp32 values or
+        f16 bits (uint16). Returns {"out", "gpu_tape"}; the tape feeds
+        cmix_block_backward_sgd."""
+        dx, dt = self._x16_or_f32(x)
+        rows = batch * time
+        tape = self.buffer(self.lib.ullis_hip_cmix_tape_bytes(rows, d_model, dim_ffn))
+        out = self.buffer(4 * rows * d_model)
+        ptrs = [self.put(np.asarray(a, t)) for a, t in
+                ((mix, np.uint16), (key_bits, np.uint32), (key_scale, np.uint16),
+                 (value_weight, np.uint16))]
+        self._check(self.lib.ullis_hip_cmix_block_forward(
+            self.ctx, dx.ptr, dt, *(p.ptr for p in ptrs), batch, time, d_model, dim_ffn, out.ptr,
+            tape.ptr), "cmix_block_forward")
+        return {"out": out.download(np.float32, rows * d_model), "gpu_tape": tape}
+
+    def cmix_block_backward_sgd(self, tape, gy, mix, key_bits, key_scale, key_latent,
+                                key_residual, value_weight, value_residual, batch, time, d_model,
+                                dim_ffn, learning_rate, ste_scale):
+        """MetalRuntime::cmix_block_backward_sgd (src/metal.rs:2165); fields of
+        CmixBlockBackwardSgd, plus next_key_bits_t."""
+        rows = batch * time
+        n_key, n_val = dim_ffn * d_model, d_model * dim_ffn
+        words = (n_key + 31) // 32
+        dg = self.put(np.asarray(gy, np.float32))
+        dm = self.put(np.asarray(mix, np.uint16))
+        db = self.put(np.asarray(key_bits, np.uint32))
+        dbt = self.buffer(4 * words)
+        self._check(self.lib.ullis_hip_transpose_bits(self.ctx, db.ptr, dim_ffn, d_model, dbt.ptr),
+                    "transpose_bits")
+        ds = self.put(np.asarray(key_scale, np.uint16))
+        dl = self.put(np.asarray(key_latent, np.uint16))
+        dlr = self.put(np.asarray(key_residual, np.float32))
+        dv = self.put(np.asarray(value_weight, np.uint16))
+        dvr = self.put(np.asarray(value_residual, np.float32))
+        g_x, g_mix, g_ks = (self.buffer(4 * rows * d_model), self.buffer(4 * d_model),
+                            self.buffer(4 * dim_ffn))
+        self._check(self.lib.ullis_hip_cmix_block_backward_sgd(
+            self.ctx, tape.ptr, dg.ptr, dm.ptr, db.ptr, dbt.ptr, ds.ptr, dl.ptr, dlr.ptr, dv.ptr,
+            dvr.ptr, batch, time, d_model, dim_ffn, learning_rate, ste_scale, g_x.ptr, g_mix.ptr,
+            g_ks.ptr), "cmix_block_backward_sgd")
+        return {
+            "g_x": g_x.download(np.float32, rows * d_model),
+            "g_mix": g_mix.download(np.float32, d_model),
+            "g_key_scale": g_ks.download(np.float32, dim_ffn),
+            "next_key_latent": dl.download(np.uint16, n_key),
+            "next_key_residual": dlr.download(np.float32, n_key),
+            "next_key_bits": db.download(np.uint32, words),
+            "next_key_bits_t": dbt.download(np.uint32, words),
+            "next_value_weight": dv.download(np.uint16, n_val),
+            "next_value_residual": dvr.download(np.float32, n_val),
+        }
+
+    def rosa_block_forward(self, x, mix_q, mix_k, mix_v, q_bits, q_scale, q_bias, k_bits,
+                           k_scale, k_bias, v_bits, v_scale, v_bias, e, o_bits, o_scale, o_bias,
+                           batch, time, channels, sam):
+        """MetalRuntime::rosa_block_forward (src/metal.rs:1334-1511). The suffix
+        automaton stays with the caller: sam(q_plane, k_plane, v_plane) returns
+        idx, u8 channel-major [batch][channels][time]
+        (rosa_qkv_batch_packed_channel_major, src/rosa.rs:486-513). Returns
+        {"out", "planes", "idx", "gpu_tape"}."""
+        dx, dt = self._x16_or_f32(x)
+        rows = batch * time
+        words = (rows * channels + 31) // 32
+        u16 = lambda a: self.put(np.asarray(a, np.uint16))
+        u32 = lambda a: self.put(np.asarray(a, np.uint32))
+        mq, mk, mv = u16(mix_q), u16(mix_k), u16(mix_v)
+        qb, qs, qbi = u32(q_bits), u16(q_scale), u16(q_bias)
+        kb, ks, kbi = u32(k_bits), u16(k_scale), u16(k_bias)
+        vb, vs, vbi = u32(v_bits), u16(v_scale), u16(v_bias)
+        planes = [self.buffer(4 * words) for _ in range(3)]
+        self._check(self.lib.ullis_hip_rosa_qkv_forward(
+            self.ctx, dx.ptr, dt, mq.ptr, mk.ptr, mv.ptr, qb.ptr, qs.ptr, qbi.ptr, kb.ptr, ks.ptr,
+            kbi.ptr, vb.ptr, vs.ptr, vbi.ptr, batch, time, channels, *(p.ptr for p in planes)),
+            "rosa_qkv_forward")
+        host_planes = [p.download(np.uint32, words) for p in planes]
+        idx = np.ascontiguousarray(sam(*host_planes), np.uint8)
+        if idx.size != rows * channels:
+            raise ValueError("ROSA idx length mismatch")
+        di, de = self.put(idx), u16(e)
+        ob, osc, obi = u32(o_bits), u16(o_scale), u16(o_bias)
+        tape = self.buffer(self.lib.ullis_hip_rosa_tape_bytes(rows, channels))
+        out = self.buffer(4 * rows * channels)
+        self._check(self.lib.ullis_hip_rosa_out_forward(
+            self.ctx, di.ptr, de.ptr, ob.ptr, osc.ptr, obi.ptr, batch, time, channels, out.ptr,
+            tape.ptr), "rosa_out_forward")
+        return {"out": out.download(np.float32, rows * channels), "planes": host_planes,
+                "idx": idx, "gpu_tape": tape}
+
+    def rosa_o_stop_grad_sgd(self, tape, gy, o_bits, o_scale, latent, residual, rows, channels,
+                             learning_rate, ste_scale):
+        """MetalRuntime::rosa_o_stop_grad_sgd (src/metal.rs:2409); fields of
+        RosaOStopGradSgd, plus next_bits_t."""
+        n = channels * channels
+        words = (n + 31) // 32
+        dg = self.put(np.asarray(gy, np.float32))
+        db = self.put(np.asarray(o_bits, np.uint32))
+        dbt = self.buffer(4 * words)
+        self._check(self.lib.ullis_hip_transpose_bits(self.ctx, db.ptr, channels, channels,
+                                                      dbt.ptr), "transpose_bits")
+        ds = self.put(np.asarray(o_scale, np.uint16))
+        dl = self.put(np.asarray(latent, np.uint16))
+        dr = self.put(np.asarray(residual, np.float32))
+        g_e, g_s, g_b = (self.buffer(4 * channels) for _ in range(3))
+        self._check(self.lib.ullis_hip_rosa_o_stop_grad_sgd(
+            self.ctx, tape.ptr, dg.ptr, db.ptr, dbt.ptr, ds.ptr, dl.ptr, dr.ptr, rows, channels,
+            learning_rate, ste_scale, g_e.ptr, g_s.ptr, g_b.ptr), "rosa_o_stop_grad_sgd")
+        return {
+            "e_gradient": g_e.download(np.float32, channels),
+            "scale_gradient": g_s.download(np.float32, channels),
+            "bias_gradient": g_b.download(np.float32, channels),
+            "next_latent": dl.download(np.uint16, n),
+            "next_residual": dr.download(np.float32, n),
+            "next_bits": db.download(np.uint32, words),
+            "next_bits_t": dbt.download(np.uint32, words),
+        }
+
 
 @dataclass
 class HeronShape:
