@@ -4,8 +4,10 @@
 Workload (config 4): one full Heron train step's GPU work, D=512, L=12,
 T=2048, vocab 8192, F=2048, batch 1, rosa_grad = stop_grad_bits, with the
 suffix-automaton output synthesised as Bernoulli(0.5) indices (+-e). Inputs
-are resident in HBM before the timed region; a step is ullis_hip_heron_step
-(forward, head + streamed CE, backward, every parameter update). The timed
+are resident in HBM before the timed region; a step is UllisHeron::
+train_step_on from token ids: the embedding gather, ullis_hip_heron_step
+(forward, head + streamed CE, backward, every parameter update) and the
+embedding scatter-SGD (HeronTrainer.step_tokens). The timed
 region is bracketed by stream synchronisation; HIP events on the library's
 stream give the step time.
 
@@ -120,7 +122,14 @@ def main() -> int:
     trainer.upload_arena(arena)
     x, labels, idx = step_inputs(shape.rows, c["d_model"], c["vocab"], c["n_layers"], c["batch"],
                                  c["time"], seed=7)
-    dx, dl, di = rt.put(x), rt.put(labels), rt.put(idx)
+    dl, di = rt.put(labels), rt.put(idx)
+    # embedding table [vocab, d] (f16 + fp32 carry) and token ids; the gather
+    # writes x_emb each step
+    rng = np.random.default_rng(7)
+    table = rt.put(rng.standard_normal(c["vocab"] * c["d_model"]).astype(np.float16).view(np.uint16))
+    table_res = rt.zeros(np.float32, c["vocab"] * c["d_model"])
+    token_ids = rt.put(rng.integers(0, c["vocab"], shape.rows).astype(np.uint32))
+    dx = rt.put(x)
     g = rt.zeros(np.float32, shape.rows * c["d_model"])
     rl = rt.zeros(np.float32, shape.rows)
     st = rt.zeros(np.float32, 4)
@@ -128,7 +137,8 @@ def main() -> int:
     qkv = rt.zeros(np.uint32, c["n_layers"] * 3 * words)
 
     def step():
-        trainer.step(dx, dl, NO_IGNORE, LR, di, g, rl, st, qkv)
+        trainer.step_tokens(table, table_res, token_ids, dl, NO_IGNORE, LR, di, dx, g, rl, st,
+                            qkv)
 
     import ctypes as C
 
@@ -193,7 +203,8 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
-        "data": "synthetic (seeded; random-init heron parameters, ROSA indices Bernoulli(0.5))",
+        "data": "synthetic (seeded; random-init heron parameters and embedding table, uniform "
+                "token ids and labels, ROSA indices Bernoulli(0.5))",
         "config": {"workload": "heron train step (config 4): D512 L12 F2048 V8192 T2048 B1, "
                                "stop_grad_bits, lr 0.01",
                    "global_batch": c["batch"], "seq_len": c["time"], "parallelism": "none (1 GPU)"},

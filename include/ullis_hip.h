@@ -140,6 +140,23 @@ int ullis_hip_packed_head_train_sgd(ullis_hip_ctx* ctx, const uint16_t* hidden16
                                     float ste_scale, float* row_loss, float* stats4,
                                     float* g_hidden, float* g_scale, float* g_bias, float* g_w);
 
+/* Embedding gather of UllisHeron::train_step_on (src/model.rs:2866-2873):
+ * x[r] = the f16 table row tokens[r] as fp32 (table [vocab, d]). The
+ * reference rejects an id >= vocab before the step (src/model.rs:2852-2861);
+ * here tokens are device data, so such a row is written as zeros and counted
+ * into *invalid (device u32, accumulated; optional) for the caller to check. */
+int ullis_hip_embedding_gather(ullis_hip_ctx* ctx, const uint16_t* table, size_t vocab, size_t d,
+                               const uint32_t* tokens, size_t rows, float* x, uint32_t* invalid);
+
+/* Embedding scatter-SGD of UllisHeron::train_step_on (src/model.rs:2986-2993):
+ * for r in row order, clipped SGD (Fp16Storage::apply_clipped_sgd) of table
+ * row tokens[r] with g[r] ([rows, d] fp32), in place with its fp32 carry.
+ * Rows sharing a token are applied in row order, as the reference's
+ * sequential loop does; ids >= vocab are skipped. */
+int ullis_hip_embedding_scatter_sgd(ullis_hip_ctx* ctx, uint16_t* table, float* residual,
+                                    size_t vocab, size_t d, const uint32_t* tokens, size_t rows,
+                                    const float* g, float learning_rate);
+
 /* ---- block-level methods of the Metal train step ----
  * The reference moves train tapes as MetalBuffers from a block's forward to
  * its backward (src/model.rs:1242-1256, 1525-1535); here the caller owns the

@@ -560,6 +560,7 @@ int ucr_rosa_e_grad(const float* g_y, const uint8_t* idx, size_t rows, size_t ch
 
 /* ----------------------------------------------------------- embedding -- */
 
+/* train_step_on's gather, src/model.rs:2866-2873 */
 int ucr_embedding_gather(const uint16_t* table, size_t d, const uint32_t* tokens, size_t rows,
                          float* x) {
   size_t row, c;
@@ -570,6 +571,8 @@ int ucr_embedding_gather(const uint16_t* table, size_t d, const uint32_t* tokens
   return 0;
 }
 
+/* train_step_on's scatter-SGD, src/model.rs:2986-2993: rows in order, so a
+ * repeated token is stepped once per row, in row order */
 int ucr_embedding_scatter_sgd(uint16_t* table, float* residual, size_t d,
                               const uint32_t* tokens, size_t rows, const float* g_x,
                               float learning_rate) {

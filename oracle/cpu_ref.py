@@ -268,6 +268,19 @@ def rosa_e_grad(g_y, idx, rows, ch):
     return out
 
 
+def embedding_gather(table, d, tokens):
+    t, k = _u16(table), _u32(tokens)
+    x = np.empty(k.size * d, np.float32)
+    lib().ucr_embedding_gather(_p(t), _sz(d), _p(k), _sz(k.size), _p(x))
+    return x
+
+
+def embedding_scatter_sgd(table, residual, d, tokens, g_x, lr):
+    t, r, k, g = _u16(table).copy(), _f32(residual).copy(), _u32(tokens), _f32(g_x)
+    lib().ucr_embedding_scatter_sgd(_p(t), _p(r), _sz(d), _p(k), _sz(k.size), _p(g), C.c_float(lr))
+    return t, r
+
+
 # -------------------------------------------------------------------- a17
 def heron_layout(dims: HeronDims):
     total = C.c_uint64()

@@ -183,3 +183,44 @@ def test_full_heron_step_properties(rt):
             lat = tensor_view(a0, lay, name[: -len(".bits")] + ".latent")
             np.testing.assert_array_equal(tensor_view(a0, lay, name), o.pack_latent_bits(lat),
                                           err_msg=name)
+
+
+def test_step_from_tokens_gathers_steps_and_scatters(rt):
+    """HeronTrainer.step_tokens (gather, step, scatter-SGD on the device)
+    against the same three stages run one at a time: the oracle's gather,
+    the device step on its output, the oracle's scatter-SGD of the returned
+    embedding gradient (all three bit-exact by construction)."""
+    shape = HeronShape(d_model=64, n_layers=2, dim_ffn=128, vocab=300, batch=2, time=64)
+    trainer = HeronTrainer(rt, shape)
+    arena = heron_arena(trainer.layout, trainer.arena_bytes, shape.dims(), seed=5)
+    _, labels, idx = step_inputs(shape.rows, 64, 300, 2, 2, 64, seed=5)
+    rng = np.random.default_rng(5)
+    table = rng.standard_normal(300 * 64).astype(np.float16).view(np.uint16)
+    table_res = (rng.standard_normal(300 * 64) * 1e-4).astype(np.float32)
+    tokens = rng.integers(0, 40, shape.rows).astype(np.uint32)  # repeats
+    nd = shape.rows * 64
+    dl, di = rt.put(labels), rt.put(idx)
+
+    trainer.upload_arena(arena)
+    dt, dtr, dk = rt.put(table), rt.put(table_res), rt.put(tokens)
+    xe, g = rt.zeros(np.float32, nd), rt.zeros(np.float32, nd)
+    rl, st, bad = rt.zeros(np.float32, shape.rows), rt.zeros(np.float32, 4), rt.zeros(np.uint32, 1)
+    trainer.step_tokens(dt, dtr, dk, dl, NO_IGNORE, 0.01, di, xe, g, rl, st, invalid=bad)
+    rt.sync()
+    assert bad.download(np.uint32)[0] == 0
+    got = (trainer.download_arena(), dt.download(np.uint16), dtr.download(np.float32),
+           rl.download(np.float32))
+
+    trainer.upload_arena(arena)
+    x = o.embedding_gather(table, 64, tokens)
+    g2 = rt.zeros(np.float32, nd)
+    rl2 = rt.zeros(np.float32, shape.rows)
+    trainer.step(rt.put(x), dl, NO_IGNORE, 0.01, di, g2, rl2)
+    rt.sync()
+    want_t, want_r = o.embedding_scatter_sgd(table, table_res, 64, tokens, g2.download(np.float32),
+                                             0.01)
+    np.testing.assert_array_equal(got[0], trainer.download_arena())
+    np.testing.assert_array_equal(got[1], want_t)
+    np.testing.assert_array_equal(got[2].view(np.uint32), want_r.view(np.uint32))
+    np.testing.assert_array_equal(got[3].view(np.uint32), rl2.download(np.float32).view(np.uint32))
+    assert not np.array_equal(got[1], table)  # the table did move

@@ -305,3 +305,50 @@ def test_device_copy_kernel(rt, dst_off, src_off, n):
     assert (got[:dst_off] == 0xAB).all() and (got[dst_off + n:] == 0xAB).all()
     src.free()
     dst.free()
+
+
+# --------------------------------------------------------------- embedding
+@pytest.mark.parametrize("vocab,d,rows,dist", [
+    (8192, 512, 2048, "zipf"),   # config 4 widths, natural repeats
+    (5, 7, 100, "uniform"),      # heavy collisions, d not a multiple of 4
+    (1, 64, 300, "uniform"),     # one token: a 300-row chain across ballot chunks
+    (50000, 256, 513, "uniform"),
+])
+def test_embedding_gather_scatter_sgd_bit_exact(rt, vocab, d, rows, dist):
+    rng = np.random.default_rng(vocab + d + rows)
+    table = f16(rng.normal(0, 0.5, vocab * d))
+    res = (rng.standard_normal(vocab * d) * 1e-4).astype(np.float32)
+    if dist == "zipf":
+        tokens = (rng.zipf(1.3, rows) - 1) % vocab
+    else:
+        tokens = rng.integers(0, vocab, rows)
+    tokens = tokens.astype(np.uint32)
+    x = rt.embedding_gather(table, tokens, vocab, d)
+    np.testing.assert_array_equal(x.view(np.uint32), o.embedding_gather(table, d, tokens).view(np.uint32))
+    g = (rng.standard_normal(rows * d) * 0.7).astype(np.float32)
+    for lr in (0.01, 0.3):
+        got_t, got_r = rt.embedding_scatter_sgd(table, res, tokens, g, vocab, d, lr)
+        want_t, want_r = o.embedding_scatter_sgd(table, res, d, tokens, g, lr)
+        np.testing.assert_array_equal(got_t, want_t)
+        np.testing.assert_array_equal(got_r.view(np.uint32), want_r.view(np.uint32))
+
+
+def test_embedding_out_of_range_ids(rt):
+    # the reference rejects ids >= vocab (src/model.rs:2850-2861); on the device
+    # the gather zeroes and counts such rows and the scatter skips them
+    from ullis_amd.runtime import HipError
+
+    vocab, d = 16, 32
+    rng = np.random.default_rng(3)
+    table = f16(rng.normal(0, 0.5, vocab * d))
+    res = np.zeros(vocab * d, np.float32)
+    tokens = np.array([3, 16, 3, 0xFFFFFFFF, 7], np.uint32)
+    with pytest.raises(HipError, match="2 token ids"):
+        rt.embedding_gather(table, tokens, vocab, d)
+    g = (rng.standard_normal(tokens.size * d)).astype(np.float32)
+    got_t, got_r = rt.embedding_scatter_sgd(table, res, tokens, g, vocab, d, 0.1)
+    keep = tokens < vocab
+    gk = g.reshape(-1, d)[keep].ravel()
+    want_t, want_r = o.embedding_scatter_sgd(table, res, d, tokens[keep], gk, 0.1)
+    np.testing.assert_array_equal(got_t, want_t)
+    np.testing.assert_array_equal(got_r.view(np.uint32), want_r.view(np.uint32))

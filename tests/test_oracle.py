@@ -445,3 +445,30 @@ def test_rosa_expand_and_e_grad_float64():
     ge = o.rosa_e_grad(gy, idx, rows, ch)
     np.testing.assert_allclose(ge, (gy.reshape(rows, ch) * (2.0 * idx.reshape(rows, ch) - 1)).sum(0),
                                atol=1e-6)
+
+
+def test_embedding_gather_and_scatter_sgd_against_numpy():
+    # train_step_on's gather / scatter loops (src/model.rs:2866-2873, 2986-2993)
+    rng = np.random.default_rng(12)
+    vocab, d, rows = 9, 5, 40
+    table = f16(rng.normal(0, 0.5, vocab * d))
+    res = (rng.standard_normal(vocab * d) * 1e-4).astype(np.float32)
+    tokens = rng.integers(0, vocab, rows).astype(np.uint32)  # many repeats
+    x = o.embedding_gather(table, d, tokens)
+    np.testing.assert_array_equal(x, h2f(table).reshape(vocab, d)[tokens].ravel())
+    g = (rng.standard_normal(rows * d) * 0.7).astype(np.float32)
+    lr = 0.05
+    got_t, got_r = o.embedding_scatter_sgd(table, res, d, tokens, g, lr)
+    want_t, want_r = table.copy(), res.copy()
+    for r, tok in enumerate(tokens):  # one row at a time, in row order
+        sl = slice(int(tok) * d, int(tok) * d + d)
+        want_t[sl], want_r[sl] = numpy_clipped(want_t[sl], want_r[sl], g[r * d:(r + 1) * d], lr)
+    np.testing.assert_array_equal(got_t, want_t)
+    np.testing.assert_array_equal(got_r.view(np.uint32), want_r.view(np.uint32))
+    # the order of repeated rows matters (f16 rounding between applications),
+    # so a reordered loop fails this check
+    rev_t, rev_r = table.copy(), res.copy()
+    for r in reversed(range(rows)):
+        sl = slice(int(tokens[r]) * d, int(tokens[r]) * d + d)
+        rev_t[sl], rev_r[sl] = numpy_clipped(rev_t[sl], rev_r[sl], g[r * d:(r + 1) * d], lr)
+    assert not (np.array_equal(rev_t, want_t) and np.array_equal(rev_r, want_r))

@@ -72,6 +72,8 @@ SIGNATURES = {
         i32,
         [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, u32, f32, f32,
          vp, vp, vp, vp, vp, vp]),
+    "ullis_hip_embedding_gather": (i32, [vp, vp, sz, sz, vp, sz, vp, vp]),
+    "ullis_hip_embedding_scatter_sgd": (i32, [vp, vp, vp, sz, sz, vp, sz, vp, f32]),
     "ullis_hip_cmix_tape_bytes": (sz, [sz, sz, sz]),
     "ullis_hip_rosa_tape_bytes": (sz, [sz, sz]),
     "ullis_hip_cmix_block_forward": (i32, [vp, vp, i32, vp, vp, vp, vp, sz, sz, sz, sz, vp, vp]),

@@ -272,6 +272,16 @@ hipError_t rosa_expand_layers(hipStream_t s, const uint8_t* idx_cm, const uint16
                               const uint16_t* const* e_dev, long layers, long batch, long time,
                               long ch, uint16_t* y16, uint8_t* idx_rm);
 
+// ---------------------------------------------------------------- embedding
+// x = f32 rows of the f16 table at tokens (ids >= vocab: zero rows, counted
+// into *invalid when non-null).
+hipError_t embedding_gather(hipStream_t s, const uint16_t* table, long vocab, long d,
+                            const uint32_t* tokens, long rows, float* x, uint32_t* invalid);
+// Clipped SGD of table rows with g, rows sharing a token applied in row order.
+hipError_t embedding_scatter_sgd(hipStream_t s, uint16_t* table, float* residual, long vocab,
+                                 long d, const uint32_t* tokens, long rows, const float* g,
+                                 float lr);
+
 // --------------------------------------------------------------- head + CE
 
 struct HeadCe {

@@ -305,6 +305,34 @@ class HipRuntime:
             out["weight_gradient"] = g_w.download(np.float32, vocab * d)
         return out
 
+    # ------------------------------------------------------------ embedding
+    def embedding_gather(self, table, tokens, vocab, d):
+        """The gather of UllisHeron::train_step_on (src/model.rs:2866-2873): fp32
+        rows of the f16 table. An id >= vocab raises, as the reference rejects
+        it before the step (the library zeroes the row and counts it)."""
+        tok = np.asarray(tokens, np.uint32)
+        dt, dk = self.put(np.asarray(table, np.uint16)), self.put(tok)
+        x = self.buffer(4 * tok.size * d)
+        bad = self.zeros(np.uint32, 1)
+        self._check(self.lib.ullis_hip_embedding_gather(self.ctx, dt.ptr, vocab, d, dk.ptr,
+                                                        tok.size, x.ptr, bad.ptr),
+                    "embedding_gather")
+        n_bad = int(bad.download(np.uint32, 1)[0])
+        if n_bad:
+            raise HipError(f"embedding_gather: {n_bad} token ids >= vocab {vocab}")
+        return x.download(np.float32, tok.size * d)
+
+    def embedding_scatter_sgd(self, table, residual, tokens, g, vocab, d, lr):
+        """The scatter-SGD of UllisHeron::train_step_on (src/model.rs:2986-2993).
+        Returns the stepped (table, residual)."""
+        tok = np.asarray(tokens, np.uint32)
+        dt, dr = self.put(np.asarray(table, np.uint16)), self.put(np.asarray(residual, np.float32))
+        dk, dg = self.put(tok), self.put(np.asarray(g, np.float32))
+        self._check(self.lib.ullis_hip_embedding_scatter_sgd(self.ctx, dt.ptr, dr.ptr, vocab, d,
+                                                             dk.ptr, tok.size, dg.ptr, lr),
+                    "embedding_scatter_sgd")
+        return dt.download(np.uint16, vocab * d), dr.download(np.float32, vocab * d)
+
     # --------------------------------------------------- block-level methods
     def _x16_or_f32(self, x):
         xa = np.asarray(x)
@@ -540,3 +568,22 @@ class HeronTrainer:
             self.h, x_emb.ptr, labels.ptr, ignore_id, lr, rosa_idx.ptr, g_emb.ptr,
             row_loss.ptr if row_loss else None, stats.ptr if stats else None,
             qkv_bits.ptr if qkv_bits else None), "heron_step")
+
+    def step_tokens(self, table: DeviceBuffer, table_res: DeviceBuffer, tokens: DeviceBuffer,
+                    labels: DeviceBuffer, ignore_id: int, lr: float, rosa_idx: DeviceBuffer,
+                    x_emb: DeviceBuffer, g_emb: DeviceBuffer, row_loss: DeviceBuffer | None = None,
+                    stats: DeviceBuffer | None = None, qkv_bits: DeviceBuffer | None = None,
+                    invalid: DeviceBuffer | None = None):
+        """UllisHeron::train_step_on from token ids (src/model.rs:2827-3025): the
+        embedding gather, the step and the embedding scatter-SGD, all
+        stream-ordered on the device. table / table_res: f16 [vocab, d] and its
+        fp32 carry; x_emb / g_emb: fp32 [rows, d] work buffers; invalid
+        (optional u32) counts token ids >= vocab."""
+        s, lib, ctx = self.shape, self.rt.lib, self.rt.ctx
+        self.rt._check(lib.ullis_hip_embedding_gather(
+            ctx, table.ptr, s.vocab, s.d_model, tokens.ptr, s.rows, x_emb.ptr,
+            invalid.ptr if invalid else None), "embedding_gather")
+        self.step(x_emb, labels, ignore_id, lr, rosa_idx, g_emb, row_loss, stats, qkv_bits)
+        self.rt._check(lib.ullis_hip_embedding_scatter_sgd(
+            ctx, table.ptr, table_res.ptr, s.vocab, s.d_model, tokens.ptr, s.rows, g_emb.ptr, lr),
+            "embedding_scatter_sgd")
