@@ -224,3 +224,42 @@ def test_step_from_tokens_gathers_steps_and_scatters(rt):
     np.testing.assert_array_equal(got[2].view(np.uint32), want_r.view(np.uint32))
     np.testing.assert_array_equal(got[3].view(np.uint32), rl2.download(np.float32).view(np.uint32))
     assert not np.array_equal(got[1], table)  # the table did move
+
+
+def test_checkpoint_resume_continues_bit_identically(rt):
+    """checkpoint_roundtrip_after_train_preserves_forward (src/model.rs:
+    4888-4941) on the device: train a step, save checkpoint v2, load it into a
+    second trainer, and the next step of both is bit-identical."""
+    from ullis_amd.checkpoint import heron_config, load_checkpoint, save_checkpoint
+
+    shape = HeronShape(d_model=64, n_layers=2, dim_ffn=128, vocab=256, batch=1, time=64)
+    a, b = HeronTrainer(rt, shape), HeronTrainer(rt, shape)
+    arena = heron_arena(a.layout, a.arena_bytes, shape.dims(), seed=4)
+    _, labels, idx = step_inputs(shape.rows, 64, 256, 2, 1, 64, seed=4)
+    rng = np.random.default_rng(4)
+    table = rng.standard_normal(256 * 64).astype(np.float16).view(np.uint16)
+    tokens = rt.put(rng.integers(0, 256, shape.rows).astype(np.uint32))
+    nd = shape.rows * 64
+    dl, di = rt.put(labels), rt.put(idx)
+    xe, g = rt.zeros(np.float32, nd), rt.zeros(np.float32, nd)
+    st = rt.zeros(np.float32, 4)
+    a.upload_arena(arena)
+    ta, tra = rt.put(table), rt.zeros(np.float32, table.size)
+    a.step_tokens(ta, tra, tokens, dl, NO_IGNORE, 0.05, di, xe, g, stats=st)
+    rt.sync()
+    data = save_checkpoint(a.download_arena(), a.layout, ta.download(np.uint16),
+                           tra.download(np.float32), heron_config(shape), step=17, loss_ema=4.5)
+    arena2, emb, emb_res, meta = load_checkpoint(data, b.layout, b.arena_bytes, shape)
+    assert meta["step"] == 17 and meta["loss_ema"] == 4.5
+    b.upload_arena(arena2)  # rebuilds the derived bits_t
+    tb, trb = rt.put(emb), rt.put(emb_res)
+    np.testing.assert_array_equal(b.download_arena(), a.download_arena())
+    outs = []
+    for tr, t, r in ((a, ta, tra), (b, tb, trb)):
+        rl = rt.zeros(np.float32, shape.rows)
+        tr.step_tokens(t, r, tokens, dl, NO_IGNORE, 0.05, di, xe, g, rl)
+        rt.sync()
+        outs.append((tr.download_arena(), t.download(np.uint16), r.download(np.float32),
+                     rl.download(np.float32)))
+    for x, y in zip(*outs):
+        np.testing.assert_array_equal(x, y)
