@@ -74,6 +74,61 @@ def cpu_baseline(rows: int) -> dict:
     }
 
 
+# Few-row forward products of a T = 1 greedy decode at batch 1 and 8 (the
+# GEMV pass of the stress profile, config 5, and the same layers at config 4):
+# (label, kind, out, in). Weight bytes per launch: out*in/8 for sign bits,
+# 2*out*in for the fp16 CMix value.
+DECODE_GEMV = [
+    ("cfg5 head", "packed", 32768, 1024), ("cfg5 cmix key", "packed", 4096, 1024),
+    ("cfg5 rosa q/k/v/o", "packed", 1024, 1024), ("cfg5 cmix value", "fp16", 1024, 4096),
+    ("cfg4 head", "packed", 8192, 512), ("cfg4 cmix key", "packed", 2048, 512),
+    ("cfg4 rosa q/k/v/o", "packed", 512, 512), ("cfg4 cmix value", "fp16", 512, 2048),
+]
+
+
+def decode_gemv(rt, reps: int) -> None:
+    """One JSON line per decode product: kernel time of one launch (its own
+    start / end timestamps, ullis_hip_time_next_launch), averaged over reps,
+    and the weight bytes it streams against the HBM peak."""
+    import ctypes as C
+
+    lib, ctx = rt.lib, rt.ctx
+    rng = np.random.default_rng(5)
+    for label, kind, out_f, in_f in DECODE_GEMV:
+        if kind == "packed":
+            w = rt.put(rng.integers(0, 2 ** 32, out_f * in_f // 32, dtype=np.uint32))
+            scale = rt.put(np.full(out_f, 0.02, np.float16).view(np.uint16))
+            bias = rt.put(np.zeros(out_f, np.float16).view(np.uint16))
+            wbytes = out_f * in_f / 8
+        else:
+            w = rt.put(rng.normal(0, 0.02, out_f * in_f).astype(np.float16).view(np.uint16))
+            wbytes = 2.0 * out_f * in_f
+        for m in (1, 8):
+            x = rt.put(rng.standard_normal(m * in_f).astype(np.float16).view(np.uint16))
+            y = rt.buffer(4 * m * out_f)
+
+            def call():
+                if kind == "packed":
+                    return lib.ullis_hip_binary_linear(ctx, x.ptr, 1, w.ptr, scale.ptr, bias.ptr, m,
+                                                       in_f, out_f, y.ptr, None)
+                return lib.ullis_hip_fp16_linear(ctx, x.ptr, 1, w.ptr, m, in_f, out_f, y.ptr, None)
+
+            total = 0.0
+            for i in range(reps + 3):
+                rt._check(lib.ullis_hip_time_next_launch(ctx, 2, 3), "arm")
+                rt._check(call(), label)
+                ms = C.c_float()
+                rt._check(lib.ullis_hip_event_elapsed_ms(ctx, 2, 3, C.byref(ms)), "elapsed")
+                if i >= 3:
+                    total += ms.value
+            us = total / reps * 1e3
+            gbs = wbytes / (us * 1e-6) / 1e9
+            print(json.dumps({"decode_gemv": label, "kind": kind, "rows": m, "out": out_f,
+                              "in": in_f, "avg_us": round(us, 2), "weight_bytes": int(wbytes),
+                              "achieved_gbs": round(gbs, 1),
+                              "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}), flush=True)
+
+
 def copy_calibration(rt, mib: int) -> None:
     """One copy kernel (ullis_hip_copy) that reads `mib` MiB and writes `mib` MiB.
 
@@ -101,6 +156,9 @@ def main() -> int:
     ap.add_argument("--probe", default="value_backward",
                     help="launch class timed for the roofline object ('none': no probe, "
                          "no roofline object)")
+    ap.add_argument("--decode-gemv", type=int, default=0, metavar="REPS",
+                    help="instead of the train step, time the few-row (T = 1 decode) forward "
+                         "products over REPS launches each and print one JSON line per product")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after the timed region, run one plain device copy kernel of this many "
                          "MiB (read + write) so HBM counters can be scaled against known bytes")
@@ -117,6 +175,9 @@ def main() -> int:
     c = CONFIG
     shape = HeronShape(**c)
     rt = HipRuntime(0)
+    if args.decode_gemv > 0:
+        decode_gemv(rt, args.decode_gemv)
+        return 0
     trainer = HeronTrainer(rt, shape)
     arena = heron_arena(trainer.layout, trainer.arena_bytes, shape.dims(), seed=7)
     trainer.upload_arena(arena)

@@ -61,6 +61,12 @@ int ullis_hip_copy(ullis_hip_ctx* ctx, void* dst_device, const void* src_device,
 /* Events on the context stream; slot in [0, 16). */
 int ullis_hip_event_record(ullis_hip_ctx* ctx, int slot);
 int ullis_hip_event_elapsed_ms(ullis_hip_ctx* ctx, int start_slot, int end_slot, float* ms);
+/* No reference counterpart (measurement): the next kernel this thread
+ * launches records its own start and end timestamps into event slots
+ * start_slot / end_slot (hipExtLaunchKernel); read them with
+ * ullis_hip_event_elapsed_ms. The arming is per thread and is consumed by
+ * that one launch. */
+int ullis_hip_time_next_launch(ullis_hip_ctx* ctx, int start_slot, int end_slot);
 
 /* ---- unit operations ---- */
 

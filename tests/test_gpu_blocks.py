@@ -72,7 +72,8 @@ def cmix_case(rng, batch, time, d, f):
     )
 
 
-@pytest.mark.parametrize("batch,time,d,f", [(1, 64, 64, 128), (2, 32, 64, 192), (1, 256, 128, 512)])
+@pytest.mark.parametrize("batch,time,d,f", [(1, 64, 64, 128), (2, 32, 64, 192), (1, 256, 128, 512),
+                                            (2, 4, 64, 256)])  # 8 rows: the few-row forward
 def test_cmix_block_forward_backward_match_oracle(rt, batch, time, d, f):
     rng = np.random.default_rng(11 + d + f)
     c = cmix_case(rng, batch, time, d, f)
@@ -136,7 +137,7 @@ def rosa_case(rng, batch, time, d):
     )
 
 
-@pytest.mark.parametrize("batch,time,d", [(1, 64, 64), (2, 64, 96), (1, 128, 128)])
+@pytest.mark.parametrize("batch,time,d", [(1, 64, 64), (2, 64, 96), (1, 128, 128), (1, 8, 64)])
 def test_rosa_block_forward_and_o_stop_grad_match_oracle(rt, batch, time, d):
     rng = np.random.default_rng(5 + d + time)
     c = rosa_case(rng, batch, time, d)

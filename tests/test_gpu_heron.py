@@ -95,6 +95,7 @@ SMALL = [
     HeronShape(d_model=64, n_layers=2, dim_ffn=256, vocab=512, batch=2, time=32),
     HeronShape(d_model=96, n_layers=3, dim_ffn=160, vocab=300, batch=1, time=48),
     HeronShape(d_model=512, n_layers=2, dim_ffn=2048, vocab=8192, batch=1, time=64),
+    HeronShape(d_model=64, n_layers=2, dim_ffn=128, vocab=256, batch=2, time=4),  # 8 rows
 ]
 
 

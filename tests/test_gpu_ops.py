@@ -352,3 +352,33 @@ def test_embedding_out_of_range_ids(rt):
     want_t, want_r = o.embedding_scatter_sgd(table, res, d, tokens[keep], gk, 0.1)
     np.testing.assert_array_equal(got_t, want_t)
     np.testing.assert_array_equal(got_r.view(np.uint32), want_r.view(np.uint32))
+
+
+# ------------------------------------------------------ few-row forward (GEMV)
+GEMV_REL = 1e-5  # same fp16-rounded inputs, fp32 sums in another order
+
+
+@pytest.mark.parametrize("rows", [1, 3, 8])
+@pytest.mark.parametrize("in_f,out_f,bias", [(512, 2048, True), (1024, 32768, True),
+                                             (96, 1000, False), (4096, 64, True)])
+def test_packed_few_rows_matches_oracle(rt, rows, in_f, out_f, bias):
+    # T = 1 decode shapes (batch <= 8): the few-row path of binary_linear
+    rng = np.random.default_rng(rows * 7 + in_f + out_f)
+    x16, bits, scale, b = rand_case(rng, rows, in_f, out_f, bias)
+    want = o.packed_forward(h2f32(x16), rows, in_f, out_f, bits, scale, b)
+    got = rt.binary_linear(x16, bits, scale, b, rows, in_f, out_f)
+    assert rel(got, want) <= GEMV_REL
+    got32 = rt.binary_linear(h2f32(x16), bits, scale, b, rows, in_f, out_f, x_dtype=2)
+    assert rel(got32, want) <= GEMV_REL
+    y16 = rt.binary_linear(x16, bits, scale, b, rows, in_f, out_f, out_dtype=np.float16)
+    np.testing.assert_array_equal(y16, f16(got))
+
+
+@pytest.mark.parametrize("rows", [1, 5, 8])
+@pytest.mark.parametrize("in_f,out_f", [(4096, 1024), (2048, 512), (40, 17)])
+def test_fp16_few_rows_matches_oracle(rt, rows, in_f, out_f):
+    rng = np.random.default_rng(rows + in_f + out_f)
+    x16 = f16(rng.standard_normal(rows * in_f))
+    w = f16(rng.normal(0, 0.05, out_f * in_f))
+    want = o.fp16_forward(h2f32(x16), rows, in_f, out_f, w)
+    assert rel(rt.fp16_linear(x16, w, rows, in_f, out_f), want) <= GEMV_REL

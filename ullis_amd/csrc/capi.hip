@@ -82,6 +82,7 @@ int ullis_hip_create(int device, ullis_hip_ctx** out) {
 
 void ullis_hip_destroy(ullis_hip_ctx* c) {
   if (!c) return;
+  if (t_launch_probe == &c->next_launch) t_launch_probe = nullptr;
   (void)hipSetDevice(c->device);
   if (c->stream) (void)hipStreamSynchronize(c->stream);
   for (auto& e : c->events)
@@ -152,6 +153,17 @@ int ullis_hip_copy(ullis_hip_ctx* c, void* dst, const void* src, size_t bytes) {
 int ullis_hip_event_record(ullis_hip_ctx* c, int slot) {
   if (!c || slot < 0 || slot >= 16) return ULLIS_HIP_ERR_INVALID;
   HIPCALL(hipEventRecord(c->events[slot], c->stream), "event record");
+  return 0;
+}
+
+int ullis_hip_time_next_launch(ullis_hip_ctx* c, int start_slot, int end_slot) {
+  if (!c || start_slot < 0 || start_slot >= 16 || end_slot < 0 || end_slot >= 16 ||
+      start_slot == end_slot)
+    return ULLIS_HIP_ERR_INVALID;
+  c->next_launch = LaunchProbe{};
+  c->next_launch.start = c->events[start_slot];
+  c->next_launch.stop = c->events[end_slot];
+  t_launch_probe = &c->next_launch;
   return 0;
 }
 

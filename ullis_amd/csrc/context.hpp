@@ -5,6 +5,7 @@
 
 #include <string>
 
+#include "common.hpp"
 #include "ops.hpp"
 
 struct ullis_hip_ctx {
@@ -14,6 +15,7 @@ struct ullis_hip_ctx {
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
   hipEvent_t events[16] = {};
+  ullis::LaunchProbe next_launch;  // armed by ullis_hip_time_next_launch
 
   int fail(int code, const std::string& msg) {
     err = msg;

@@ -399,6 +399,18 @@ hipError_t packed_forward(hipStream_t s, const void* x, int x_dtype, long rows, 
   const int mask = (o.y32 ? kOutY32 : 0) | (o.y32 && o.resid ? kOutResid : 0) |
                    (o.y16 ? kOutY16 : 0) | (o.relu2_16 ? kOutRelu2 : 0) |
                    (o.sign_bits ? kOutBits : 0);
+  if (packed_gemv_ok(rows, in, out, x, x_dtype, o)) {
+    switch (mask) {
+      case kOutY32:
+      case kOutY16:
+      case kOutY32 | kOutY16:
+      case kOutY32 | kOutResid:
+      case kOutY16 | kOutRelu2:
+        return packed_gemv(s, x, x_dtype, rows, in, out, bits, scale, bias, o);
+      default:
+        return hipErrorInvalidValue;
+    }
+  }
   auto run = [&](auto out_tag) {
     constexpr int OUT = decltype(out_tag)::value;
     EpiPackedFwd<OUT> epi{scale, bias, o};
@@ -652,6 +664,8 @@ hipError_t transpose_bits(hipStream_t s, const uint32_t* bits, long out, long in
 
 hipError_t fp16_forward(hipStream_t s, const void* x, int x_dtype, long rows, long in, long out,
                         const uint16_t* w, float* y32, const float* resid, uint16_t* y16) {
+  if (fp16_gemv_ok(rows, in, out, x, x_dtype, w) && (!resid || y32))
+    return fp16_gemv(s, x, x_dtype, rows, in, out, w, y32, resid, y16);
   EpiF16Fwd epi{y32, resid, y16};
   hipError_t err = hipSuccess;
   if (x_dtype == kF16 && lds::mk_ok(x, in) && lds::mk_ok(w, in) &&

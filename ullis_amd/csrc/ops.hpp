@@ -141,6 +141,19 @@ hipError_t pack_latent_bits(hipStream_t s, const uint16_t* latent, long out, lon
 hipError_t transpose_bits(hipStream_t s, const uint32_t* bits, long out, long in,
                           uint32_t* bits_t);
 
+// Few-row forward products (rows <= kGemvMaxRows; T = 1 decode): the weights
+// stream once, x stays in LDS. packed_forward / fp16_forward take these
+// paths by themselves when the *_gemv_ok conditions hold.
+constexpr int kGemvMaxRows = 8;
+bool packed_gemv_ok(long rows, long in, long out, const void* x, int x_dtype,
+                    const PackedFwdOut& o);
+hipError_t packed_gemv(hipStream_t s, const void* x, int x_dtype, long rows, long in, long out,
+                       const uint32_t* bits, const uint16_t* scale, const uint16_t* bias,
+                       const PackedFwdOut& o);
+bool fp16_gemv_ok(long rows, long in, long out, const void* x, int x_dtype, const uint16_t* w);
+hipError_t fp16_gemv(hipStream_t s, const void* x, int x_dtype, long rows, long in, long out,
+                     const uint16_t* w, float* y32, const float* resid, uint16_t* y16);
+
 // -------------------------------------------------------------- fp16 linear
 
 // y = x . W^T (W f16 [out, in]); same output options as packed_forward (no
