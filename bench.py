@@ -129,6 +129,75 @@ def decode_gemv(rt, reps: int) -> None:
                               "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}), flush=True)
 
 
+# Config 5, the stress profile of the MFMA path (a parity-test case, not the
+# bench line): D=1024, L=24, T=4096, batch 8, vocab 32768, key 1024->4096.
+STRESS = dict(d_model=1024, n_layers=24, dim_ffn=4096, vocab=32768, batch=8, time=4096)
+STRESS_PROBES = ("value_backward", "key_backward", "o_backward", "key_forward",
+                 "value_forward", "head_ce")
+
+
+def stress_profile(rt, steps: int, warmup: int) -> None:
+    """One JSON line: the config-5 train step (from token ids) and, from one
+    probe pass per launch class, each class's MFMA rate at these shapes."""
+    import ctypes as C
+    from ullis_amd.runtime import HeronShape, HeronTrainer
+    from ullis_amd.synth import heron_arena, step_inputs
+
+    c = STRESS
+    shape = HeronShape(**c)
+    tr = HeronTrainer(rt, shape)
+    tr.upload_arena(heron_arena(tr.layout, tr.arena_bytes, shape.dims(), seed=7))
+    _, labels, idx = step_inputs(shape.rows, c["d_model"], c["vocab"], c["n_layers"], c["batch"],
+                                 c["time"], seed=7)
+    rng = np.random.default_rng(7)
+    nd = shape.rows * c["d_model"]
+    table = rt.put(rng.standard_normal(c["vocab"] * c["d_model"]).astype(np.float16).view(np.uint16))
+    table_res = rt.zeros(np.float32, c["vocab"] * c["d_model"])
+    tok = rt.put(rng.integers(0, c["vocab"], shape.rows).astype(np.uint32))
+    dl, di = rt.put(labels), rt.put(idx)
+    xe, g = rt.zeros(np.float32, nd), rt.zeros(np.float32, nd)
+    st = rt.zeros(np.float32, 4)
+    lib, ctx = rt.lib, rt.ctx
+
+    def run(n):
+        rt.sync()
+        rt._check(lib.ullis_hip_event_record(ctx, 0), "event")
+        for _ in range(n):
+            tr.step_tokens(table, table_res, tok, dl, NO_IGNORE, LR, di, xe, g, stats=st)
+        rt._check(lib.ullis_hip_event_record(ctx, 1), "event")
+        rt.sync()
+        ms = C.c_float()
+        rt._check(lib.ullis_hip_event_elapsed_ms(ctx, 0, 1, C.byref(ms)), "elapsed")
+        return ms.value
+
+    for _ in range(warmup):
+        run(1)
+    ms = run(steps) / steps
+    # per layer: Q/K/V/O forward + O backward (6 D^2), key and value forward +
+    # backward (6 D F); head: logits, recompute, backward (3 D V); 2 flops/MAC
+    d, f = c["d_model"], c["dim_ffn"]
+    flops = 2.0 * shape.rows * (c["n_layers"] * 6 * d * (d + f) + 3 * d * c["vocab"])
+    kernels = {}
+    for name in STRESS_PROBES:
+        tr.probe_begin(name)
+        run(1)
+        k = tr.probe_end(name)
+        if k["count"]:
+            avg_s = k["total_ms"] / k["count"] / 1e3
+            tf = k["work"] / avg_s / 1e12
+            kernels[name] = {"kernel": k["name"], "avg_us": round(avg_s * 1e6, 1),
+                             "achieved_tflops": round(tf, 1),
+                             "frac": round(tf / FP16_PEAK_TFLOPS, 4), "launches": k["count"]}
+    print(json.dumps({
+        "stress": "config 5: heron D1024 L24 F4096 V32768 T4096 B8, stop_grad_bits, lr 0.01",
+        "ms_per_step": round(ms, 2), "tokens_per_s": round(shape.rows / (ms / 1e3), 1),
+        "algorithmic_tflop_per_step": round(flops / 1e12, 2),
+        "achieved_tflops": round(flops / (ms / 1e3) / 1e12, 1),
+        "loss_last_step": round(float(st.download(np.float32, 4)[0]), 5),
+        "kernels": kernels}), flush=True)
+    tr.close()
+
+
 def copy_calibration(rt, mib: int) -> None:
     """One copy kernel (ullis_hip_copy) that reads `mib` MiB and writes `mib` MiB.
 
@@ -159,6 +228,9 @@ def main() -> int:
     ap.add_argument("--decode-gemv", type=int, default=0, metavar="REPS",
                     help="instead of the train step, time the few-row (T = 1 decode) forward "
                          "products over REPS launches each and print one JSON line per product")
+    ap.add_argument("--stress", action="store_true",
+                    help="instead of the bench line, run config 5 (the MFMA stress profile) "
+                         "and print its step time and per-kernel MFMA rates")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after the timed region, run one plain device copy kernel of this many "
                          "MiB (read + write) so HBM counters can be scaled against known bytes")
@@ -177,6 +249,9 @@ def main() -> int:
     rt = HipRuntime(0)
     if args.decode_gemv > 0:
         decode_gemv(rt, args.decode_gemv)
+        return 0
+    if args.stress:
+        stress_profile(rt, args.steps, args.warmup)
         return 0
     trainer = HeronTrainer(rt, shape)
     arena = heron_arena(trainer.layout, trainer.arena_bytes, shape.dims(), seed=7)

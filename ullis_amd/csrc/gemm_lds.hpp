@@ -110,6 +110,16 @@ struct OpMK {
     const int c = (ks16 >> 3) + (lane >> 5);
     return *reinterpret_cast<const half8*>(stage + row * (BK * 2) + 16 * (c ^ swz(row)));
   }
+  // Phases of the pipelined K loop: pre() does the LDS read; lut() and fix()
+  // have nothing to do for an fp16 operand.
+  using Pre = half8;
+  using Raw = half8;
+  __device__ __forceinline__ Pre pre(const char* stage, const char* extra, int base, int ks16,
+                                     int lane, int k0rel) const {
+    return frag(stage, extra, base, ks16, lane, k0rel);
+  }
+  __device__ __forceinline__ Raw lut(const Pre& p, const char*) const { return p; }
+  __device__ __forceinline__ half8 fix(const Raw& r) const { return r; }
 };
 
 // fp16 [k][row] with rows contiguous (a transposed operand).
@@ -154,6 +164,14 @@ struct OpKM {
     const u32x4 r = {l[0], l[1], h[0], h[1]};
     return __builtin_bit_cast(half8, r);
   }
+  using Pre = half8;
+  using Raw = half8;
+  __device__ __forceinline__ Pre pre(const char* stage, const char* extra, int base, int ks16,
+                                     int lane, int k0rel) const {
+    return frag(stage, extra, base, ks16, lane, k0rel);
+  }
+  __device__ __forceinline__ Raw lut(const Pre& p, const char*) const { return p; }
+  __device__ __forceinline__ half8 fix(const Raw& r) const { return r; }
 };
 
 // Packed sign bits [row][k/32] (LSB-first u32 words, row pitch `ldw` words).
@@ -177,14 +195,25 @@ struct OpBits {
   // extra: 16-entry sign table (128 B), then the scale range when SCALED.
   static constexpr int kLut = 128;
   static constexpr int kExtra = kLut + (SCALED ? kMaxScaleK * 2 : 0);
+  // Sign words sit in LDS as [row][WPR] with word w of row r in slot
+  // w ^ swzw(r): the 32 rows one fragment read touches then hit 32 distinct
+  // banks instead of 32 / WPR.
+  __device__ static int swzw(int row) {
+    if constexpr (WPR == 1)
+      return 0;
+    else
+      return (row >> (WPR == 2 ? 4 : WPR == 4 ? 3 : 2)) & (WPR - 1);
+  }
   __device__ void prepare(char* extra, int kbeg, int kend) const {
-    // Entry n (4 weight bits) = the fp16 sign bits of 4 halves: 0x8000 where
-    // bit j of n is 0 (weight -1). Every entry is 8 bytes, so 16 entries cover
+    // Entry n (4 weight bits) = 4 halves: +-1 (the sign from bit j of n, 0 is
+    // -1) for the plain operand, only the sign bits for the scaled one (they
+    // are XORed into the scales). Every entry is 8 bytes, so 16 entries cover
     // the 32 banks of a 128-byte row once: lookups never conflict.
     if (threadIdx.x < 32) {
       const int n = threadIdx.x >> 1, h = threadIdx.x & 1;
       const uint32_t nb = ~(uint32_t)n >> (2 * h);
-      reinterpret_cast<uint32_t*>(extra)[threadIdx.x] = ((nb & 1u) << 15) | ((nb & 2u) << 30);
+      const uint32_t sign = ((nb & 1u) << 15) | ((nb & 2u) << 30);
+      reinterpret_cast<uint32_t*>(extra)[threadIdx.x] = SCALED ? sign : (sign | 0x3C003C00u);
     }
     if constexpr (SCALED) {
       uint16_t* s = reinterpret_cast<uint16_t*>(extra + kLut);
@@ -197,7 +226,7 @@ struct OpBits {
       const int base = (wave * kInst + t) * (kWordsPerWave / kInst);
       if (lane < kWordsPerWave / kInst) {
         const int id = base + lane;
-        const int row = id / WPR, w = id % WPR;
+        const int row = id / WPR, w = (id % WPR) ^ swzw(row);
         const int r = min(row0 + row, rows - 1);
         dma4(p + (long)r * ldw + ((kofs + k0) >> 5) + w, stage + base * 4);
       }
@@ -209,16 +238,51 @@ struct OpBits {
     const int row = base + (lane & 31);
     const int kk = ks16 + 8 * (lane >> 5);  // k offset within the stage
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-    const uint32_t word = reinterpret_cast<const uint32_t*>(stage)[row * WPR + (kk >> 5)];
+    const uint32_t word =
+        reinterpret_cast<const uint32_t*>(stage)[row * WPR + ((kk >> 5) ^ swzw(row))];
     const int sh = kk & 31;
     const u32x2 lo = *reinterpret_cast<const u32x2*>(extra + 8 * ((word >> sh) & 15u));
     const u32x2 hi = *reinterpret_cast<const u32x2*>(extra + 8 * ((word >> (sh + 4)) & 15u));
     u32x4 o = {lo[0], lo[1], hi[0], hi[1]};
+    if constexpr (SCALED) o ^= *reinterpret_cast<const u32x4*>(extra + kLut + 2 * (k0rel + kk));
+    return __builtin_bit_cast(half8, o);
+  }
+  // Phases of the pipelined K loop: pre() reads the lane's 8 sign bits (and
+  // its 8 scales), lut() reads their halves from the table, fix() applies
+  // the signs to the scales (scaled operand only).
+  struct Pre {
+    uint32_t word;  // the sign word holding the lane's 8 weight bits
+    int sh;         // their offset in it
+    u32x4 sc;       // SCALED: the fp16 scales of those 8 inputs
+  };
+  __device__ __forceinline__ Pre pre(const char* stage, const char* extra, int base, int ks16,
+                                     int lane, int k0rel) const {
+    const int row = base + (lane & 31);
+    const int kk = ks16 + 8 * (lane >> 5);
+    Pre p;
+    p.word = reinterpret_cast<const uint32_t*>(stage)[row * WPR + ((kk >> 5) ^ swzw(row))];
+    p.sh = kk & 31;
     if constexpr (SCALED) {
-      o ^= *reinterpret_cast<const u32x4*>(extra + kLut + 2 * (k0rel + kk));
+      p.sc = *reinterpret_cast<const u32x4*>(extra + kLut + 2 * (k0rel + kk));
     } else {
-      o |= 0x3C003C00u;
+      p.sc = u32x4{0u, 0u, 0u, 0u};
     }
+    return p;
+  }
+  struct Raw {
+    u32x4 sign;  // sign bits of the 8 halves
+    u32x4 sc;
+  };
+  __device__ __forceinline__ Raw lut(const Pre& p, const char* extra) const {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const uint32_t bits8 = p.word >> p.sh;
+    const u32x2 lo = *reinterpret_cast<const u32x2*>(extra + 8 * (bits8 & 15u));
+    const u32x2 hi = *reinterpret_cast<const u32x2*>(extra + 8 * ((bits8 >> 4) & 15u));
+    return Raw{u32x4{lo[0], lo[1], hi[0], hi[1]}, p.sc};
+  }
+  __device__ __forceinline__ half8 fix(const Raw& r) const {
+    u32x4 o = r.sign;
+    if constexpr (SCALED) o ^= r.sc;
     return __builtin_bit_cast(half8, o);
   }
 };
@@ -451,19 +515,55 @@ __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const
     if (kt + NS - 1 < nk) issue(kt + NS - 1);
     const char* st = smem + (kt % NS) * STAGE;
     const int k0rel = kt * BK;
+    // Software pipeline over the stage's 16-deep K steps. Step s's MFMAs use
+    // sign patterns read from the table kLut steps earlier, whose LDS words
+    // were read kLut + 1 steps earlier (an fp16 operand is read kLut + 1
+    // steps early). Scheduling barriers keep the LDS reads of later steps
+    // ahead of this step's MFMAs, so the LDS latency hides behind the MFMAs
+    // of the steps in between: at these tile sizes a wave runs alone on its
+    // SIMD, and nothing else would hide it.
+    constexpr int S = BK / 16;
+    constexpr int kLut = S > 3 ? 3 : S - 1;
+    constexpr int kPre = kLut + 1;
+    constexpr int RP = kPre + 1, RR = kLut + 1;  // ring sizes
+    typename OA::Pre pa[RP][TM];
+    typename OB::Pre pb[RP][TN];
+    typename OA::Raw ra[RR][TM];
+    typename OB::Raw rb[RR][TN];
+    auto pre = [&](int s) {
 #pragma unroll
-    for (int ks = 0; ks < BK; ks += 16) {
-      half8 af[TM], bf[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) af[i] = a.frag(st, extra_a, wm * WM + i * 32, ks, lane, k0rel);
+      for (int i = 0; i < TM; ++i)
+        pa[s % RP][i] = a.pre(st, extra_a, wm * WM + i * 32, 16 * s, lane, k0rel);
 #pragma unroll
       for (int j = 0; j < TN; ++j)
-        bf[j] = b.frag(st + OA::kBytes, extra_b, wn * WN + j * 32, ks, lane, k0rel);
+        pb[s % RP][j] = b.pre(st + OA::kBytes, extra_b, wn * WN + j * 32, 16 * s, lane, k0rel);
+    };
+    auto lut = [&](int s) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) ra[s % RR][i] = a.lut(pa[s % RP][i], extra_a);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) rb[s % RR][j] = b.lut(pb[s % RP][j], extra_b);
+    };
+#pragma unroll
+    for (int t = 0; t < kPre && t < S; ++t) pre(t);
+#pragma unroll
+    for (int t = 0; t < kLut; ++t) lut(t);
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      if (s + kPre < S) pre(s + kPre);
+      if (s + kLut < S) lut(s + kLut);
+      __builtin_amdgcn_sched_barrier(0);
+      half8 af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = a.fix(ra[s % RR][i]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bf[j] = b.fix(rb[s % RR][j]);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   wait_barrier<0>();  // every wave is done reading the ring
@@ -581,7 +681,10 @@ struct LdsDeep {
 struct LdsBig {
   static constexpr int bm = 128, bn = 128, bk = 32, ns = 4;
 };
-// Per-call-site choice (with_lds): kAuto = LdsMid / LdsShort by K; kDeep =
+
+constexpr long kBigAutoBlocks = 512;
+// Per-call-site choice (with_lds): kAuto = LdsBig for large products, else
+// LdsMid / LdsShort by K; kDeep =
 // the four-stage BK 128 ring for launches of one block per CU whose operands
 // come from HBM; kBig = 128x128 tiles.
 enum class LdsPolicy { kAuto, kDeep, kBig };
@@ -603,6 +706,15 @@ bool with_lds(long M, long N, long K, int splits, hipError_t* err, F&& f,
     return true;
   }
   if (policy == LdsPolicy::kBig && K % LdsBig::bk == 0 && M % 128 == 0 && N % 128 == 0) {
+    *err = f(LdsBig{});
+    return true;
+  }
+
+  // Large products (two or more 128x128 tiles per CU): the 128x128 tile
+  // streams half the operand bytes per MFMA of a 64x64 one (measured on the
+  // config-5 step: 128 -> 115 ms; config 4 has no product this large).
+  if (K % LdsBig::bk == 0 && M % 128 == 0 && N % 128 == 0 &&
+      (M / 128) * (N / 128) * splits >= kBigAutoBlocks) {
     *err = f(LdsBig{});
     return true;
   }

@@ -139,8 +139,10 @@ struct ullis_hip_heron {
   int probe = 0;
   int probe_used = 0;
   std::vector<hipEvent_t> probe_events;
-  unsigned long long* probe_stamps = nullptr;  // device [kProbeMax][kStampCap][2], lazily
+  unsigned long long* probe_stamps = nullptr;  // device [kStampTotal][2], lazily
   std::vector<long> probe_blocks;              // per probed launch: stamped blocks, 0 = events
+  std::vector<long> probe_offset;              // per probed launch: first stamp slot
+  long stamp_used = 0;                         // stamp slots taken since the probe was armed
   double wall_khz = 0.0;                       // device wall-clock rate (s_memrealtime)
 
   template <class T>
@@ -185,7 +187,9 @@ bool bind_packed(ullis_hip_heron* h, const std::string& p, long out, long in, bo
   } while (0)
 
 constexpr int kProbeMax = 512;
-constexpr long kStampCap = 8192;  // blocks per stamped launch (larger grids use events)
+// (start, end) slots for every workgroup of the stamped launches of one probe
+// pass; a launch that no longer fits is timed by events instead
+constexpr long kStampTotal = 1L << 22;
 
 __global__ void probe_stamps_clear_kernel(unsigned long long* st, long n) {
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -203,8 +207,8 @@ __global__ void probe_stamps_clear_kernel(unsigned long long* st, long n) {
     if (on_) {                                                                     \
       lp_.start = h->probe_events[2 * h->probe_used];                              \
       lp_.stop = h->probe_events[2 * h->probe_used + 1];                           \
-      lp_.stamps = h->probe_stamps + 2 * kStampCap * h->probe_used;                \
-      lp_.stamp_cap = kStampCap;                                                   \
+      lp_.stamps = h->probe_stamps + 2 * h->stamp_used;                            \
+      lp_.stamp_cap = kStampTotal - h->stamp_used;                                 \
       t_launch_probe = &lp_;                                                       \
     }                                                                              \
     const int rc_ = c->hip((expr), (what));                                        \
@@ -214,6 +218,8 @@ __global__ void probe_stamps_clear_kernel(unsigned long long* st, long n) {
     if (on_) {                                                                     \
       if (!consumed_) return c->fail(ULLIS_HIP_ERR_RUNTIME, "probe: no kernel launched"); \
       h->probe_blocks[h->probe_used] = lp_.used_stamps ? lp_.blocks : 0;           \
+      h->probe_offset[h->probe_used] = h->stamp_used;                              \
+      if (lp_.used_stamps) h->stamp_used += lp_.blocks;                            \
       ++h->probe_used;                                                             \
     }                                                                              \
   } while (0)
@@ -563,6 +569,7 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
     }
   }
   h->probe_blocks.assign(kProbeMax, 0);
+  h->probe_offset.assign(kProbeMax, 0);
   {
     int dev = 0, khz = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -618,9 +625,10 @@ int ullis_hip_heron_probe(ullis_hip_heron* h, int probe_id) {
   if (!h || probe_id < 0 || probe_id >= ULLIS_HIP_PROBE_COUNT) return ULLIS_HIP_ERR_INVALID;
   h->probe = probe_id;
   h->probe_used = 0;
+  h->stamp_used = 0;
   if (probe_id != ULLIS_HIP_PROBE_NONE) {
     ullis_hip_ctx* c = h->ctx;
-    const long n = 2 * kStampCap * kProbeMax;
+    const long n = 2 * kStampTotal;
     if (!h->probe_stamps)
       STEP(hipMalloc(&h->probe_stamps, sizeof(unsigned long long) * n), "probe stamps alloc");
     launch(probe_stamps_clear_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, c->stream,
@@ -640,7 +648,7 @@ int ullis_hip_heron_probe_read(ullis_hip_heron* h, float* total_ms, int* launche
   for (int i = 0; i < h->probe_used; ++i) {
     if (const long nb = h->probe_blocks[i]) {
       st.resize(2 * (size_t)nb);
-      STEP(hipMemcpy(st.data(), h->probe_stamps + 2 * kStampCap * i,
+      STEP(hipMemcpy(st.data(), h->probe_stamps + 2 * h->probe_offset[i],
                      sizeof(unsigned long long) * st.size(), hipMemcpyDeviceToHost),
            "probe stamps");
       unsigned long long t0 = ~0ull, t1 = 0;
@@ -662,6 +670,7 @@ int ullis_hip_heron_probe_read(ullis_hip_heron* h, float* total_ms, int* launche
   *total_ms = (float)sum;
   *launches = h->probe_used;
   h->probe_used = 0;
+  h->stamp_used = 0;
   return 0;
 }
 
