@@ -382,3 +382,42 @@ def test_fp16_few_rows_matches_oracle(rt, rows, in_f, out_f):
     w = f16(rng.normal(0, 0.05, out_f * in_f))
     want = o.fp16_forward(h2f32(x16), rows, in_f, out_f, w)
     assert rel(rt.fp16_linear(x16, w, rows, in_f, out_f), want) <= GEMV_REL
+
+
+# ------------------------------------------ tile configurations of large products
+@pytest.mark.parametrize("rows,in_f,out_f,chunk", [
+    (8192, 512, 8192, 1024),   # 2048 128x256 tiles: LdsHuge
+    (4096, 512, 2048, 1024),   # 512 128x128 tiles: LdsBig
+])
+def test_large_products_match_small_tile_path(rt, rows, in_f, out_f, chunk):
+    """A large product takes bigger tiles; every output element is still the
+    same MFMA sequence over K, so the result equals the one computed in row
+    chunks small enough for 64x64 tiles, bit for bit; and a row sample
+    matches the oracle."""
+    rng = np.random.default_rng(rows + out_f)
+    x16, bits, scale, b = rand_case(rng, rows, in_f, out_f)
+    whole = rt.binary_linear(x16, bits, scale, b, rows, in_f, out_f)
+    parts = np.concatenate([
+        rt.binary_linear(x16[r0 * in_f:(r0 + chunk) * in_f], bits, scale, b, chunk, in_f, out_f)
+        for r0 in range(0, rows, chunk)])
+    np.testing.assert_array_equal(whole.view(np.uint32), parts.view(np.uint32))
+    sample = np.r_[0:16, rows - 16:rows]
+    xs = h2f32(x16).reshape(rows, in_f)[sample]
+    want = o.packed_forward(xs.ravel(), len(sample), in_f, out_f, bits, scale, b)
+    assert rel(whole.reshape(rows, out_f)[sample].ravel(), want) <= REL
+
+
+def test_large_backward_matches_small_tile_path(rt):
+    # dX of 8192 x 1024 from K 4096 takes 128x128 tiles; in 1024-row chunks 64x64
+    rows, in_f, out_f, chunk = 8192, 1024, 4096, 1024
+    rng = np.random.default_rng(77)
+    x16, bits, scale, _ = rand_case(rng, rows, in_f, out_f, bias=False)
+    gy = (rng.standard_normal(rows * out_f) * 1e-2).astype(np.float32)
+    whole = rt.binary_linear_backward(x16, gy, bits, scale, False, rows, in_f, out_f)
+    gx = np.concatenate([
+        rt.binary_linear_backward(x16[r0 * in_f:(r0 + chunk) * in_f],
+                                  gy[r0 * out_f:(r0 + chunk) * out_f], bits, scale, False, chunk,
+                                  in_f, out_f)["input_gradient"]
+        for r0 in range(0, rows, chunk)])
+    # the chunks scale their fp16 gradient operand by their own max |gy|
+    assert rel(whole["input_gradient"], gx) <= 1e-5

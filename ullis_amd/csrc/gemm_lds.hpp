@@ -452,11 +452,22 @@ inline constexpr bool kHasSplit = false;
 template <class E>
 inline constexpr bool kHasSplit<E, decltype(std::declval<E&>().set_split(0))> = true;
 
+// Ring depth of a config for an operand pair: the config's stage count, cut
+// to what fits in kRingCap bytes (a deep ring of sign-bit stages is cheap; of
+// fp16 stages it is not).
+constexpr int kRingCap = 128 * 1024;
+template <int NS, class OA, class OB>
+constexpr int ring_ns() {
+  constexpr int STAGE = OA::kBytes + OB::kBytes;
+  return NS * STAGE <= kRingCap ? NS : (kRingCap / STAGE < 2 ? 2 : kRingCap / STAGE);
+}
+
 // LDS bytes of one block of the streamed-LDS GEMM: the stage ring (which the
 // epilogue reuses) and the operands' extra tables.
-template <int BM, int BN, int BK, int NS, class OA, class OB>
+template <int BM, int BN, int BK, int NS_CFG, class OA, class OB>
 constexpr int lds_ring_bytes() {
   constexpr int STAGE = OA::kBytes + OB::kBytes;
+  constexpr int NS = ring_ns<NS_CFG, OA, OB>();
   return NS * STAGE > 4 * kBufFloats * 4 ? NS * STAGE : 4 * kBufFloats * 4;
 }
 template <int BM, int BN, int BK, int NS, class OA, class OB>
@@ -466,17 +477,18 @@ constexpr int lds_smem_bytes() {
 
 // One output tile (bid: tile index, kz: K split) of C = A . B^T in the block's
 // LDS (smem: lds_smem_bytes, 1024-byte aligned).
-template <int BM, int BN, int BK, int NS, class OA, class OB, class Epi>
+template <int BM, int BN, int BK, int NS_CFG, class OA, class OB, class Epi>
 __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const OA& a,
                                               const OB& b, Epi& epi, int M, int N, int K,
                                               int k_split, const TileMap& map) {
+  constexpr int NS = ring_ns<NS_CFG, OA, OB>();
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int STAGE = OA::kBytes + OB::kBytes;
   constexpr int IPS = OA::kInst + OB::kInst;  // loads per wave per stage
   static_assert(TM >= 1 && TN >= 1, "tile too small");
   static_assert(NS >= 2 && IPS * (NS - 2) < 64, "pipeline depth");
-  constexpr int RING = lds_ring_bytes<BM, BN, BK, NS, OA, OB>();
+  constexpr int RING = lds_ring_bytes<BM, BN, BK, NS_CFG, OA, OB>();
   char* extra_a = smem + RING;
   char* extra_b = extra_a + OA::kExtra;
 
@@ -681,8 +693,12 @@ struct LdsDeep {
 struct LdsBig {
   static constexpr int bm = 128, bn = 128, bk = 32, ns = 4;
 };
+struct LdsHuge {
+  static constexpr int bm = 128, bn = 256, bk = 32, ns = 4;
+};
 
 constexpr long kBigAutoBlocks = 512;
+constexpr long kHugeAutoBlocks = 1024;
 // Per-call-site choice (with_lds): kAuto = LdsBig for large products, else
 // LdsMid / LdsShort by K; kDeep =
 // the four-stage BK 128 ring for launches of one block per CU whose operands
@@ -713,6 +729,14 @@ bool with_lds(long M, long N, long K, int splits, hipError_t* err, F&& f,
   // Large products (two or more 128x128 tiles per CU): the 128x128 tile
   // streams half the operand bytes per MFMA of a 64x64 one (measured on the
   // config-5 step: 128 -> 115 ms; config 4 has no product this large).
+  // Very large products (four or more 128x256 tiles per CU): 128x256 tiles,
+  // eight MFMAs per fragment step per wave (config-5 step 115 -> 111.5 ms;
+  // deeper rings for them measured slower: fewer blocks fit per CU).
+  if (K % LdsHuge::bk == 0 && M % 128 == 0 && N % 256 == 0 &&
+      (M / 128) * (N / 256) * splits >= kHugeAutoBlocks) {
+    *err = f(LdsHuge{});
+    return true;
+  }
   if (K % LdsBig::bk == 0 && M % 128 == 0 && N % 128 == 0 &&
       (M / 128) * (N / 128) * splits >= kBigAutoBlocks) {
     *err = f(LdsBig{});
