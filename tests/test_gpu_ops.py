@@ -421,3 +421,19 @@ def test_large_backward_matches_small_tile_path(rt):
         for r0 in range(0, rows, chunk)])
     # the chunks scale their fp16 gradient operand by their own max |gy|
     assert rel(whole["input_gradient"], gx) <= 1e-5
+
+
+def test_large_fp16_product_matches_small_tile_path(rt):
+    # 16384 x 4096 from K 512: 2048 128x256 tiles; 1024-row chunks take the
+    # 64x64 four-stage ring; the K order of the MFMAs is the same in both
+    rows, in_f, out_f, chunk = 16384, 512, 4096, 1024
+    rng = np.random.default_rng(91)
+    x16 = f16(rng.standard_normal(rows * in_f))
+    w = f16(rng.normal(0, 0.05, out_f * in_f))
+    whole = rt.fp16_linear(x16, w, rows, in_f, out_f)
+    parts = np.concatenate([rt.fp16_linear(x16[r0 * in_f:(r0 + chunk) * in_f], w, chunk, in_f, out_f)
+                            for r0 in range(0, rows, chunk)])
+    np.testing.assert_array_equal(whole.view(np.uint32), parts.view(np.uint32))
+    sample = np.r_[0:8, rows - 8:rows]
+    want = o.fp16_forward(h2f32(x16).reshape(rows, in_f)[sample].ravel(), len(sample), in_f, out_f, w)
+    assert rel(whole.reshape(rows, out_f)[sample].ravel(), want) <= REL

@@ -717,21 +717,17 @@ template <class F>
 bool with_lds(long M, long N, long K, int splits, hipError_t* err, F&& f,
               LdsPolicy policy = LdsPolicy::kAuto) {
   if (M <= 0 || N <= 0 || K <= 0 || splits < 1) return false;
-  if (policy == LdsPolicy::kDeep && K % LdsDeep::bk == 0) {
-    *err = f(LdsDeep{});
-    return true;
-  }
   if (policy == LdsPolicy::kBig && K % LdsBig::bk == 0 && M % 128 == 0 && N % 128 == 0) {
     *err = f(LdsBig{});
     return true;
   }
-
-  // Large products (two or more 128x128 tiles per CU): the 128x128 tile
-  // streams half the operand bytes per MFMA of a 64x64 one (measured on the
-  // config-5 step: 128 -> 115 ms; config 4 has no product this large).
-  // Very large products (four or more 128x256 tiles per CU): 128x256 tiles,
-  // eight MFMAs per fragment step per wave (config-5 step 115 -> 111.5 ms;
-  // deeper rings for them measured slower: fewer blocks fit per CU).
+  // Very large products (four or more 128x256 tiles per CU) take 128x256
+  // tiles, eight MFMAs per fragment step per wave; large ones (two or more
+  // 128x128 tiles per CU) 128x128 tiles, half the operand bytes per MFMA of
+  // a 64x64 tile. Both before the kDeep policy, which is tuned for config
+  // 4's shapes (config-5 value forward 708 -> 415 us); the value dX keeps
+  // its 128x128 tiles (kBig: 128x256 measured 1.45x slower for it). Deeper
+  // rings for the 128x256 tiles measured slower: fewer blocks fit per CU.
   if (K % LdsHuge::bk == 0 && M % 128 == 0 && N % 256 == 0 &&
       (M / 128) * (N / 256) * splits >= kHugeAutoBlocks) {
     *err = f(LdsHuge{});
@@ -740,6 +736,10 @@ bool with_lds(long M, long N, long K, int splits, hipError_t* err, F&& f,
   if (K % LdsBig::bk == 0 && M % 128 == 0 && N % 128 == 0 &&
       (M / 128) * (N / 128) * splits >= kBigAutoBlocks) {
     *err = f(LdsBig{});
+    return true;
+  }
+  if (policy == LdsPolicy::kDeep && K % LdsDeep::bk == 0) {
+    *err = f(LdsDeep{});
     return true;
   }
   if (K % LdsMid::bk == 0) {
