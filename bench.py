@@ -231,6 +231,8 @@ def main() -> int:
     ap.add_argument("--stress", action="store_true",
                     help="instead of the bench line, run config 5 (the MFMA stress profile) "
                          "and print its step time and per-kernel MFMA rates")
+    ap.add_argument("--graph", type=int, default=0,
+                    help="1: replay each step's launches from a captured HIP graph")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after the timed region, run one plain device copy kernel of this many "
                          "MiB (read + write) so HBM counters can be scaled against known bytes")
@@ -256,6 +258,7 @@ def main() -> int:
     trainer = HeronTrainer(rt, shape)
     arena = heron_arena(trainer.layout, trainer.arena_bytes, shape.dims(), seed=7)
     trainer.upload_arena(arena)
+    trainer.set_graph(bool(args.graph))
     x, labels, idx = step_inputs(shape.rows, c["d_model"], c["vocab"], c["n_layers"], c["batch"],
                                  c["time"], seed=7)
     dl, di = rt.put(labels), rt.put(idx)

@@ -268,6 +268,15 @@ int ullis_hip_heron_refresh_derived(ullis_hip_heron* h);
 int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels,
                          uint32_t ignore_id, float learning_rate, const uint8_t* rosa_idx,
                          float* g_emb, float* row_loss, float* stats4, uint32_t* qkv_bits);
+/*
+ * Step graph (no counterpart in the reference, whose Metal backend encodes
+ * command buffers per step): with enable != 0, ullis_hip_heron_step captures
+ * its launches on both streams into a HIP graph the first time and replays the
+ * graph while it is called with the same pointers, ignore_id and
+ * learning_rate (other arguments capture again). Probed steps run eagerly.
+ * enable = 0 drops the graph.
+ */
+int ullis_hip_heron_set_graph(ullis_hip_heron* h, int enable);
 
 /*
  * Kernel probe, the device-side counterpart of the reference's per-phase

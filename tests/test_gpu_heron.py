@@ -186,6 +186,42 @@ def test_full_heron_step_properties(rt):
                                           err_msg=name)
 
 
+def test_graph_replay_matches_eager_steps(rt):
+    """ullis_hip_heron_set_graph: steps replayed from the captured graph are
+    bit-identical to eager steps, a new learning rate captures again, and
+    turning the graph off returns to eager launches."""
+    shape = HeronShape(d_model=256, n_layers=3, dim_ffn=1024, vocab=2048, batch=2, time=256)
+    trainer = HeronTrainer(rt, shape)
+    arena = heron_arena(trainer.layout, trainer.arena_bytes, shape.dims(), seed=11)
+    x, labels, idx = step_inputs(shape.rows, 256, 2048, 3, 2, 256, seed=11)
+    dx, dl, di = rt.put(x), rt.put(labels), rt.put(idx)
+    g = rt.zeros(np.float32, shape.rows * 256)
+    rl = rt.zeros(np.float32, shape.rows)
+    st = rt.zeros(np.float32, 4)
+    lrs = (0.01, 0.01, 0.01, 0.02, 0.02)
+
+    def run(graph):
+        trainer.upload_arena(arena)
+        trainer.set_graph(graph)
+        outs = []
+        for i, lr in enumerate(lrs):
+            if graph and i == len(lrs) - 1:
+                trainer.set_graph(False)
+            trainer.step(dx, dl, NO_IGNORE, lr, di, g, rl, st)
+            rt.sync()
+            outs.append((trainer.download_arena(), g.download(np.float32),
+                         rl.download(np.float32), st.download(np.float32)))
+        return outs
+
+    eager, graph = run(False), run(True)
+    for i, (e, r) in enumerate(zip(eager, graph)):
+        np.testing.assert_array_equal(e[0], r[0], err_msg=f"arena after step {i}")
+        for a, b in zip(e[1:], r[1:]):
+            np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32),
+                                          err_msg=f"step {i}")
+    assert not np.array_equal(eager[0][0], eager[1][0])  # the steps did move the state
+
+
 def test_step_from_tokens_gathers_steps_and_scatters(rt):
     """HeronTrainer.step_tokens (gather, step, scatter-SGD on the device)
     against the same three stages run one at a time: the oracle's gather,

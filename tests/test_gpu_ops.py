@@ -424,7 +424,7 @@ def test_large_backward_matches_small_tile_path(rt):
 
 
 def test_large_fp16_product_matches_small_tile_path(rt):
-    # 16384 x 4096 from K 512: 2048 128x256 tiles; 1024-row chunks take the
+    # 16384 x 4096 from K 512: 1024 256x256 tiles; 1024-row chunks take the
     # 64x64 four-stage ring; the K order of the MFMAs is the same in both
     rows, in_f, out_f, chunk = 16384, 512, 4096, 1024
     rng = np.random.default_rng(91)

@@ -696,14 +696,20 @@ struct LdsBig {
 struct LdsHuge {
   static constexpr int bm = 128, bn = 256, bk = 32, ns = 4;
 };
+struct LdsGiant {
+  static constexpr int bm = 256, bn = 256, bk = 32, ns = 4;
+};
 
 constexpr long kBigAutoBlocks = 512;
 constexpr long kHugeAutoBlocks = 1024;
+constexpr long kGiantAutoBlocks = 512;
 // Per-call-site choice (with_lds): kAuto = LdsBig for large products, else
 // LdsMid / LdsShort by K; kDeep =
 // the four-stage BK 128 ring for launches of one block per CU whose operands
-// come from HBM; kBig = 128x128 tiles.
-enum class LdsPolicy { kAuto, kDeep, kBig };
+// come from HBM; kBig = 128x128 tiles; kDeepGiant = kDeep, with 256x256
+// tiles for very large products (two k-contiguous fp16 operands only: with
+// a sign-bit or transposed operand those tiles measured slower than 128x256).
+enum class LdsPolicy { kAuto, kDeep, kBig, kDeepGiant };
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool mk_ok(const void* p, long ld) { return p && aligned16(p) && ld % 8 == 0; }
@@ -728,6 +734,13 @@ bool with_lds(long M, long N, long K, int splits, hipError_t* err, F&& f,
   // 4's shapes (config-5 value forward 708 -> 415 us); the value dX keeps
   // its 128x128 tiles (kBig: 128x256 measured 1.45x slower for it). Deeper
   // rings for the 128x256 tiles measured slower: fewer blocks fit per CU.
+  // 256x256 tiles: 16 MFMAs per fragment step per wave (config-5 value
+  // forward 418 -> 335 us).
+  if (policy == LdsPolicy::kDeepGiant && K % LdsGiant::bk == 0 && M % 256 == 0 &&
+      N % 256 == 0 && (M / 256) * (N / 256) * splits >= kGiantAutoBlocks) {
+    *err = f(LdsGiant{});
+    return true;
+  }
   if (K % LdsHuge::bk == 0 && M % 128 == 0 && N % 256 == 0 &&
       (M / 128) * (N / 256) * splits >= kHugeAutoBlocks) {
     *err = f(LdsHuge{});
@@ -738,7 +751,7 @@ bool with_lds(long M, long N, long K, int splits, hipError_t* err, F&& f,
     *err = f(LdsBig{});
     return true;
   }
-  if (policy == LdsPolicy::kDeep && K % LdsDeep::bk == 0) {
+  if ((policy == LdsPolicy::kDeep || policy == LdsPolicy::kDeepGiant) && K % LdsDeep::bk == 0) {
     *err = f(LdsDeep{});
     return true;
   }

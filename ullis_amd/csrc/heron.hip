@@ -144,6 +144,21 @@ struct ullis_hip_heron {
   std::vector<long> probe_offset;              // per probed launch: first stamp slot
   long stamp_used = 0;                         // stamp slots taken since the probe was armed
   double wall_khz = 0.0;                       // device wall-clock rate (s_memrealtime)
+  // step graph (ullis_hip_heron_set_graph): the launches of one step on both
+  // streams, captured once and replayed while the step's arguments repeat
+  struct StepArgs {
+    const void* p[7];
+    uint32_t ignore_id;
+    float lr;
+    bool operator==(const StepArgs& o) const {
+      for (int i = 0; i < 7; ++i)
+        if (p[i] != o.p[i]) return false;
+      return ignore_id == o.ignore_id && lr == o.lr;
+    }
+  };
+  bool graph_on = false;
+  hipGraphExec_t graph_exec = nullptr;
+  StepArgs graph_args{};
 
   template <class T>
   T* tensor(const std::string& name) {
@@ -611,6 +626,7 @@ void ullis_hip_heron_destroy(ullis_hip_heron* h) {
   if (h->act) (void)hipFree(h->act);
   if (h->job_mem) (void)hipFree(h->job_mem);
   if (h->probe_stamps) (void)hipFree(h->probe_stamps);
+  if (h->graph_exec) (void)hipGraphExecDestroy(h->graph_exec);
   delete h;
 }
 
@@ -686,16 +702,16 @@ int ullis_hip_heron_refresh_derived(ullis_hip_heron* h) {
   return 0;
 }
 
-int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels,
-                         uint32_t ignore_id, float lr, const uint8_t* rosa_idx, float* g_emb,
-                         float* row_loss, float* stats4, uint32_t* qkv_bits) {
-  if (!h) return ULLIS_HIP_ERR_INVALID;
+}  // extern "C"
+
+namespace {
+
+// Every launch of one train step, on the context stream and the second
+// stream (arguments checked by ullis_hip_heron_step).
+int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels,
+                  uint32_t ignore_id, float lr, const uint8_t* rosa_idx, float* g_emb,
+                  float* row_loss, float* stats4, uint32_t* qkv_bits) {
   ullis_hip_ctx* c = h->ctx;
-  if (!x_emb || !labels || !rosa_idx || !g_emb)
-    return c->fail(ULLIS_HIP_ERR_INVALID, "heron step needs x_emb, labels, rosa_idx and g_emb");
-  if (!(lr > 0.0f) || !__builtin_isfinite(lr))
-    return c->fail(ULLIS_HIP_ERR_INVALID,
-                   "train step requires a positive learning rate and time >= 2");
   hipStream_t s = c->stream;
   const long R = h->rows, D = h->D, F = h->F, L = h->L, T = h->time, B = h->batch;
   const long nd = R * D, nf = R * F;
@@ -906,6 +922,66 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
     if (int rc = run_update_seg(h, s, (int)L + 1, lr)) return rc;
   for (const Packed* k : h->trans_generic)
     STEP(transpose_bits(s, k->bits, k->out, k->in, k->bits_t), "bits_t");
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ullis_hip_heron_set_graph(ullis_hip_heron* h, int enable) {
+  if (!h) return ULLIS_HIP_ERR_INVALID;
+  ullis_hip_ctx* c = h->ctx;
+  h->graph_on = enable != 0;
+  if (h->graph_exec) {
+    STEP(hipStreamSynchronize(c->stream), "graph sync");
+    STEP(hipGraphExecDestroy(h->graph_exec), "graph destroy");
+    h->graph_exec = nullptr;
+  }
+  return 0;
+}
+
+int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels,
+                         uint32_t ignore_id, float lr, const uint8_t* rosa_idx, float* g_emb,
+                         float* row_loss, float* stats4, uint32_t* qkv_bits) {
+  if (!h) return ULLIS_HIP_ERR_INVALID;
+  ullis_hip_ctx* c = h->ctx;
+  if (!x_emb || !labels || !rosa_idx || !g_emb)
+    return c->fail(ULLIS_HIP_ERR_INVALID, "heron step needs x_emb, labels, rosa_idx and g_emb");
+  if (!(lr > 0.0f) || !__builtin_isfinite(lr))
+    return c->fail(ULLIS_HIP_ERR_INVALID,
+                   "train step requires a positive learning rate and time >= 2");
+  // probed steps run eagerly: the probe times individual launches
+  if (!h->graph_on || h->probe != ULLIS_HIP_PROBE_NONE || t_launch_probe)
+    return step_launches(h, x_emb, labels, ignore_id, lr, rosa_idx, g_emb, row_loss, stats4,
+                         qkv_bits);
+  const ullis_hip_heron::StepArgs args{
+      {x_emb, labels, rosa_idx, g_emb, row_loss, stats4, qkv_bits}, ignore_id, lr};
+  hipStream_t s = c->stream;
+  if (!h->graph_exec || !(args == h->graph_args)) {
+    if (h->graph_exec) {
+      STEP(hipGraphExecDestroy(h->graph_exec), "graph destroy");
+      h->graph_exec = nullptr;
+    }
+    STEP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "graph capture");
+    const int rc = step_launches(h, x_emb, labels, ignore_id, lr, rosa_idx, g_emb, row_loss,
+                                 stats4, qkv_bits);
+    hipGraph_t g = nullptr;
+    const hipError_t end = hipStreamEndCapture(s, &g);
+    if (rc) {
+      if (g) (void)hipGraphDestroy(g);
+      return rc;
+    }
+    if (int rc2 = c->hip(end, "graph capture end")) return rc2;
+    const hipError_t inst = hipGraphInstantiate(&h->graph_exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (int rc2 = c->hip(inst, "graph instantiate")) {
+      h->graph_exec = nullptr;
+      return rc2;
+    }
+    h->graph_args = args;
+  }
+  STEP(hipGraphLaunch(h->graph_exec, s), "graph launch");
   return 0;
 }
 

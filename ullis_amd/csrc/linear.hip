@@ -676,7 +676,7 @@ hipError_t fp16_forward(hipStream_t s, const void* x, int x_dtype, long rows, lo
         return lds::launch_lds<T>(s, a, b, epi, rows, out, in, 1);
         // one block per CU at heron sizes, reading an operand fresh from HBM:
         // the four-stage ring (measured 18.9 -> 15.2 us in the step)
-      }, lds::LdsPolicy::kDeep))
+      }, lds::LdsPolicy::kDeepGiant))
     return err;
   return with_tile(rows, out, [&](auto t) {
     using T = decltype(t);

@@ -548,6 +548,12 @@ class HeronTrainer:
         return {"name": label, "probe": name, "bound": bound, "work": work,
                 "total_ms": total.value, "count": count.value}
 
+    def set_graph(self, enable: bool = True):
+        """Replay the step's launches from a captured HIP graph while the
+        step's pointers, ignore id and learning rate repeat."""
+        self.rt._check(self.rt.lib.ullis_hip_heron_set_graph(self.h, 1 if enable else 0),
+                       "set graph")
+
     def upload_arena(self, arena: np.ndarray):
         a = np.ascontiguousarray(arena, dtype=np.uint8)
         assert a.nbytes == self.arena_bytes
