@@ -129,6 +129,82 @@ def decode_gemv(rt, reps: int) -> None:
                               "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}), flush=True)
 
 
+# LayerNorm launches timed alone (no other stream sharing the CUs): config 4's
+# [2048, 512] and config 5's [32768, 1024] activations.
+LN_ISOLATED = ((2048, 512), (32768, 1024))
+
+
+def layer_norm_isolated(rt, reps: int) -> None:
+    """One JSON line per LayerNorm launch and shape: the row kernel's own time
+    (ullis_hip_time_next_launch, averaged over reps), its algorithmic HBM bytes
+    (fp32 x in, fp16 y out forward; fp32 x, gy in and fp32 gx out backward)
+    against the HBM peak, and a device copy of the same bytes (read + write)
+    timed back to back with events as the floor a launch of that size meets.
+    Launches cycle over enough buffer sets (>= 512 MiB) that their operands
+    come from HBM, not from the 256 MB last-level cache."""
+    import ctypes as C
+
+    lib, ctx = rt.lib, rt.ctx
+    rng = np.random.default_rng(3)
+    for rows, ch in LN_ISOLATED:
+        n = rows * ch
+        nsets = max(2, -(-(512 << 20) // (14 * n)))
+        w = rt.put(np.ones(ch, np.float16).view(np.uint16))
+        b = rt.put(np.zeros(ch, np.float16).view(np.uint16))
+        gw, gb = rt.buffer(4 * ch), rt.buffer(4 * ch)
+        xs = [rt.put(rng.standard_normal(n).astype(np.float32)) for _ in range(nsets)]
+        gys = [rt.put(rng.standard_normal(n).astype(np.float32)) for _ in range(nsets)]
+        y16s = [rt.buffer(2 * n) for _ in range(nsets)]
+        gxs = [rt.buffer(4 * n) for _ in range(nsets)]
+        # copy-floor operands: up to the backward's 6n bytes each way
+        srcs = [rt.buffer(6 * n) for _ in range(nsets)]
+        dsts = [rt.buffer(6 * n) for _ in range(nsets)]
+
+        def fwd(k):
+            return lib.ullis_hip_layer_norm(ctx, xs[k].ptr, w.ptr, b.ptr, rows, ch, None,
+                                            y16s[k].ptr)
+
+        def bwd(k):
+            return lib.ullis_hip_layer_norm_backward(ctx, xs[k].ptr, gys[k].ptr, w.ptr, rows, ch,
+                                                     gxs[k].ptr, gw.ptr, gb.ptr)
+
+        for name, nbytes, call in (("ln_forward", 6.0 * n, fwd),
+                                   ("ln_backward_rows", 12.0 * n, bwd)):
+            total = 0.0
+            for i in range(reps + 3):
+                rt._check(lib.ullis_hip_time_next_launch(ctx, 2, 3), "arm")
+                rt._check(call(i % nsets), name)
+                ms = C.c_float()
+                rt._check(lib.ullis_hip_event_elapsed_ms(ctx, 2, 3, C.byref(ms)), "elapsed")
+                if i >= 3:
+                    total += ms.value
+            us = total / reps * 1e3
+            # the same bytes moved by a device copy (half read, half written)
+            half = int(nbytes // 2) // 16 * 16
+            assert half <= 6 * n
+            for k in range(3):
+                rt._check(lib.ullis_hip_copy(ctx, dsts[k % nsets].ptr, srcs[k % nsets].ptr, half),
+                          "copy")
+            rt.sync()
+            rt._check(lib.ullis_hip_event_record(ctx, 0), "event")
+            for k in range(reps):
+                rt._check(lib.ullis_hip_copy(ctx, dsts[k % nsets].ptr, srcs[k % nsets].ptr, half),
+                          "copy")
+            rt._check(lib.ullis_hip_event_record(ctx, 1), "event")
+            rt.sync()
+            ms = C.c_float()
+            rt._check(lib.ullis_hip_event_elapsed_ms(ctx, 0, 1, C.byref(ms)), "elapsed")
+            copy_us = ms.value / reps * 1e3
+            gbs = nbytes / (us * 1e-6) / 1e9
+            print(json.dumps({"layer_norm": name, "rows": rows, "ch": ch, "avg_us": round(us, 2),
+                              "algorithmic_bytes": int(nbytes), "achieved_gbs": round(gbs, 1),
+                              "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "buffer_sets": nsets,
+                              "same_bytes_copy_us": round(copy_us, 2),
+                              "copy_gbs": round(2 * half / (copy_us * 1e-6) / 1e9, 1)}),
+                  flush=True)
+        del xs, gys, y16s, gxs, srcs, dsts
+
+
 # Config 5, the stress profile of the MFMA path (a parity-test case, not the
 # bench line): D=1024, L=24, T=4096, batch 8, vocab 32768, key 1024->4096.
 STRESS = dict(d_model=1024, n_layers=24, dim_ffn=4096, vocab=32768, batch=8, time=4096)
@@ -228,6 +304,9 @@ def main() -> int:
     ap.add_argument("--decode-gemv", type=int, default=0, metavar="REPS",
                     help="instead of the train step, time the few-row (T = 1 decode) forward "
                          "products over REPS launches each and print one JSON line per product")
+    ap.add_argument("--ln-isolated", type=int, default=0, metavar="REPS",
+                    help="instead of the train step, time the LayerNorm row kernels alone over "
+                         "REPS launches each, beside a device copy of the same bytes")
     ap.add_argument("--stress", action="store_true",
                     help="instead of the bench line, run config 5 (the MFMA stress profile) "
                          "and print its step time and per-kernel MFMA rates")
@@ -254,6 +333,9 @@ def main() -> int:
         return 0
     if args.stress:
         stress_profile(rt, args.steps, args.warmup)
+        return 0
+    if args.ln_isolated > 0:
+        layer_norm_isolated(rt, args.ln_isolated)
         return 0
     trainer = HeronTrainer(rt, shape)
     arena = heron_arena(trainer.layout, trainer.arena_bytes, shape.dims(), seed=7)
