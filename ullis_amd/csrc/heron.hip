@@ -960,6 +960,8 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
   hipStream_t s = c->stream;
   if (!h->graph_exec || !(args == h->graph_args)) {
     if (h->graph_exec) {
+      // the previous graph may still be running
+      STEP(hipStreamSynchronize(s), "graph sync");
       STEP(hipGraphExecDestroy(h->graph_exec), "graph destroy");
       h->graph_exec = nullptr;
     }
