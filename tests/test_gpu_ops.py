@@ -386,7 +386,8 @@ def test_fp16_few_rows_matches_oracle(rt, rows, in_f, out_f):
 
 # ------------------------------------------ tile configurations of large products
 @pytest.mark.parametrize("rows,in_f,out_f,chunk", [
-    (8192, 512, 8192, 1024),   # 2048 128x256 tiles: LdsHuge
+    (8192, 512, 8192, 1024),   # 1024 256x256 tiles: LdsGiant, sign bits expanded in LDS
+    (8320, 512, 8192, 1040),   # 2080 128x256 tiles (rows not a multiple of 256): LdsHuge
     (4096, 512, 2048, 1024),   # 512 128x128 tiles: LdsBig
 ])
 def test_large_products_match_small_tile_path(rt, rows, in_f, out_f, chunk):

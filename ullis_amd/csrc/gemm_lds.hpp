@@ -287,6 +287,84 @@ struct OpBits {
   }
 };
 
+// Packed sign bits [row][k/32] expanded once per stage into an fp16 +-1 tile
+// in LDS (unscaled only). The raw words stream in as for OpBits; after the
+// stage has landed, the block's threads each expand whole words into the
+// stage's fp16 tile (laid out and swizzled as OpMK's), and the fragments are
+// then plain ds_read_b128 reads. One expansion serves every wave that reads
+// the tile, which pays for 256-row tiles (four waves share each column).
+template <int ROWS, int BK>
+struct OpBitsX {
+  const uint32_t* p;
+  long ldw;  // words between rows
+  int rows;
+  static constexpr int WPR = BK / 32;  // words per row per stage
+  static constexpr int kWords = ROWS * WPR;
+  static constexpr int kInst = kWords <= 256 ? 1 : kWords / 256;  // one word per lane per load
+  static_assert(kWords % 256 == 0, "the stage's words must be whole block loads");
+  static constexpr int kWordsPerWave = kWords / 4;
+  static constexpr int kWordBytes = ((kWords * 4 + 1023) / 1024) * 1024;
+  static constexpr int CPR = BK / 8;  // 16-byte chunks per tile row
+  static constexpr int kBytes = kWordBytes + ROWS * BK * 2;
+  static constexpr int kExtra = 0;
+  static constexpr bool kExpand = true;
+  static_assert(CPR == 4 || CPR == 8 || CPR == 16 || CPR == 32, "BK 32, 64, 128 or 256");
+  __device__ static int swz(int row) { return OpMK<ROWS, BK>::swz(row); }
+  __device__ void prepare(char*, int, int) const {}
+  __device__ __forceinline__ void issue(char* stage, int row0, int k0, int wave, int lane) const {
+#pragma unroll
+    for (int t = 0; t < kInst; ++t) {
+      const int id = (wave * kInst + t) * 64 + lane;
+      const int row = id / WPR, w = id % WPR;
+      const int r = min(row0 + row, rows - 1);
+      dma4(p + (long)r * ldw + (k0 >> 5) + w, stage + (wave * kInst + t) * 256);
+    }
+  }
+  // Word id (row id / WPR, k 32 (id % WPR) .. +31) -> four 16-byte chunks of
+  // the tile; bit j (LSB first) is +1 when set, -1 when clear.
+  __device__ __forceinline__ void expand(char* stage) const {
+    char* tile = stage + kWordBytes;
+#pragma unroll
+    for (int t = 0; t < kWords / 256; ++t) {
+      const int id = t * 256 + (int)threadIdx.x;
+      const uint32_t word = reinterpret_cast<const uint32_t*>(stage)[id];
+      const int row = id / WPR, w = id % WPR;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t byte = word >> (8 * q);
+        u32x4 o;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          o[m] = 0xBC00BC00u ^ (((byte >> (2 * m)) & 1u) << 15) ^
+                 (((byte >> (2 * m + 1)) & 1u) << 31);
+        const int c = 4 * w + q;
+        *reinterpret_cast<u32x4*>(tile + row * (BK * 2) + 16 * (c ^ swz(row))) = o;
+      }
+    }
+  }
+  __device__ __forceinline__ half8 frag(const char* stage, const char*, int base, int ks16,
+                                        int lane, int) const {
+    const int row = base + (lane & 31);
+    const int c = (ks16 >> 3) + (lane >> 5);
+    return *reinterpret_cast<const half8*>(stage + kWordBytes + row * (BK * 2) +
+                                           16 * (c ^ swz(row)));
+  }
+  using Pre = half8;
+  using Raw = half8;
+  __device__ __forceinline__ Pre pre(const char* stage, const char* extra, int base, int ks16,
+                                     int lane, int k0rel) const {
+    return frag(stage, extra, base, ks16, lane, k0rel);
+  }
+  __device__ __forceinline__ Raw lut(const Pre& p, const char*) const { return p; }
+  __device__ __forceinline__ half8 fix(const Raw& r) const { return r; }
+};
+
+// Operands that expand a landed stage in LDS before its fragments are read.
+template <class O, class = void>
+inline constexpr bool kExpands = false;
+template <class O>
+inline constexpr bool kExpands<O, std::enable_if_t<O::kExpand>> = true;
+
 // wait_barrier<IPS * later>() for a runtime `later` in [0, S] (the K-loop tail).
 template <int IPS, int S>
 __device__ __forceinline__ void wait_stages(int later) {
@@ -525,6 +603,13 @@ __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const
     // Stage kt is complete once at most the later stages' loads are in flight.
     wait_stages<IPS, NS - 2>(nk - 1 - kt);
     if (kt + NS - 1 < nk) issue(kt + NS - 1);
+    if constexpr (kExpands<OA> || kExpands<OB>) {
+      // the stage's words have landed for every wave: expand them, then
+      // barrier again (LDS writes only; the loads in flight stay in flight)
+      if constexpr (kExpands<OA>) a.expand(smem + (kt % NS) * STAGE);
+      if constexpr (kExpands<OB>) b.expand(smem + (kt % NS) * STAGE + OA::kBytes);
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
     const char* st = smem + (kt % NS) * STAGE;
     const int k0rel = kt * BK;
     // Software pipeline over the stage's 16-deep K steps. Step s's MFMAs use
@@ -764,6 +849,12 @@ bool with_lds(long M, long N, long K, int splits, hipError_t* err, F&& f,
     return true;
   }
   return false;
+}
+
+// The 256x256-tile product for an M x N output with K in whole BK steps.
+inline bool giant_ok(long M, long N, long K) {
+  return K > 0 && K % LdsGiant::bk == 0 && M % 256 == 0 && N % 256 == 0 &&
+         (M / 256) * (N / 256) >= kGiantAutoBlocks;
 }
 
 template <class T, class OA, class OB, class Epi, int G>
