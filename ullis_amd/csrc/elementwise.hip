@@ -282,6 +282,11 @@ __global__ void f32_to_f16_kernel(const float* v, long n, uint16_t* out16) {
   if (i < n) out16[i] = f32_to_f16_bits(v[i]);
 }
 
+__global__ void add_f32_kernel(const float* a, const float* b, long n, float* out) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = a[i] + b[i];
+}
+
 __global__ __launch_bounds__(1024) void partial_reduce_kernel(const float* part, int nblk,
                                                               long ncols, long split, VecTarget a,
                                                               VecTarget b) {
@@ -357,6 +362,12 @@ inline dim3 grid1d(long n, int threads = 256) { return dim3((unsigned)cdiv(n, th
 inline bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
+
+hipError_t add_f32(hipStream_t s, const float* a, const float* b, long n, float* out) {
+  if (n <= 0) return hipSuccess;
+  launch(add_f32_kernel, grid1d(n), dim3(256), 0, s, a, b, n, out);
+  return hipGetLastError();
+}
 
 hipError_t fill_f32(hipStream_t s, float* p, long n, float v) {
   if (n <= 0) return hipSuccess;

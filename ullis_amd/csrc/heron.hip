@@ -86,6 +86,9 @@ struct ullis_hip_heron {
   void* act = nullptr;  // one allocation for activations, tapes and scratch
   // activations / tapes
   float *resid = nullptr, *after_rosa = nullptr;
+  // O products (bias + scale * y . S^T, before the residual add) of every
+  // layer, computed at the step's start on the second stream
+  float* o_pre = nullptr;
   uint16_t *ln16 = nullptr, *q16 = nullptr, *k16 = nullptr, *v16 = nullptr;
   uint16_t *y16 = nullptr, *ln2_16 = nullptr, *shifted16 = nullptr;
   uint8_t* idx_rm = nullptr;
@@ -97,8 +100,8 @@ struct ullis_hip_heron {
   uint16_t* ln3_16 = nullptr;    // LN3 output scratch of the second stream's fallback path
   // second stream and its ordering events
   hipStream_t side = nullptr;
-  std::vector<hipEvent_t> ev_fwd, ev_bwd;
-  hipEvent_t ev_join = nullptr, ev_head = nullptr;
+  std::vector<hipEvent_t> ev_fwd, ev_bwd, ev_o;
+  hipEvent_t ev_join = nullptr, ev_head = nullptr, ev_start = nullptr;
   float *g_x = nullptr, *g_a = nullptr, *g_b = nullptr;
   float *slots = nullptr, *stats = nullptr;
   float* row_loss = nullptr;
@@ -499,6 +502,7 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
   auto add = [&](size_t b) { bytes += Carver::bytes_for(b); };
   add(4ul * nd * (L + 1));   // resid
   add(4ul * nd * L);         // after_rosa
+  add(4ul * nd * L);         // o_pre
   for (int i = 0; i < 4; ++i) add(2ul * nd);  // ln16 q16 k16 v16
   add(2ul * nd * L);         // y16
   add(2ul * nd * L);         // ln2_16
@@ -534,6 +538,7 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
   Carver cv(h->act);
   h->resid = cv.take<float>(nd * (L + 1));
   h->after_rosa = cv.take<float>(nd * L);
+  h->o_pre = cv.take<float>(nd * L);
   h->ln16 = cv.take<uint16_t>(nd);
   h->q16 = cv.take<uint16_t>(nd);
   h->k16 = cv.take<uint16_t>(nd);
@@ -574,9 +579,11 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
     bool ok2 = hipStreamCreateWithFlags(&h->side, hipStreamNonBlocking) == hipSuccess;
     h->ev_fwd.assign(L, nullptr);
     h->ev_bwd.assign(L, nullptr);
-    for (auto* v : {&h->ev_fwd, &h->ev_bwd})
+    h->ev_o.assign(L, nullptr);
+    for (auto* v : {&h->ev_fwd, &h->ev_bwd, &h->ev_o})
       for (auto& e : *v) ok2 = ok2 && hipEventCreateWithFlags(&e, hipEventDisableTiming) == hipSuccess;
     ok2 = ok2 && hipEventCreateWithFlags(&h->ev_join, hipEventDisableTiming) == hipSuccess;
+    ok2 = ok2 && hipEventCreateWithFlags(&h->ev_start, hipEventDisableTiming) == hipSuccess;
     ok2 = ok2 && hipEventCreateWithFlags(&h->ev_head, hipEventDisableTiming) == hipSuccess;
     if (!ok2) {
       ullis_hip_heron_destroy(h);
@@ -616,10 +623,11 @@ void ullis_hip_heron_destroy(ullis_hip_heron* h) {
   if (h->ctx) (void)hipStreamSynchronize(h->ctx->stream);
   for (auto& e : h->probe_events) (void)hipEventDestroy(e);
   if (h->side) (void)hipStreamSynchronize(h->side);
-  for (auto* v : {&h->ev_fwd, &h->ev_bwd})
+  for (auto* v : {&h->ev_fwd, &h->ev_bwd, &h->ev_o})
     for (auto& e : *v)
       if (e) (void)hipEventDestroy(e);
   if (h->ev_join) (void)hipEventDestroy(h->ev_join);
+  if (h->ev_start) (void)hipEventDestroy(h->ev_start);
   if (h->ev_head) (void)hipEventDestroy(h->ev_head);
   if (h->side) (void)hipStreamDestroy(h->side);
   if (h->arena) (void)hipFree(h->arena);
@@ -726,6 +734,21 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
   // y = (2 idx - 1) e of every layer (e is not updated before the step's end)
   STEP(rosa_expand_layers(s, rosa_idx, h->e_host.data(), h->e_dev, L, B, T, D, h->y16, h->idx_rm),
        "rosa y");
+  // The O products of every layer (src/model.rs:1428) read only y and the O
+  // weights, all final here (updates run at the step's end): the second
+  // stream computes them ahead of the layers, and each layer's LN2 adds its
+  // residual x_l, so the residual chain no longer waits for an O GEMM per
+  // layer.
+  STEP(hipEventRecord(h->ev_start, s), "event");
+  STEP(hipStreamWaitEvent(h->side, h->ev_start, 0), "event wait");
+  for (long l = 0; l < L; ++l) {
+    const Block& b = h->blocks[l];
+    PackedFwdOut o;
+    o.y32 = h->o_pre + l * nd;
+    STEP(packed_forward(h->side, h->y16 + l * nd, kF16, R, D, D, b.o.bits, b.o.scale, b.o.bias, o),
+         "o");
+    STEP(hipEventRecord(h->ev_o[l], h->side), "event");
+  }
 
   // ------------------------------------------------------------- forward
   for (long l = 0; l < L; ++l) {
@@ -752,22 +775,17 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
                                    qkv + (l * 3 + 2) * words};
       STEP(packed_forward_bits3(h->side, xin, R, D, D, wb, sc, bi, planes), "qkv");
     }
-    uint16_t* y16 = h->y16 + l * nd;
     float* ar = h->after_rosa + l * nd;
-    {
-      PackedFwdOut o;
-      o.y32 = ar;
-      o.resid = x_l;
-      STEP(packed_forward(s, y16, kF16, R, D, D, b.o.bits, b.o.scale, b.o.bias, o), "o");
-    }
-    // CMix (src/model.rs:1018-1078)
+    // CMix (src/model.rs:1018-1078) on ar = x_l + o_l (add_inplace,
+    // src/model.rs:2890), formed by the LN2 kernel
     uint16_t* ln2 = h->ln2_16 + l * nd;
     uint16_t* sh = h->shifted16 + l * nd;
     uint16_t* key = h->key16 + l * nf;
     uint16_t* r2 = h->relu2_16 + l * nf;
+    STEP(hipStreamWaitEvent(s, h->ev_o[l], 0), "event wait");
     PROBED(ULLIS_HIP_PROBE_LN_FORWARD,
-           layer_norm_mix_forward(s, ar, R, T, D, b.ln2.w, b.ln2.b, ln2, true, b.cx_k, sh, nullptr,
-                                  nullptr, nullptr, nullptr),
+           layer_norm_mix_forward(s, h->o_pre + l * nd, R, T, D, b.ln2.w, b.ln2.b, ln2, true,
+                                  b.cx_k, sh, nullptr, nullptr, nullptr, nullptr, x_l, ar),
            "ln2 + mix");
     {
       PackedFwdOut o;

@@ -22,16 +22,26 @@ constexpr int kRowsPerBlock = 4;
 
 // LayerNorm of one row by one wave: lane holds channels [4 (lane + 64 j), +4)
 // of chunk j (NV float4 chunks per lane, ch <= 256 * NV, ch % 4 == 0).
+// With rr, the row normalised is xr + rr (fp32 sums), and sum_out (if set)
+// receives it.
 template <int NV>
 __device__ __forceinline__ void ln_row_vec(const float* __restrict__ xr, int ch, int lane,
                                            const uint16_t* __restrict__ w,
-                                           const uint16_t* __restrict__ b, floatx4 (&out)[NV]) {
+                                           const uint16_t* __restrict__ b, floatx4 (&out)[NV],
+                                           const float* __restrict__ rr = nullptr,
+                                           float* __restrict__ sum_out = nullptr) {
   floatx4 v[NV];
   float s = 0.0f;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int c = (lane + 64 * j) * 4;
     v[j] = c < ch ? *reinterpret_cast<const floatx4*>(xr + c) : (floatx4){};
+    if (rr && c < ch) {
+      const floatx4 r = *reinterpret_cast<const floatx4*>(rr + c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[j][e] = r[e] + v[j][e];
+      if (sum_out) *reinterpret_cast<floatx4*>(sum_out + c) = v[j];
+    }
     s += (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]);
   }
   const float mean = wave_sum(s) / (float)ch;
@@ -106,7 +116,8 @@ __device__ __forceinline__ void mix4_store(const half4& x, const half4& p, const
 // wave normalises its row and the previous row of the same sequence (the
 // same per-row arithmetic as ln_fwd_vec_kernel), so out_i = mix_i of the
 // fp16 rows without the LayerNorm output making a round trip through HBM.
-// y16 (optional) also receives the fp16 LayerNorm output.
+// y16 (optional) also receives the fp16 LayerNorm output. With resid, the
+// LayerNorm input is resid + x (a residual add), which sum_out receives.
 template <int NV>
 __global__ __launch_bounds__(256) void ln_mix_kernel(const float* __restrict__ x, long rows,
                                                      int time, int ch,
@@ -115,14 +126,19 @@ __global__ __launch_bounds__(256) void ln_mix_kernel(const float* __restrict__ x
                                                      uint16_t* __restrict__ y16,
                                                      const uint16_t* mix0, uint16_t* out0,
                                                      const uint16_t* mix1, uint16_t* out1,
-                                                     const uint16_t* mix2, uint16_t* out2) {
+                                                     const uint16_t* mix2, uint16_t* out2,
+                                                     const float* __restrict__ resid,
+                                                     float* __restrict__ sum_out) {
   const int lane = threadIdx.x & 63;
   const long row = (long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
   floatx4 cur[NV], prev[NV];
-  ln_row_vec<NV>(x + row * ch, ch, lane, w, b, cur);
+  ln_row_vec<NV>(x + row * ch, ch, lane, w, b, cur, resid ? resid + row * ch : nullptr,
+                 resid ? sum_out + row * ch : nullptr);
   const bool has_prev = row % time != 0;  // uniform over the wave
-  if (has_prev) ln_row_vec<NV>(x + (row - 1) * ch, ch, lane, w, b, prev);
+  if (has_prev)
+    ln_row_vec<NV>(x + (row - 1) * ch, ch, lane, w, b, prev,
+                   resid ? resid + (row - 1) * ch : nullptr);
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int c = (lane + 64 * j) * 4;
@@ -520,19 +536,27 @@ hipError_t layer_norm_forward(hipStream_t s, const float* x, long rows, long ch,
 hipError_t layer_norm_mix_forward(hipStream_t s, const float* x, long rows, long time, long ch,
                                   const uint16_t* w, const uint16_t* b, uint16_t* y16, bool keep_y,
                                   const uint16_t* mix0, uint16_t* out0, const uint16_t* mix1,
-                                  uint16_t* out1, const uint16_t* mix2, uint16_t* out2) {
+                                  uint16_t* out1, const uint16_t* mix2, uint16_t* out2,
+                                  const float* resid, float* sum_out) {
   if (rows <= 0 || ch <= 0 || time <= 0) return hipSuccess;
+  if (resid && !sum_out) return hipErrorInvalidValue;
   auto a8 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; };
   const bool fused = ch % 4 == 0 && ch <= 4096 && time <= INT32_MAX && vec_ok(x) && a8(y16) &&
                      (!out0 || (a8(out0) && a8(mix0))) && (!out1 || (a8(out1) && a8(mix1))) &&
-                     (!out2 || (a8(out2) && a8(mix2)));
+                     (!out2 || (a8(out2) && a8(mix2))) &&
+                     (!resid || (vec_ok(resid) && vec_ok(sum_out)));
   if (fused) {
     return by_nv(ch, [&](auto nv) {
       launch(ln_mix_kernel<decltype(nv)::value>, dim3((unsigned)cdiv(rows, kRowsPerBlock)),
              dim3(256), 0, s, x, rows, (int)time, (int)ch, w, b, keep_y ? y16 : nullptr, mix0,
-             out0, mix1, out1, mix2, out2);
+             out0, mix1, out1, mix2, out2, resid, sum_out);
       return hipGetLastError();
     });
+  }
+  if (resid) {
+    const hipError_t e = add_f32(s, resid, x, rows * ch, sum_out);
+    if (e != hipSuccess) return e;
+    x = sum_out;
   }
   hipError_t e = layer_norm_forward(s, x, rows, ch, w, b, nullptr, y16);
   if (e != hipSuccess) return e;

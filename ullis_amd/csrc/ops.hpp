@@ -181,10 +181,15 @@ hipError_t fp16_weight_finish(hipStream_t s, const float* part, int splits, long
 // LayerNorm whose fp16 output feeds time_shift_mix (up to three mixes) in one
 // kernel; same results as layer_norm_forward(y16) then time_shift_mix. y16
 // receives the fp16 LayerNorm output when keep_y (it is scratch otherwise).
+// With resid, the LayerNorm input is resid + x (fp32), written to sum_out.
 hipError_t layer_norm_mix_forward(hipStream_t s, const float* x, long rows, long time, long ch,
                                   const uint16_t* w, const uint16_t* b, uint16_t* y16, bool keep_y,
                                   const uint16_t* mix0, uint16_t* out0, const uint16_t* mix1,
-                                  uint16_t* out1, const uint16_t* mix2, uint16_t* out2);
+                                  uint16_t* out1, const uint16_t* mix2, uint16_t* out2,
+                                  const float* resid = nullptr, float* sum_out = nullptr);
+
+// out = a + b elementwise (fp32).
+hipError_t add_f32(hipStream_t s, const float* a, const float* b, long n, float* out);
 hipError_t layer_norm_forward(hipStream_t s, const float* x, long rows, long ch,
                               const uint16_t* w, const uint16_t* b, float* y32, uint16_t* y16);
 
