@@ -736,19 +736,23 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
        "rosa y");
   // The O products of every layer (src/model.rs:1428) read only y and the O
   // weights, all final here (updates run at the step's end): the second
-  // stream computes them ahead of the layers, and each layer's LN2 adds its
+  // stream computes them ahead of their layers, and each layer's LN2 adds its
   // residual x_l, so the residual chain no longer waits for an O GEMM per
-  // layer.
-  STEP(hipEventRecord(h->ev_start, s), "event");
-  STEP(hipStreamWaitEvent(h->side, h->ev_start, 0), "event wait");
-  for (long l = 0; l < L; ++l) {
+  // layer. Layer 0's runs now; layer l + 1's is queued on the second stream
+  // once x_l is complete, ahead of layer l's Q/K/V branch, which paces the
+  // second stream's work with the layers instead of front-loading it.
+  auto o_forward = [&](long l) -> int {
     const Block& b = h->blocks[l];
     PackedFwdOut o;
     o.y32 = h->o_pre + l * nd;
     STEP(packed_forward(h->side, h->y16 + l * nd, kF16, R, D, D, b.o.bits, b.o.scale, b.o.bias, o),
          "o");
     STEP(hipEventRecord(h->ev_o[l], h->side), "event");
-  }
+    return 0;
+  };
+  STEP(hipEventRecord(h->ev_start, s), "event");
+  STEP(hipStreamWaitEvent(h->side, h->ev_start, 0), "event wait");
+  if (int rc = o_forward(0)) return rc;
 
   // ------------------------------------------------------------- forward
   for (long l = 0; l < L; ++l) {
@@ -763,6 +767,8 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
     // second stream once x_l is complete.
     STEP(hipEventRecord(h->ev_fwd[l], s), "event");
     STEP(hipStreamWaitEvent(h->side, h->ev_fwd[l], 0), "event wait");
+    if (l + 1 < L)
+      if (int rc = o_forward(l + 1)) return rc;
     STEP(layer_norm_mix_forward(h->side, x_l, R, T, D, b.ln3.w, b.ln3.b, h->ln3_16, false, b.x_q,
                                 h->q16, b.x_k, h->k16, b.x_v, h->v16),
          "ln3 + mix3");
