@@ -793,8 +793,10 @@ constexpr long kGiantAutoBlocks = 512;
 // the four-stage BK 128 ring for launches of one block per CU whose operands
 // come from HBM; kBig = 128x128 tiles; kDeepGiant = kDeep, with 256x256
 // tiles for very large products (two k-contiguous fp16 operands only: with
-// a sign-bit or transposed operand those tiles measured slower than 128x256).
-enum class LdsPolicy { kAuto, kDeep, kBig, kDeepGiant };
+// a sign-bit or transposed operand those tiles measured slower than 128x256);
+// kNoBig = kAuto without the 128x128 rule (config 4's head logits, 1024 such
+// tiles: 64x64 tiles measured faster, the head op 170 -> 156 us).
+enum class LdsPolicy { kAuto, kDeep, kBig, kDeepGiant, kNoBig };
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool mk_ok(const void* p, long ld) { return p && aligned16(p) && ld % 8 == 0; }
@@ -831,7 +833,7 @@ bool with_lds(long M, long N, long K, int splits, hipError_t* err, F&& f,
     *err = f(LdsHuge{});
     return true;
   }
-  if (K % LdsBig::bk == 0 && M % 128 == 0 && N % 128 == 0 &&
+  if (policy != LdsPolicy::kNoBig && K % LdsBig::bk == 0 && M % 128 == 0 && N % 128 == 0 &&
       (M / 128) * (N / 128) * splits >= kBigAutoBlocks) {
     *err = f(LdsBig{});
     return true;

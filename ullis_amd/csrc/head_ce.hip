@@ -341,7 +341,7 @@ hipError_t logits_gemm(hipStream_t s, const uint16_t* hidden16, long rows, long 
         lds::OpMK<T::bm, T::bk> a{reinterpret_cast<const half_t*>(hidden16), d, (int)rows};
         lds::OpBits<T::bn, T::bk, false> b{bits_rows, d / 32, (int)ncols, nullptr, 0};
         return lds::launch_lds<T>(s, a, b, epi, rows, ncols, d, 1);
-      }))
+      }, lds::LdsPolicy::kNoBig))
     return err;
   const bool vec = (reinterpret_cast<uintptr_t>(hidden16) & 15u) == 0 && d % 8 == 0;
   auto run = [&](auto cfg) {
