@@ -269,6 +269,20 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
                          uint32_t ignore_id, float learning_rate, const uint8_t* rosa_idx,
                          float* g_emb, float* row_loss, float* stats4, uint32_t* qkv_bits);
 /*
+ * One step from token ids (UllisHeron::train_step_on with its embedding
+ * gather and scatter-SGD, src/model.rs:2866-2873, 2986-2993): gathers
+ * table[tokens] (f16 [vocab, d]) into x_emb, runs ullis_hip_heron_step, and
+ * applies the clipped SGD of g_emb to the table rows (table_residual: fp32
+ * carry, [vocab, d]) in row order, as soon as g_emb is complete. invalid
+ * (may be NULL) counts token ids >= vocab, whose rows gather as zeros and
+ * are not updated. Runs eagerly (no step graph).
+ */
+int ullis_hip_heron_step_tokens(ullis_hip_heron* h, uint16_t* table, float* table_residual,
+                                size_t vocab, const uint32_t* tokens, const uint32_t* labels,
+                                uint32_t ignore_id, float learning_rate, const uint8_t* rosa_idx,
+                                float* x_emb, float* g_emb, float* row_loss, float* stats4,
+                                uint32_t* qkv_bits, uint32_t* invalid);
+/*
  * Step graph (no counterpart in the reference, whose Metal backend encodes
  * command buffers per step): with enable != 0, ullis_hip_heron_step captures
  * its launches on both streams into a HIP graph the first time and replays the

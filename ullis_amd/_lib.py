@@ -93,6 +93,8 @@ SIGNATURES = {
     "ullis_hip_heron_arena": (i32, [vp, C.POINTER(vp), C.POINTER(C.c_uint64)]),
     "ullis_hip_heron_refresh_derived": (i32, [vp]),
     "ullis_hip_heron_step": (i32, [vp, vp, vp, u32, f32, vp, vp, vp, vp, vp]),
+    "ullis_hip_heron_step_tokens": (i32, [vp, vp, vp, sz, vp, vp, u32, f32, vp, vp, vp, vp, vp,
+                                         vp, vp]),
     "ullis_hip_heron_set_graph": (i32, [vp, i32]),
     "ullis_hip_heron_probe": (i32, [vp, i32]),
     "ullis_hip_heron_probe_read": (i32, [vp, C.POINTER(f32), C.POINTER(i32)]),

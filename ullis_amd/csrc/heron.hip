@@ -714,11 +714,22 @@ int ullis_hip_heron_refresh_derived(ullis_hip_heron* h) {
 
 namespace {
 
+// The embedding table a step from token ids updates (src/model.rs:2986-2993).
+struct EmbedArgs {
+  uint16_t* table;
+  float* residual;
+  long vocab;
+  const uint32_t* tokens;
+};
+
 // Every launch of one train step, on the context stream and the second
-// stream (arguments checked by ullis_hip_heron_step).
+// stream (arguments checked by ullis_hip_heron_step). With emb, the
+// embedding scatter-SGD of g_emb runs as soon as g_emb is complete, beside
+// the second stream's last updates.
 int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels,
                   uint32_t ignore_id, float lr, const uint8_t* rosa_idx, float* g_emb,
-                  float* row_loss, float* stats4, uint32_t* qkv_bits) {
+                  float* row_loss, float* stats4, uint32_t* qkv_bits,
+                  const EmbedArgs* emb = nullptr) {
   ullis_hip_ctx* c = h->ctx;
   hipStream_t s = c->stream;
   const long R = h->rows, D = h->D, F = h->F, L = h->L, T = h->time, B = h->batch;
@@ -936,6 +947,10 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
     }
   }
 
+  if (emb)
+    STEP(embedding_scatter_sgd(s, emb->table, emb->residual, emb->vocab, D, emb->tokens, R, g_emb,
+                               lr),
+         "embedding scatter sgd");
   // the second stream's work is done before the updates and the step's end
   STEP(hipEventRecord(h->ev_join, h->side), "event");
   STEP(hipStreamWaitEvent(s, h->ev_join, 0), "event wait");
@@ -952,6 +967,29 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
 }  // namespace
 
 extern "C" {
+
+int ullis_hip_heron_step_tokens(ullis_hip_heron* h, uint16_t* table, float* table_residual,
+                                size_t vocab, const uint32_t* tokens, const uint32_t* labels,
+                                uint32_t ignore_id, float lr, const uint8_t* rosa_idx,
+                                float* x_emb, float* g_emb, float* row_loss, float* stats4,
+                                uint32_t* qkv_bits, uint32_t* invalid) {
+  if (!h) return ULLIS_HIP_ERR_INVALID;
+  ullis_hip_ctx* c = h->ctx;
+  if (!table || !table_residual || !tokens || !labels || !rosa_idx || !x_emb || !g_emb)
+    return c->fail(ULLIS_HIP_ERR_INVALID,
+                   "heron step from tokens needs the table, its carry, tokens, labels, rosa_idx, "
+                   "x_emb and g_emb");
+  if (vocab == 0 || vocab > (size_t)UINT32_MAX)
+    return c->fail(ULLIS_HIP_ERR_INVALID, "embedding vocab must be non-zero and fit u32");
+  if (!(lr > 0.0f) || !__builtin_isfinite(lr))
+    return c->fail(ULLIS_HIP_ERR_INVALID,
+                   "train step requires a positive learning rate and time >= 2");
+  STEP(embedding_gather(c->stream, table, (long)vocab, h->D, tokens, h->rows, x_emb, invalid),
+       "embedding gather");
+  const EmbedArgs emb{table, table_residual, (long)vocab, tokens};
+  return step_launches(h, x_emb, labels, ignore_id, lr, rosa_idx, g_emb, row_loss, stats4,
+                       qkv_bits, &emb);
+}
 
 int ullis_hip_heron_set_graph(ullis_hip_heron* h, int enable) {
   if (!h) return ULLIS_HIP_ERR_INVALID;

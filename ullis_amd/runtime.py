@@ -585,11 +585,8 @@ class HeronTrainer:
         stream-ordered on the device. table / table_res: f16 [vocab, d] and its
         fp32 carry; x_emb / g_emb: fp32 [rows, d] work buffers; invalid
         (optional u32) counts token ids >= vocab."""
-        s, lib, ctx = self.shape, self.rt.lib, self.rt.ctx
-        self.rt._check(lib.ullis_hip_embedding_gather(
-            ctx, table.ptr, s.vocab, s.d_model, tokens.ptr, s.rows, x_emb.ptr,
-            invalid.ptr if invalid else None), "embedding_gather")
-        self.step(x_emb, labels, ignore_id, lr, rosa_idx, g_emb, row_loss, stats, qkv_bits)
-        self.rt._check(lib.ullis_hip_embedding_scatter_sgd(
-            ctx, table.ptr, table_res.ptr, s.vocab, s.d_model, tokens.ptr, s.rows, g_emb.ptr, lr),
-            "embedding_scatter_sgd")
+        self.rt._check(self.rt.lib.ullis_hip_heron_step_tokens(
+            self.h, table.ptr, table_res.ptr, self.shape.vocab, tokens.ptr, labels.ptr, ignore_id,
+            lr, rosa_idx.ptr, x_emb.ptr, g_emb.ptr, row_loss.ptr if row_loss else None,
+            stats.ptr if stats else None, qkv_bits.ptr if qkv_bits else None,
+            invalid.ptr if invalid else None), "heron_step_tokens")
