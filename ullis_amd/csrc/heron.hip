@@ -742,8 +742,9 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
   bool ln0_now = false;
 
   STEP(fill_f32(s, h->slots, L + 2, 0.0f), "clear amax slots");
-  // y = (2 idx - 1) e of every layer (e is not updated before the step's end)
-  STEP(rosa_expand_layers(s, rosa_idx, h->e_host.data(), h->e_dev, L, B, T, D, h->y16, h->idx_rm),
+  // y = (2 idx - 1) e (e is not updated before the step's end): layer 0's
+  // here, the other layers' on the second stream after layer 0's O product
+  STEP(rosa_expand_layers(s, rosa_idx, h->e_host.data(), h->e_dev, 1, B, T, D, h->y16, h->idx_rm),
        "rosa y");
   // The O products of every layer (src/model.rs:1428) read only y and the O
   // weights, all final here (updates run at the step's end): the second
@@ -764,6 +765,10 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
   STEP(hipEventRecord(h->ev_start, s), "event");
   STEP(hipStreamWaitEvent(h->side, h->ev_start, 0), "event wait");
   if (int rc = o_forward(0)) return rc;
+  if (L > 1)
+    STEP(rosa_expand_layers(h->side, rosa_idx + nd, h->e_host.data() + 1, h->e_dev + 1, L - 1, B,
+                            T, D, h->y16 + nd, h->idx_rm + nd),
+         "rosa y");
 
   // ------------------------------------------------------------- forward
   for (long l = 0; l < L; ++l) {
