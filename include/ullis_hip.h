@@ -130,21 +130,27 @@ int ullis_hip_transpose_bits(ullis_hip_ctx* ctx, const uint32_t* bits, size_t ou
                              uint32_t* bits_t);
 
 /* MetalRuntime::packed_head_train_sgd, src/metal.rs:3300-3510, as driven by
- * UllisHeron::apply_head_ce (src/model.rs:3145-3193): next-token CE over the
- * packed head with horizon 1, streamed over vocab tiles (no [rows, vocab]
- * buffer), then the head update: BinaryConnect latent step (ste_scale),
- * scale clipped SGD at learning_rate and bias clipped SGD at 8 x learning_rate,
- * then bits / bits_t repack. learning_rate == 0 computes gradients only.
- * stats4 (device) receives {mean_loss, n_valid, gradient_scale, loss_sum}.
- * g_scale / g_bias / g_w (device, optional) receive the gradients. */
+ * UllisHeron::apply_head_ce (src/model.rs:3145-3193): CE of row r against
+ * targets[r + horizon] over the packed head (causal_ce_row_valid,
+ * src/model.rs:27-39; apply_head_ce passes horizon 1), streamed over vocab
+ * tiles (no [rows, vocab] buffer), then the head update: BinaryConnect latent
+ * step (ste_scale), scale clipped SGD at learning_rate and bias clipped SGD
+ * at 8 x learning_rate, then bits / bits_t repack. learning_rate == 0
+ * computes gradients only. stats4 (device) receives {mean_loss, n_valid,
+ * gradient_scale, loss_sum}. g_scale / g_bias / g_w (device, optional)
+ * receive the gradients. A target >= vocab other than ignore_id (which the
+ * reference's train step refuses, src/model.rs:2852-2861) leaves its row out
+ * of the loss and the gradient and is counted into *invalid (device u32,
+ * optional, accumulated); the caller decides whether to keep the update. */
 int ullis_hip_packed_head_train_sgd(ullis_hip_ctx* ctx, const uint16_t* hidden16, uint32_t* bits,
                                     uint32_t* bits_t, uint16_t* scale, uint16_t* bias,
                                     uint16_t* latent, float* latent_residual,
                                     float* scale_residual, float* bias_residual,
                                     const uint32_t* targets, size_t rows, size_t time, size_t d,
-                                    size_t vocab, uint32_t ignore_id, float learning_rate,
-                                    float ste_scale, float* row_loss, float* stats4,
-                                    float* g_hidden, float* g_scale, float* g_bias, float* g_w);
+                                    size_t vocab, size_t horizon, uint32_t ignore_id,
+                                    float learning_rate, float ste_scale, float* row_loss,
+                                    float* stats4, float* g_hidden, float* g_scale, float* g_bias,
+                                    float* g_w, uint32_t* invalid);
 
 /* Embedding gather of UllisHeron::train_step_on (src/model.rs:2866-2873):
  * x[r] = the f16 table row tokens[r] as fp32 (table [vocab, d]). The
@@ -264,18 +270,27 @@ int ullis_hip_heron_refresh_derived(ullis_hip_heron* h);
  * row_loss fp32 [batch*time]; stats4 {mean_loss, n_valid, gscale, loss_sum};
  * qkv_bits (may be NULL) u32 [n_layers][3][ceil(batch*time*d/32)], the Q/K/V
  * sign bit-planes handed to the automaton. All pointers are device pointers.
+ * invalid (may be NULL) receives the number of labels >= vocab other than
+ * ignore_id. train_step_on refuses such a step before any update
+ * (src/model.rs:2852-2861); labels are device data here, so the step runs,
+ * but when the count is non-zero its update launches change no parameter,
+ * and the loss and gradients leave those rows out.
  */
 int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels,
                          uint32_t ignore_id, float learning_rate, const uint8_t* rosa_idx,
-                         float* g_emb, float* row_loss, float* stats4, uint32_t* qkv_bits);
+                         float* g_emb, float* row_loss, float* stats4, uint32_t* qkv_bits,
+                         uint32_t* invalid);
 /*
  * One step from token ids (UllisHeron::train_step_on with its embedding
  * gather and scatter-SGD, src/model.rs:2866-2873, 2986-2993): gathers
  * table[tokens] (f16 [vocab, d]) into x_emb, runs ullis_hip_heron_step, and
  * applies the clipped SGD of g_emb to the table rows (table_residual: fp32
  * carry, [vocab, d]) in row order, as soon as g_emb is complete. invalid
- * (may be NULL) counts token ids >= vocab, whose rows gather as zeros and
- * are not updated. Runs eagerly (no step graph).
+ * (may be NULL) receives the number of token ids >= vocab plus labels >=
+ * vocab other than ignore_id; when it is non-zero the step changed no
+ * parameter and no table row (the reference refuses the step,
+ * src/model.rs:2852-2861). Replayed from the step graph like
+ * ullis_hip_heron_step when that is on.
  */
 int ullis_hip_heron_step_tokens(ullis_hip_heron* h, uint16_t* table, float* table_residual,
                                 size_t vocab, const uint32_t* tokens, const uint32_t* labels,
@@ -283,11 +298,52 @@ int ullis_hip_heron_step_tokens(ullis_hip_heron* h, uint16_t* table, float* tabl
                                 float* x_emb, float* g_emb, float* row_loss, float* stats4,
                                 uint32_t* qkv_bits, uint32_t* invalid);
 /*
+ * CausalLoss of the last step (src/model.rs:58-80, as train_step_on fills it,
+ * src/model.rs:2997-3024), into *out (DEVICE memory, sizeof(ullis_hip_causal_loss)
+ * bytes): loss, valid count, sign-bit flips per class (head, CMix key, ROSA
+ * O) and their total, row-loss percentiles, unigram CE and unique targets,
+ * and the rms / mean-abs statistics of the embedding gradient (g_emb), the
+ * head scale gradient, head scale / bias / latent, the first block's CMix
+ * value weight and the head's mean latent step; residual_abs_mean is the
+ * mean |carry| of the embedding table when table_residual (table_elems
+ * floats) is given, else 0. Call after a step and before the next one, with
+ * the g_emb, labels, ignore_id and row_loss (NULL: the step wrote none) of
+ * that step. Stream-ordered; statistics are fixed-order sums, so they match
+ * the reference's sequential sums to rounding.
+ */
+typedef struct ullis_hip_causal_loss {
+  float next_token;
+  uint32_t next_token_count;
+  uint32_t binary_flip_count;
+  float loss_p10;
+  float loss_p50;
+  float loss_p90;
+  float unigram_ce;
+  uint32_t unique_targets;
+  uint32_t flips_head;
+  uint32_t flips_cmix;
+  uint32_t flips_rosa_o;
+  float embed_grad_rms;
+  float head_scale_grad_rms;
+  float head_scale_rms;
+  float residual_abs_mean;
+  float cmix_value_rms;
+  float head_latent_abs_mean;
+  float head_latent_step_abs;
+  float head_bias_rms;
+} ullis_hip_causal_loss;
+int ullis_hip_heron_causal_loss(ullis_hip_heron* h, const float* g_emb, const uint32_t* labels,
+                                uint32_t ignore_id, const float* row_loss,
+                                const float* table_residual, size_t table_elems,
+                                ullis_hip_causal_loss* out);
+
+/*
  * Step graph (no counterpart in the reference, whose Metal backend encodes
- * command buffers per step): with enable != 0, ullis_hip_heron_step captures
- * its launches on both streams into a HIP graph the first time and replays the
- * graph while it is called with the same pointers, ignore_id and
- * learning_rate (other arguments capture again). Probed steps run eagerly.
+ * command buffers per step): with enable != 0, ullis_hip_heron_step and
+ * ullis_hip_heron_step_tokens capture their launches on both streams into a
+ * HIP graph the first time and replay the graph while they are called with
+ * the same pointers, vocab, ignore_id and learning_rate (other arguments
+ * capture again). Probed steps run eagerly.
  * enable = 0 drops the graph.
  */
 int ullis_hip_heron_set_graph(ullis_hip_heron* h, int enable);

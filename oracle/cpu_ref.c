@@ -383,6 +383,18 @@ int ucr_head_ce(const float* hidden, size_t rows, size_t time, size_t d, size_t 
                 const uint32_t* bits, const uint16_t* scale, const uint16_t* bias,
                 const uint32_t* targets, uint32_t ignore_id, float* mean_loss, size_t* n_valid,
                 float* row_loss, float* g_hidden, float* g_w, float* g_scale, float* g_bias) {
+  return ucr_head_ce_horizon(hidden, rows, time, 1, d, vocab, bits, scale, bias, targets,
+                             ignore_id, mean_loss, n_valid, row_loss, g_hidden, g_w, g_scale,
+                             g_bias);
+}
+
+/* The Metal method takes the horizon (src/metal.rs:3300-3316, causal_supervised_count
+ * and the softmax_cross_entropy kernel); apply_head_ce passes 1. */
+int ucr_head_ce_horizon(const float* hidden, size_t rows, size_t time, size_t horizon, size_t d,
+                        size_t vocab, const uint32_t* bits, const uint16_t* scale,
+                        const uint16_t* bias, const uint32_t* targets, uint32_t ignore_id,
+                        float* mean_loss, size_t* n_valid, float* row_loss, float* g_hidden,
+                        float* g_w, float* g_scale, float* g_bias) {
   size_t row, v, nv = 0;
   float loss_scale, loss_sum = 0.0f;
   float* logits = (float*)malloc(vocab * sizeof(float));
@@ -395,7 +407,7 @@ int ucr_head_ce(const float* hidden, size_t rows, size_t time, size_t d, size_t 
     return -1;
   }
   for (row = 0; row < rows; ++row) {
-    if (ucr_causal_ce_row_valid(row, time, 1, targets, rows, ignore_id)) nv += 1;
+    if (ucr_causal_ce_row_valid(row, time, horizon, targets, rows, ignore_id)) nv += 1;
   }
   loss_scale = ucr_causal_ce_gradient_scale(nv, time);
   memset(g_w, 0, vocab * d * sizeof(float));
@@ -407,8 +419,8 @@ int ucr_head_ce(const float* hidden, size_t rows, size_t time, size_t d, size_t 
     size_t target;
     const float* h;
     float mx = -INFINITY, exp_sum = 0.0f, ce;
-    if (!ucr_causal_ce_row_valid(row, time, 1, targets, rows, ignore_id)) continue;
-    target = targets[row + 1];
+    if (!ucr_causal_ce_row_valid(row, time, horizon, targets, rows, ignore_id)) continue;
+    target = targets[row + horizon];
     h = hidden + row * d;
     ucr_packed_forward(h, 1, d, vocab, bits, scale, bias, logits);
     for (v = 0; v < vocab; ++v) mx = fmaxf(mx, logits[v]);
@@ -431,6 +443,135 @@ int ucr_head_ce(const float* hidden, size_t rows, size_t time, size_t d, size_t 
   free(exps);
   free(gy);
   return 0;
+}
+
+/* ------------------------------------------------ CausalLoss statistics ---- */
+
+/* rms, src/model.rs:3293-3299: sqrt(sum v^2 / n), sequential f32 sum */
+float ucr_rms(const float* v, size_t n) {
+  float s = 0.0f;
+  size_t i;
+  if (n == 0) return 0.0f;
+  for (i = 0; i < n; ++i) s += v[i] * v[i];
+  return sqrtf(s / (float)n);
+}
+
+/* rms_fp16, src/model.rs:3301-3312 */
+float ucr_rms_fp16(const uint16_t* v, size_t n) {
+  float s = 0.0f;
+  size_t i;
+  if (n == 0) return 0.0f;
+  for (i = 0; i < n; ++i) {
+    const float x = ucr_f16_to_f32(v[i]);
+    s += x * x;
+  }
+  return sqrtf(s / (float)n);
+}
+
+/* mean_abs, src/model.rs:3314-3319 */
+float ucr_mean_abs(const float* v, size_t n) {
+  float s = 0.0f;
+  size_t i;
+  if (n == 0) return 0.0f;
+  for (i = 0; i < n; ++i) s += fabsf(v[i]);
+  return s / (float)n;
+}
+
+/* mean_abs_fp16, src/model.rs:3321-3327 */
+float ucr_mean_abs_fp16(const uint16_t* v, size_t n) {
+  float s = 0.0f;
+  size_t i;
+  if (n == 0) return 0.0f;
+  for (i = 0; i < n; ++i) s += fabsf(ucr_f16_to_f32(v[i]));
+  return s / (float)n;
+}
+
+/* mean_abs_delta_fp16, src/model.rs:3329-3339 */
+float ucr_mean_abs_delta_fp16(const uint16_t* before, const uint16_t* after, size_t n) {
+  float s = 0.0f;
+  size_t i;
+  if (n == 0) return 0.0f;
+  for (i = 0; i < n; ++i) s += fabsf(ucr_f16_to_f32(before[i]) - ucr_f16_to_f32(after[i]));
+  return s / (float)n;
+}
+
+/* f32::total_cmp as an unsigned key */
+static uint32_t total_key(float v) {
+  const uint32_t b = f32_bits(v);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+static int cmp_total(const void* a, const void* b) {
+  const uint32_t ka = total_key(*(const float*)a), kb = total_key(*(const float*)b);
+  return ka < kb ? -1 : (ka > kb ? 1 : 0);
+}
+
+/* loss_percentiles, src/model.rs:3341-3363: finite losses of valid rows
+ * (horizon 1), sorted by total_cmp; p-th = valid[min(round(p (n-1)), n-1)]
+ * with the product and the rounding (half away from zero) in f32. */
+void ucr_loss_percentiles(const float* row_loss, size_t rows, size_t time, const uint32_t* targets,
+                          uint32_t ignore_id, float* out3) {
+  const float ps[3] = {0.10f, 0.50f, 0.90f};
+  float* valid = (float*)malloc((rows ? rows : 1) * sizeof(float));
+  size_t n = 0, row;
+  int q;
+  out3[0] = out3[1] = out3[2] = 0.0f;
+  if (!valid) return;
+  for (row = 0; row < rows; ++row) {
+    if (!ucr_causal_ce_row_valid(row, time, 1, targets, rows, ignore_id)) continue;
+    if (!isfinite(row_loss[row])) continue;
+    valid[n++] = row_loss[row];
+  }
+  if (n > 0) {
+    qsort(valid, n, sizeof(float), cmp_total);
+    for (q = 0; q < 3; ++q) {
+      size_t at = (size_t)roundf(ps[q] * (float)(n - 1));
+      if (at > n - 1) at = n - 1;
+      out3[q] = valid[at];
+    }
+  }
+  free(valid);
+}
+
+static int cmp_u32(const void* a, const void* b) {
+  const uint32_t x = *(const uint32_t*)a, y = *(const uint32_t*)b;
+  return x < y ? -1 : (x > y ? 1 : 0);
+}
+
+/* unigram_cross_entropy, src/model.rs:3365-3390: counts of targets[row + 1]
+ * over valid rows; ce = -sum count * ln(count / n) / n (f32). The reference
+ * iterates a HashMap, whose order is not fixed; here the counts are taken in
+ * ascending target order. */
+float ucr_unigram_cross_entropy(const uint32_t* targets, size_t rows, size_t time,
+                                uint32_t ignore_id, size_t* unique) {
+  uint32_t* ids = (uint32_t*)malloc((rows ? rows : 1) * sizeof(uint32_t));
+  size_t n = 0, row, i, u = 0;
+  float ce = 0.0f, nf;
+  *unique = 0;
+  if (!ids) return 0.0f;
+  for (row = 0; row < rows; ++row) {
+    if (!ucr_causal_ce_row_valid(row, time, 1, targets, rows, ignore_id)) continue;
+    ids[n++] = targets[row + 1];
+  }
+  if (n == 0) {
+    free(ids);
+    return 0.0f;
+  }
+  qsort(ids, n, sizeof(uint32_t), cmp_u32);
+  nf = (float)n;
+  for (i = 0; i < n;) {
+    size_t j = i;
+    float count, p;
+    while (j < n && ids[j] == ids[i]) ++j;
+    count = (float)(j - i);
+    p = count / nf;
+    ce -= count * logf(p);
+    u += 1;
+    i = j;
+  }
+  free(ids);
+  *unique = u;
+  return ce / nf;
 }
 
 /* --------------------------------------------------------------- a14 ---- */
@@ -716,6 +857,8 @@ int ucr_heron_train_step(const ullis_heron_dims* dims, uint8_t* arena, const flo
   float *g_x = NULL, *g_tmp = NULL, *g_tmp2 = NULL, *g_w = NULL, *g_scale = NULL, *g_bias = NULL;
   float *gw_ln = NULL, *gb_ln = NULL, *g_mix = NULL, *g_e = NULL, *g_f = NULL, *g_f2 = NULL;
   uint32_t* before = NULL;
+  uint16_t* before_latent = NULL;
+  float head_scale_grad_rms = 0.0f, head_latent_step_abs = 0.0f;
   uint64_t total;
   float mean_loss = 0.0f;
   size_t n_valid = 0, flips_head = 0, flips_cmix = 0, flips_rosa_o = 0;
@@ -751,6 +894,7 @@ int ucr_heron_train_step(const ullis_heron_dims* dims, uint8_t* arena, const flo
   XMALLOC(g_f, nf);
   XMALLOC(g_f2, nf);
   XMALLOC(before, ucr_packed_word_count(max_w));
+  XMALLOC(before_latent, v * d);
   for (layer = 0; layer < L; ++layer) {
     block_tape* tp = &tapes[layer];
     if (layer == 0) XMALLOC(tp->ln0_in, nd);
@@ -854,6 +998,8 @@ int ucr_heron_train_step(const ullis_heron_dims* dims, uint8_t* arena, const flo
     ucr_head_ce(hidden, rows, time, d, v, head.bits, head.scale, head.bias, labels, ignore_id,
                 &loss, &nv, row_loss, g_x, g_w, g_scale, g_bias);
     memcpy(before, head.bits, ucr_packed_word_count(v * d) * 4);
+    memcpy(before_latent, head.latent, v * d * sizeof(uint16_t));
+    head_scale_grad_rms = ucr_rms(g_scale, v); /* rms(&g_scale), src/model.rs:3270 */
     /* flip_after_gradients(g_w, g_scale, None, lr, ste) then head bias at 8x lr */
     ucr_packed_apply_sgd(d, v, head.latent, head.latent_res, head.scale, head.scale_res, NULL,
                          NULL, head.bits, g_w, g_scale, NULL, lr, (float)(time - 1));
@@ -861,6 +1007,7 @@ int ucr_heron_train_step(const ullis_heron_dims* dims, uint8_t* arena, const flo
       clipped_sgd_one(&head.bias[c], &head.bias_res[c], g_bias[c], lr * HEAD_BIAS_LR_MULT);
     }
     flips_head = ucr_bit_flip_count(before, head.bits, ucr_packed_word_count(v * d));
+    head_latent_step_abs = ucr_mean_abs_delta_fp16(before_latent, head.latent, v * d);
     mean_loss = loss;
     n_valid = nv;
   }
@@ -949,11 +1096,29 @@ int ucr_heron_train_step(const ullis_heron_dims* dims, uint8_t* arena, const flo
   }
   memcpy(g_emb, g_x, nd * sizeof(float));
   if (stats) {
+    /* CausalLoss, src/model.rs:2997-3024 */
+    uint16_t* value0;
+    size_t uniq = 0;
+    float pct[3];
     stats->mean_loss = mean_loss;
     stats->n_valid = n_valid;
     stats->flips_head = flips_head;
     stats->flips_cmix = flips_cmix;
     stats->flips_rosa_o = flips_rosa_o;
+    ucr_loss_percentiles(row_loss, rows, time, labels, ignore_id, pct);
+    stats->loss_p10 = pct[0];
+    stats->loss_p50 = pct[1];
+    stats->loss_p90 = pct[2];
+    stats->unigram_ce = ucr_unigram_cross_entropy(labels, rows, time, ignore_id, &uniq);
+    stats->unique_targets = uniq;
+    stats->embed_grad_rms = ucr_rms(g_emb, nd);
+    stats->head_scale_grad_rms = head_scale_grad_rms;
+    stats->head_scale_rms = ucr_rms_fp16(head.scale, v);
+    value0 = tensor_ptr(&a, "blocks.0.ffn.value");
+    stats->cmix_value_rms = value0 ? ucr_rms_fp16(value0, d * f) : 0.0f;
+    stats->head_latent_abs_mean = ucr_mean_abs_fp16(head.latent, v * d);
+    stats->head_latent_step_abs = head_latent_step_abs;
+    stats->head_bias_rms = head.bias ? ucr_rms_fp16(head.bias, v) : 0.0f;
   }
 
 done:
@@ -990,6 +1155,7 @@ done:
   free(g_f);
   free(g_f2);
   free(before);
+  free(before_latent);
   free(a.descs);
   return rc;
 }

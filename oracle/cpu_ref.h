@@ -74,6 +74,25 @@ int ucr_head_ce(const float* hidden, size_t rows, size_t time, size_t d, size_t 
                 const uint32_t* bits, const uint16_t* scale, const uint16_t* bias,
                 const uint32_t* targets, uint32_t ignore_id, float* mean_loss, size_t* n_valid,
                 float* row_loss, float* g_hidden, float* g_w, float* g_scale, float* g_bias);
+/* the same with the target of row r at targets[r + horizon] (horizon 1 above) */
+int ucr_head_ce_horizon(const float* hidden, size_t rows, size_t time, size_t horizon, size_t d,
+                        size_t vocab, const uint32_t* bits, const uint16_t* scale,
+                        const uint16_t* bias, const uint32_t* targets, uint32_t ignore_id,
+                        float* mean_loss, size_t* n_valid, float* row_loss, float* g_hidden,
+                        float* g_w, float* g_scale, float* g_bias);
+
+/* CausalLoss statistics (src/model.rs:3293-3390) */
+float ucr_rms(const float* v, size_t n);
+float ucr_rms_fp16(const uint16_t* v, size_t n);
+float ucr_mean_abs(const float* v, size_t n);
+float ucr_mean_abs_fp16(const uint16_t* v, size_t n);
+float ucr_mean_abs_delta_fp16(const uint16_t* before, const uint16_t* after, size_t n);
+/* p10 / p50 / p90 of the finite losses of valid rows (horizon 1) */
+void ucr_loss_percentiles(const float* row_loss, size_t rows, size_t time, const uint32_t* targets,
+                          uint32_t ignore_id, float* out3);
+/* CE of the batch's target unigram over valid rows; *unique = distinct targets */
+float ucr_unigram_cross_entropy(const uint32_t* targets, size_t rows, size_t time,
+                                uint32_t ignore_id, size_t* unique);
 
 /* a14: FP16 linear (CMix value) */
 int ucr_fp16_forward(const float* x, size_t rows, size_t in, size_t out, const uint16_t* w,
@@ -91,12 +110,24 @@ int ucr_rosa_y_from_idx(const uint8_t* idx, const uint16_t* e, size_t rows, size
 int ucr_rosa_e_grad(const float* g_y, const uint8_t* idx, size_t rows, size_t ch, float* g_e);
 
 /* a17: one Heron train step on the parameter arena, embedding excluded */
+/* The CausalLoss fields train_step_on fills (src/model.rs:2997-3024), except
+ * residual_abs_mean (the embedding carry, outside the arena). */
 typedef struct ucr_step_stats {
   float mean_loss;
   uint64_t n_valid;
   uint64_t flips_head;
   uint64_t flips_cmix;
   uint64_t flips_rosa_o;
+  float loss_p10, loss_p50, loss_p90;
+  float unigram_ce;
+  uint64_t unique_targets;
+  float embed_grad_rms;
+  float head_scale_grad_rms;
+  float head_scale_rms;
+  float cmix_value_rms;
+  float head_latent_abs_mean;
+  float head_latent_step_abs;
+  float head_bias_rms;
 } ucr_step_stats;
 
 int ucr_heron_train_step(const ullis_heron_dims* dims, uint8_t* arena, const float* x_emb,

@@ -33,7 +33,13 @@ class TensorDesc(C.Structure):
 
 class StepStats(C.Structure):
     _fields_ = [("mean_loss", C.c_float), ("n_valid", C.c_uint64), ("flips_head", C.c_uint64),
-                ("flips_cmix", C.c_uint64), ("flips_rosa_o", C.c_uint64)]
+                ("flips_cmix", C.c_uint64), ("flips_rosa_o", C.c_uint64),
+                ("loss_p10", C.c_float), ("loss_p50", C.c_float), ("loss_p90", C.c_float),
+                ("unigram_ce", C.c_float), ("unique_targets", C.c_uint64),
+                ("embed_grad_rms", C.c_float), ("head_scale_grad_rms", C.c_float),
+                ("head_scale_rms", C.c_float), ("cmix_value_rms", C.c_float),
+                ("head_latent_abs_mean", C.c_float), ("head_latent_step_abs", C.c_float),
+                ("head_bias_rms", C.c_float)]
 
 
 _LIB = None
@@ -55,6 +61,10 @@ def lib() -> C.CDLL:
         _LIB.ucr_causal_ce_row_valid.argtypes = [C.c_size_t, C.c_size_t, C.c_size_t, C.c_void_p,
                                                  C.c_size_t, C.c_uint32]
         _LIB.ucr_bit_flip_count.restype = C.c_size_t
+        for name in ["ucr_rms", "ucr_rms_fp16", "ucr_mean_abs", "ucr_mean_abs_fp16",
+                     "ucr_mean_abs_delta_fp16", "ucr_unigram_cross_entropy"]:
+            getattr(_LIB, name).restype = C.c_float
+        _LIB.ucr_head_ce_horizon.restype = C.c_int
         _LIB.ucr_heron_layout.restype = C.c_size_t
         _LIB.ucr_heron_layout.argtypes = [C.POINTER(HeronDims), C.POINTER(TensorDesc), C.c_size_t,
                                           C.POINTER(C.c_uint64)]
@@ -203,7 +213,7 @@ def causal_ce_gradient_scale(n_valid, time):
     return lib().ucr_causal_ce_gradient_scale(n_valid, time)
 
 
-def head_ce(hidden, rows, time, d, vocab, bits, scale, bias, targets, ignore_id):
+def head_ce(hidden, rows, time, d, vocab, bits, scale, bias, targets, ignore_id, horizon=1):
     h, b, s, t = _f32(hidden), _u32(bits), _u16(scale), _u32(targets)
     bb = None if bias is None else _u16(bias)
     mean = C.c_float()
@@ -213,13 +223,57 @@ def head_ce(hidden, rows, time, d, vocab, bits, scale, bias, targets, ignore_id)
     g_w = np.zeros(vocab * d, np.float32)
     g_s = np.zeros(vocab, np.float32)
     g_b = np.zeros(vocab, np.float32) if bias is not None else None
-    rc = lib().ucr_head_ce(_p(h), _sz(rows), _sz(time), _sz(d), _sz(vocab), _p(b), _p(s), _p(bb),
-                           _p(t), C.c_uint32(ignore_id), C.byref(mean), C.byref(nv), _p(row_loss),
-                           _p(g_h), _p(g_w), _p(g_s), _p(g_b))
+    rc = lib().ucr_head_ce_horizon(_p(h), _sz(rows), _sz(time), _sz(horizon), _sz(d), _sz(vocab),
+                                   _p(b), _p(s), _p(bb), _p(t), C.c_uint32(ignore_id),
+                                   C.byref(mean), C.byref(nv), _p(row_loss), _p(g_h), _p(g_w),
+                                   _p(g_s), _p(g_b))
     assert rc == 0
     return {"mean_loss": mean.value, "n_valid": nv.value, "row_loss": row_loss,
             "hidden_gradient": g_h, "weight_gradient": g_w, "scale_gradient": g_s,
             "bias_gradient": g_b}
+
+
+# ---------------------------------------------------- CausalLoss statistics
+def rms(v) -> float:
+    v = _f32(v).ravel()
+    return lib().ucr_rms(_p(v), _sz(v.size))
+
+
+def rms_fp16(bits) -> float:
+    b = _u16(bits).ravel()
+    return lib().ucr_rms_fp16(_p(b), _sz(b.size))
+
+
+def mean_abs(v) -> float:
+    v = _f32(v).ravel()
+    return lib().ucr_mean_abs(_p(v), _sz(v.size))
+
+
+def mean_abs_fp16(bits) -> float:
+    b = _u16(bits).ravel()
+    return lib().ucr_mean_abs_fp16(_p(b), _sz(b.size))
+
+
+def mean_abs_delta_fp16(before, after) -> float:
+    a, b = _u16(before).ravel(), _u16(after).ravel()
+    assert a.size == b.size
+    return lib().ucr_mean_abs_delta_fp16(_p(a), _p(b), _sz(a.size))
+
+
+def loss_percentiles(row_loss, time, targets, ignore_id):
+    rl, t = _f32(row_loss).ravel(), _u32(targets).ravel()
+    out = np.zeros(3, np.float32)
+    lib().ucr_loss_percentiles(_p(rl), _sz(rl.size), _sz(time), _p(t), C.c_uint32(ignore_id),
+                               _p(out))
+    return tuple(float(x) for x in out)
+
+
+def unigram_cross_entropy(targets, time, ignore_id):
+    t = _u32(targets).ravel()
+    u = C.c_size_t()
+    ce = lib().ucr_unigram_cross_entropy(_p(t), _sz(t.size), _sz(time), C.c_uint32(ignore_id),
+                                         C.byref(u))
+    return float(ce), int(u.value)
 
 
 # ---------------------------------------------------------------- a14 - a16
@@ -308,6 +362,6 @@ def heron_train_step(dims: HeronDims, arena: np.ndarray, x_emb, labels, ignore_i
                                     _p(row_loss), _p(qkv), C.byref(st))
     if rc != 0:
         raise RuntimeError(f"ucr_heron_train_step failed: {rc}")
-    return {"g_emb": g_emb, "row_loss": row_loss, "qkv_bits": qkv, "mean_loss": st.mean_loss,
-            "n_valid": st.n_valid, "flips_head": st.flips_head, "flips_cmix": st.flips_cmix,
-            "flips_rosa_o": st.flips_rosa_o}
+    out = {"g_emb": g_emb, "row_loss": row_loss, "qkv_bits": qkv}
+    out.update({name: getattr(st, name) for name, _ in StepStats._fields_})
+    return out

@@ -52,7 +52,9 @@ def test_null_context_is_rejected_without_a_gpu():
     rc = lib.ullis_hip_binary_linear(None, None, 1, None, None, None, 1, 1, 1, None, None)
     assert rc == -1
     assert lib.ullis_hip_sync(None) == -1
-    assert lib.ullis_hip_heron_step(None, None, None, 0, 0.01, None, None, None, None, None) == -1
+    assert lib.ullis_hip_heron_step(None, None, None, 0, 0.01, None, None, None, None, None,
+                                    None) == -1
+    assert lib.ullis_hip_heron_causal_loss(None, None, None, 0, None, None, 0, None) == -1
 
 
 class _FakeLib:

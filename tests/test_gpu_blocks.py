@@ -40,6 +40,17 @@ def rel(a, r):
     return float(np.max(np.abs(a - r))) / max(float(np.max(np.abs(r))), 1e-30)
 
 
+def record_drift(case: str, drift: dict) -> None:
+    """Writes one case's measured drift to gpurun_out/block_drift/<case>.json
+    (the figures the bounds above rest on)."""
+    import json
+    import pathlib
+
+    out = pathlib.Path(__file__).resolve().parent.parent / "gpurun_out" / "block_drift"
+    out.mkdir(parents=True, exist_ok=True)
+    (out / f"{case}.json").write_text(json.dumps(drift, indent=1, sort_keys=True))
+
+
 def bit_frac(a, b, n):
     return float(np.mean(unpack_bits(a, n) != unpack_bits(b, n)))
 
@@ -103,20 +114,112 @@ def test_cmix_block_forward_backward_match_oracle(rt, batch, time, d, f):
         None, pb["weight_gradient"], pb["scale_gradient"], None, lr, ste)
     g_x, g_mix = o.lerp_shift_backward(o.time_shift_delta(x, batch, time, d), c["mix"],
                                        pb["input_gradient"], batch, time, d)
-    assert rel(bwd["g_x"], g_x) <= BLOCK_REL
-    assert rel(bwd["g_mix"], g_mix) <= BLOCK_REL
-    assert rel(bwd["g_key_scale"], pb["scale_gradient"]) <= BLOCK_REL
     v0 = effective(c["value"], c["value_residual"])
-    assert rel(effective(bwd["next_value_weight"], bwd["next_value_residual"]) - v0,
-               effective(v_new, v_res) - v0) <= UPDATE_REL
     k0 = effective(c["key_latent"], c["key_residual"])
-    assert rel(effective(bwd["next_key_latent"], bwd["next_key_residual"]) - k0,
-               effective(lat, lat_res) - k0) <= UPDATE_REL
+    drift = {
+        "out": rel(fwd["out"], out),
+        "g_x": rel(bwd["g_x"], g_x),
+        "g_mix": rel(bwd["g_mix"], g_mix),
+        "g_key_scale": rel(bwd["g_key_scale"], pb["scale_gradient"]),
+        "value_step": rel(effective(bwd["next_value_weight"], bwd["next_value_residual"]) - v0,
+                          effective(v_new, v_res) - v0),
+        "key_step": rel(effective(bwd["next_key_latent"], bwd["next_key_residual"]) - k0,
+                        effective(lat, lat_res) - k0),
+        "key_bits_frac": bit_frac(bwd["next_key_bits"], bits_new, f * d),
+    }
+    record_drift(f"cmix_b{batch}t{time}d{d}f{f}", drift)
+    assert drift["g_x"] <= BLOCK_REL
+    assert drift["g_mix"] <= BLOCK_REL
+    assert drift["g_key_scale"] <= BLOCK_REL
+    assert drift["value_step"] <= UPDATE_REL
+    assert drift["key_step"] <= UPDATE_REL
     # bits are the repack of the updated latent; bits_t their transpose
     np.testing.assert_array_equal(bwd["next_key_bits"], o.pack_latent_bits(bwd["next_key_latent"]))
     np.testing.assert_array_equal(bwd["next_key_bits_t"],
                                   o.transpose_bits(bwd["next_key_bits"], f, d))
     assert bit_frac(bwd["next_key_bits"], bits_new, f * d) <= BITS_FRAC
+
+
+def test_cmix_block_backward_nonfinite_gradient_matches_oracle(rt):
+    """A NaN and an Inf in the upstream gradient of a CMix block
+    (src/model.rs:1145-1177): every gradient is NaN / Inf / finite where the
+    oracle's is; the value weight's clipped SGD takes +-Inf as a +-1 step and
+    NaN into the canonical quiet NaN (src/precision.rs:29-31, 106-113), bit
+    for bit with the oracle on those elements; the key latent's BinaryConnect
+    step leaves every weight with a non-finite gradient exactly as it was
+    (src/precision.rs:125-127). The key scale gradient of an Inf row is
+    non-finite on both sides (the reference's sum order gives +-Inf, the
+    identity sum_i sign G gives NaN here)."""
+    batch, time, d, f = 1, 64, 64, 128
+    rows = batch * time
+    lr, ste = 0.01, float(time - 1)
+    # a seed whose keys in the two injected rows are clear of zero, so the
+    # ReLU^2 zero pattern (Inf * 0 = NaN) is the same on both sides
+    for seed in range(100, 200):
+        rng = np.random.default_rng(seed)
+        c = cmix_case(rng, batch, time, d, f)
+        key_bits = o.pack_latent_bits(c["key_latent"])
+        x = h2f(c["x16"])
+        shifted = mixed(x, c["mix"], batch, time, d)
+        key = o.packed_forward(shifted, rows, d, f, key_bits, c["key_scale"]).reshape(rows, f)
+        w_row = c["value"].reshape(d, f)[20]  # the Inf's column meets this weight row
+        if np.abs(key[[9, 40]]).min() > 5e-3 and ((w_row & 0x7FFF) != 0).all():
+            break
+    c["gy"][9 * d + 3] = np.nan
+    c["gy"][40 * d + 20] = np.inf
+    fwd = rt.cmix_block_forward(c["x16"], c["mix"], key_bits, c["key_scale"], c["value"], batch,
+                                time, d, f)
+    bwd = rt.cmix_block_backward_sgd(fwd["gpu_tape"], c["gy"], c["mix"], key_bits, c["key_scale"],
+                                     c["key_latent"], c["key_residual"], c["value"],
+                                     c["value_residual"], batch, time, d, f, lr, ste)
+    relu2 = np.maximum(key.ravel(), 0.0) ** 2
+    g_relu2, g_value = o.fp16_backward(relu2, c["gy"], rows, f, d, c["value"])
+    v_new, v_res = o.clipped_sgd(c["value"], c["value_residual"], g_value, lr)
+    g_key = np.where(key.ravel() > 0, g_relu2 * 2.0 * key.ravel(), 0.0).astype(np.float32)
+    pb = o.packed_backward_ste(shifted, g_key, rows, d, f, key_bits, c["key_scale"], want_gb=False)
+    lat, lat_res, _, _, _, _, _ = o.packed_apply_sgd(
+        d, f, c["key_latent"], c["key_residual"], c["key_scale"], np.zeros(f, np.float32), None,
+        None, pb["weight_gradient"], pb["scale_gradient"], None, lr, ste)
+    g_x, g_mix = o.lerp_shift_backward(o.time_shift_delta(x, batch, time, d), c["mix"],
+                                       pb["input_gradient"], batch, time, d)
+
+    def masks_and_finite(a, r, name, tol=BLOCK_REL):
+        a, r = np.asarray(a, np.float64), np.asarray(r, np.float64)
+        for m in (np.isnan, np.isposinf, np.isneginf):
+            np.testing.assert_array_equal(m(a), m(r), err_msg=f"{name} {m.__name__}")
+        fin = np.isfinite(r)
+        if fin.any():  # g_mix sums over every row: all of it is NaN here
+            assert rel(a[fin], r[fin]) <= tol, name
+
+    masks_and_finite(bwd["g_x"], g_x, "g_x")
+    masks_and_finite(bwd["g_mix"], g_mix, "g_mix")
+    np.testing.assert_array_equal(np.isfinite(bwd["g_key_scale"]),
+                                  np.isfinite(pb["scale_gradient"]))
+    assert not np.isfinite(bwd["g_key_scale"]).all()
+    # value weight: non-finite gradients give the oracle's bits exactly
+    gv = np.asarray(g_value)
+    nan, inf = np.isnan(gv), np.isinf(gv)
+    assert nan.any() and inf.any()
+    nv = bwd["next_value_weight"]
+    np.testing.assert_array_equal(nv[inf], v_new[inf])
+    np.testing.assert_array_equal(bwd["next_value_residual"][inf].view(np.uint32),
+                                  v_res[inf].view(np.uint32))
+    assert ((nv[nan] & 0x7FFF) == 0x7E00).all() and np.isnan(bwd["next_value_residual"][nan]).all()
+    fin = np.isfinite(gv)
+    v0 = effective(c["value"], c["value_residual"])[fin]
+    assert rel(effective(nv, bwd["next_value_residual"])[fin] - v0,
+               effective(v_new, v_res)[fin] - v0) <= UPDATE_REL
+    # key latent: weights with a non-finite gradient keep latent and carry
+    gk = np.asarray(pb["weight_gradient"])
+    skip = ~np.isfinite(gk)
+    assert skip.any()
+    np.testing.assert_array_equal(bwd["next_key_latent"][skip], c["key_latent"][skip])
+    np.testing.assert_array_equal(bwd["next_key_residual"][skip].view(np.uint32),
+                                  c["key_residual"][skip].view(np.uint32))
+    np.testing.assert_array_equal(lat[skip], c["key_latent"][skip])
+    k0 = effective(c["key_latent"], c["key_residual"])[~skip]
+    assert rel(effective(bwd["next_key_latent"], bwd["next_key_residual"])[~skip] - k0,
+               effective(lat, lat_res)[~skip] - k0) <= UPDATE_REL
 
 
 def rosa_case(rng, batch, time, d):
@@ -176,12 +279,21 @@ def test_rosa_block_forward_and_o_stop_grad_match_oracle(rt, batch, time, d):
     lat, lat_res, _, _, _, _, bits_new = o.packed_apply_sgd(
         d, d, c["latent"], c["residual"], op["scale"], np.zeros(d, np.float32), None, None,
         pb["weight_gradient"], pb["scale_gradient"], None, lr, ste)
-    assert rel(bwd["e_gradient"], g_e) <= BLOCK_REL
-    assert rel(bwd["scale_gradient"], pb["scale_gradient"]) <= BLOCK_REL
-    assert rel(bwd["bias_gradient"], pb["bias_gradient"]) <= 1e-5  # fp32 column sums
     l0 = effective(c["latent"], c["residual"])
-    assert rel(effective(bwd["next_latent"], bwd["next_residual"]) - l0,
-               effective(lat, lat_res) - l0) <= UPDATE_REL
+    drift = {
+        "out": rel(fwd["out"], out),
+        "e_gradient": rel(bwd["e_gradient"], g_e),
+        "scale_gradient": rel(bwd["scale_gradient"], pb["scale_gradient"]),
+        "bias_gradient": rel(bwd["bias_gradient"], pb["bias_gradient"]),
+        "o_step": rel(effective(bwd["next_latent"], bwd["next_residual"]) - l0,
+                      effective(lat, lat_res) - l0),
+        "o_bits_frac": bit_frac(bwd["next_bits"], bits_new, d * d),
+    }
+    record_drift(f"rosa_b{batch}t{time}d{d}", drift)
+    assert drift["e_gradient"] <= BLOCK_REL
+    assert drift["scale_gradient"] <= BLOCK_REL
+    assert drift["bias_gradient"] <= 1e-5  # fp32 column sums
+    assert drift["o_step"] <= UPDATE_REL
     np.testing.assert_array_equal(bwd["next_bits"], o.pack_latent_bits(bwd["next_latent"]))
     np.testing.assert_array_equal(bwd["next_bits_t"], o.transpose_bits(bwd["next_bits"], d, d))
     assert bit_frac(bwd["next_bits"], bits_new, d * d) <= BITS_FRAC

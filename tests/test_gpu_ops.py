@@ -116,6 +116,64 @@ def test_binary_linear_backward_parity(rt, rows, in_f, out_f):
         assert rel(g[k], w[k]) <= REL, k
 
 
+def finite_rel_and_masks(a, r, name):
+    """Non-finite entries must sit where the oracle's are (NaN where NaN, +-Inf
+    where +-Inf); the finite ones within REL of the finite reference."""
+    a = np.asarray(a, np.float64)
+    r = np.asarray(r, np.float64)
+    np.testing.assert_array_equal(np.isnan(a), np.isnan(r), err_msg=name + " NaN mask")
+    np.testing.assert_array_equal(np.isposinf(a), np.isposinf(r), err_msg=name + " +Inf mask")
+    np.testing.assert_array_equal(np.isneginf(a), np.isneginf(r), err_msg=name + " -Inf mask")
+    fin = np.isfinite(r)
+    if fin.any():
+        assert rel(a[fin], r[fin]) <= REL, name
+
+
+@pytest.mark.parametrize("inject", ["nan", "inf"])
+def test_binary_linear_backward_nonfinite_gradient(rt, inject):
+    # A NaN or an Inf in the upstream gradient reaches the products as in the
+    # reference's fp32 arithmetic: the gradient's fp16 operand keeps it (the
+    # amax scale is taken over finite values only), so every output that sums
+    # over it is NaN / Inf exactly where the oracle's is, and the rest keeps
+    # the finite tolerance. One known divergence: for an Inf in column o the
+    # reference forms g_scale[o] = sum_r gy[r,o] (sum_i sign x[r,i]) = +-Inf,
+    # while here g_scale[o] = sum_i sign[o,i] G[o,i] adds +Inf and -Inf terms
+    # of G's row o and gives NaN; both are non-finite.
+    rows, in_f, out_f = 256, 128, 192
+    rng = np.random.default_rng(99)
+    x16, bits, scale, _ = rand_case(rng, rows, in_f, out_f)
+    x16[(x16 & 0x7FFF) == 0] = f16([0.5])[0]  # no Inf * 0 in the products
+    gy = rng.normal(0, 1e-2, rows * out_f).astype(np.float32)
+    if inject == "nan":
+        gy[17 * out_f + 5] = np.nan
+        gy[30 * out_f + 77] = np.uint32(0xFFC00000).view(np.float32)
+    else:
+        gy[101 * out_f + 77] = np.inf
+        gy[3 * out_f + 5] = -np.inf
+    g = rt.binary_linear_backward(x16, gy, bits, scale, True, rows, in_f, out_f)
+    w = o.packed_backward_ste(h2f32(x16), gy, rows, in_f, out_f, bits, scale)
+    for k in ["input_gradient", "weight_gradient", "bias_gradient"]:
+        finite_rel_and_masks(g[k], w[k], k)
+    if inject == "nan":
+        finite_rel_and_masks(g["scale_gradient"], w["scale_gradient"], "scale_gradient")
+    else:
+        np.testing.assert_array_equal(np.isfinite(g["scale_gradient"]),
+                                      np.isfinite(w["scale_gradient"]))
+        fin = np.isfinite(w["scale_gradient"])
+        assert rel(g["scale_gradient"][fin], w["scale_gradient"][fin]) <= REL
+    assert not np.isfinite(g["weight_gradient"][5 * in_f:6 * in_f]).any()
+    assert not np.isfinite(g["weight_gradient"][77 * in_f:78 * in_f]).any()
+    # the BinaryConnect step skips non-finite gradients (src/precision.rs:125-127)
+    lat = f16(rng.uniform(-0.01, 0.01, out_f * in_f))
+    res = np.zeros(out_f * in_f, np.float32)
+    gl, gr, _, _ = rt.apply_latent_sgd(lat, res, g["weight_gradient"], out_f, in_f, 0.01, 63.0)
+    bad = ~np.isfinite(g["weight_gradient"])
+    np.testing.assert_array_equal(gl[bad], lat[bad])
+    wl, wr = o.binaryconnect_sgd(lat, res, g["weight_gradient"], 0.01, 63.0)
+    np.testing.assert_array_equal(gl, wl)
+    np.testing.assert_array_equal(gr.view(np.uint32), wr.view(np.uint32))
+
+
 @pytest.mark.parametrize("rows,in_f,out_f", [(2048, 2048, 512), (2048, 512, 2048), (50, 24, 40)])
 def test_fp16_linear_parity(rt, rows, in_f, out_f):
     rng = np.random.default_rng(11 + rows + in_f)
@@ -186,11 +244,20 @@ def test_sgd_random_bit_exact(rt, lr):
     g[::97] = 0.0
     g[::101] = np.inf
     g[::103] = np.nan
-    gc = np.nan_to_num(g, posinf=3.0, nan=0.5)
-    a, b = rt.clipped_sgd_fp16(p, res, gc, lr)
-    wa, wb = o.clipped_sgd(p, res, gc, lr)
-    np.testing.assert_array_equal(a, wa)
-    np.testing.assert_array_equal(b.view(np.uint32), wb.view(np.uint32))
+    g[::107] = np.uint32(0xFFC00000).view(np.float32)  # negative quiet NaN
+    g[::109] = np.uint32(0x7FA00001).view(np.float32)  # NaN with a payload
+    g[::113] = -np.inf
+    # clipped SGD takes non-finite gradients as the reference does: +-Inf
+    # clamps to +-1 (bit-exact), NaN carries into the value as the canonical
+    # quiet NaN 0x7e00 (src/precision.rs:29-31) and into the carry. IEEE 754
+    # leaves the sign of a NaN result open (x86 and gfx950 differ in how a
+    # subtraction treats it), so NaN values are compared up to the sign bit.
+    a, b = rt.clipped_sgd_fp16(p, res, g, lr)
+    wa, wb = o.clipped_sgd(p, res, g, lr)
+    nan = np.isnan(g)
+    np.testing.assert_array_equal(a[~nan], wa[~nan])
+    np.testing.assert_array_equal(b[~nan].view(np.uint32), wb[~nan].view(np.uint32))
+    assert ((a[nan] & 0x7FFF) == 0x7E00).all() and np.isnan(b[nan]).all()
     a, b = rt.binaryconnect_sgd_fp16(p, res, g, lr)
     wa, wb = o.binaryconnect_sgd(p, res, g, lr)
     np.testing.assert_array_equal(a, wa)
@@ -255,6 +322,7 @@ def test_head_ce_metal_fixture(rt):
     (256, 64, 64, 1000, 0xFFFFFFFF),
     (512, 128, 128, 2500, 7),
     (256, 256, 512, 8192, 0xFFFFFFFF),  # config 3 widths (d 512, vocab 8192), 256 rows
+    (2048, 2048, 512, 8192, 0xFFFFFFFF),  # config 3 at full size (T = 2048)
 ])
 def test_head_ce_parity_and_update(rt, rows, time, d, vocab, ignore):
     rng = np.random.default_rng(rows + d + vocab)
@@ -288,6 +356,56 @@ def test_head_ce_parity_and_update(rt, rows, time, d, vocab, ignore):
     wbits = o.pack_latent_bits(wl)
     np.testing.assert_array_equal(got["next_bits"], wbits)
     np.testing.assert_array_equal(got["next_bits_t"], o.transpose_bits(wbits, vocab, d))
+
+
+@pytest.mark.parametrize("horizon", [2, 5])
+def test_head_ce_horizon_matches_oracle(rt, horizon):
+    # packed_head_train_sgd's horizon (src/metal.rs:3300-3316; causal_ce_row_valid,
+    # src/model.rs:27-39): row r is scored against targets[r + horizon]
+    rows, time, d, vocab = 256, 64, 64, 1000
+    rng = np.random.default_rng(40 + horizon)
+    hidden16 = f16(rng.standard_normal(rows * d))
+    lat = f16(rng.uniform(-0.01, 0.01, vocab * d))
+    bits = pack_bits(h2f32(lat) >= 0)
+    scale = f16(rng.uniform(0.005, 0.02, vocab))
+    targets = rng.integers(0, vocab, rows).astype(np.uint32)
+    targets[::9] = 3
+    got = rt.packed_head_train_sgd(hidden16, bits, scale, None, lat, np.zeros(vocab * d, np.float32),
+                                   np.zeros(vocab, np.float32), None, targets, rows, time, d,
+                                   vocab, 3, 0.0, 1.0, want_g_w=True, horizon=horizon)
+    want = o.head_ce(h2f32(hidden16), rows, time, d, vocab, bits, scale, None, targets, 3,
+                     horizon=horizon)
+    assert got["n_valid"] == want["n_valid"] < rows - rows // time
+    assert got["invalid"] == 0
+    assert np.max(np.abs(got["row_loss"] - want["row_loss"])) <= 1e-4
+    for k in ["hidden_gradient", "scale_gradient", "weight_gradient"]:
+        assert rel(got[k], want[k]) <= REL, k
+
+
+def test_head_ce_labels_outside_vocab_are_counted_and_left_out(rt):
+    # A label >= vocab (other than the ignore id) is refused by the reference's
+    # train step (src/model.rs:2852-2861). The unit op counts it and leaves the
+    # row out, which is the oracle's result with that label set to the ignore id.
+    rows, time, d, vocab = 128, 64, 64, 500
+    rng = np.random.default_rng(41)
+    hidden16 = f16(rng.standard_normal(rows * d))
+    lat = f16(rng.uniform(-0.01, 0.01, vocab * d))
+    bits = pack_bits(h2f32(lat) >= 0)
+    scale = f16(rng.uniform(0.005, 0.02, vocab))
+    targets = rng.integers(0, vocab, rows).astype(np.uint32)
+    targets[[10, 40, 0]] = [vocab, vocab + 7, 0xFFFFFFF0]
+    got = rt.packed_head_train_sgd(hidden16, bits, scale, None, lat, np.zeros(vocab * d, np.float32),
+                                   np.zeros(vocab, np.float32), None, targets, rows, time, d,
+                                   vocab, 0xFFFFFFFF, 0.0, 1.0, want_g_w=True)
+    assert got["invalid"] == 3
+    clean = targets.copy()
+    clean[[10, 40, 0]] = 0xFFFFFFFE
+    want = o.head_ce(h2f32(hidden16), rows, time, d, vocab, bits, scale, None, clean, 0xFFFFFFFE)
+    assert got["n_valid"] == want["n_valid"] == rows - 2 - 2
+    assert got["row_loss"][9] == 0.0 and got["row_loss"][39] == 0.0
+    assert np.max(np.abs(got["row_loss"] - want["row_loss"])) <= 1e-4
+    for k in ["hidden_gradient", "scale_gradient", "weight_gradient"]:
+        assert rel(got[k], want[k]) <= REL, k
 
 
 # -------------------------------------------------------------- device copy

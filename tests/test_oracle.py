@@ -67,8 +67,13 @@ def numpy_clipped(p_bits, res, g, lr):
     cur = np.asarray(p_bits, np.uint16).view(F16).astype(np.float32)
     upd = np.float32(lr) * np.clip(np.asarray(g, np.float32), np.float32(-1), np.float32(1))
     desired = (cur - upd) + np.asarray(res, np.float32)
-    rounded = desired.astype(F16)
-    return rounded.view(np.uint16), desired - rounded.astype(np.float32)
+    with np.errstate(invalid="ignore"):
+        rounded = desired.astype(F16)
+    bits = rounded.view(np.uint16).copy()
+    # Fp16::from_f32 (src/precision.rs:29-31): any NaN -> sign | 0x7e00
+    nan = np.isnan(desired)
+    bits[nan] = ((desired[nan].view(np.uint32) >> 16) & 0x8000).astype(np.uint16) | 0x7E00
+    return bits, desired - rounded.astype(np.float32)
 
 
 def numpy_binaryconnect(p_bits, res, g, lr):
@@ -116,10 +121,17 @@ def test_sgd_random_bit_exact_against_numpy(lr):
     g[::97] = 0.0
     g[::101] = np.inf
     g[::103] = np.nan
-    gp, gr = o.clipped_sgd(p, res, np.nan_to_num(g, posinf=3.0, nan=0.5), lr)
-    wp, wr = numpy_clipped(p, res, np.nan_to_num(g, posinf=3.0, nan=0.5), lr)
+    # non-finite gradients too: Inf clamps to +-1, NaN carries into value
+    # (canonical sign | 0x7e00) and residual (src/precision.rs:29-31, 106-113)
+    g[::107] = np.uint32(0xFFC00000).view(np.float32)
+    g[::109] = np.uint32(0x7FA00001).view(np.float32)
+    g[::113] = -np.inf
+    gp, gr = o.clipped_sgd(p, res, g, lr)
+    wp, wr = numpy_clipped(p, res, g, lr)
     np.testing.assert_array_equal(gp, wp)
-    np.testing.assert_array_equal(gr.view(np.uint32), wr.view(np.uint32))
+    nan = np.isnan(g)
+    assert np.isnan(gr[nan]).all() and ((gp[nan] & 0x7FFF) == 0x7E00).all()
+    np.testing.assert_array_equal(gr[~nan].view(np.uint32), wr[~nan].view(np.uint32))
     gp, gr = o.binaryconnect_sgd(p, res, g, lr)
     wp, wr = numpy_binaryconnect(p, res, g, lr)
     np.testing.assert_array_equal(gp, wp)
@@ -364,6 +376,89 @@ def test_head_ce_ignore_id_excludes_targets():
     valid = [r % time + 1 < time and t[r + 1] != 4 for r in range(rows)]
     assert out["n_valid"] == sum(valid)
     assert all(out["row_loss"][r] == 0.0 for r in range(rows) if not valid[r])
+
+
+def test_head_ce_horizon_float64():
+    # causal_ce_row_valid with horizon h (src/model.rs:27-39): row r is
+    # scored against targets[r + h] while r % T + h < T
+    rng = np.random.default_rng(13)
+    rows, time, d, vocab = 12, 6, 4, 7
+    plus = rng.integers(0, 2, vocab * d).astype(bool)
+    signs = np.where(plus, 1.0, -1.0).reshape(vocab, d)
+    hidden = rng.standard_normal(rows * d)
+    t = rng.integers(0, vocab, rows).astype(np.uint32)
+    for h in (1, 2, 3):
+        out = o.head_ce(hidden, rows, time, d, vocab, pack_bits(plus), f16([0.4] * vocab), None,
+                        t, 0xFFFFFFFF, horizon=h)
+        H = hidden.astype(np.float32).astype(np.float64).reshape(rows, d)
+        logits = h2f(f16([0.4]))[0] * H @ signs.T
+        valid = np.array([r % time + h < time and r + h < rows for r in range(rows)])
+        assert out["n_valid"] == valid.sum()
+        lse = np.log(np.exp(logits).sum(1))
+        want = np.where(valid, lse - logits[np.arange(rows), t[np.minimum(np.arange(rows) + h,
+                                                                           rows - 1)]], 0.0)
+        np.testing.assert_allclose(out["row_loss"], want, atol=2e-6)
+
+
+# ------------------------------------------------- CausalLoss statistics
+def test_causal_loss_statistics_float64():
+    # rms / rms_fp16 / mean_abs / mean_abs_fp16 / mean_abs_delta_fp16,
+    # src/model.rs:3293-3339, against float64 numpy
+    rng = np.random.default_rng(21)
+    v = rng.standard_normal(100_000).astype(np.float32) * 3
+    h = f16(rng.standard_normal(50_000) * 0.2)
+    h2 = f16(h.view(F16).astype(np.float64) + rng.standard_normal(50_000) * 1e-3)
+    hv = h.view(F16).astype(np.float64)
+    assert abs(o.rms(v) - np.sqrt(np.mean(v.astype(np.float64) ** 2))) <= 1e-4 * np.sqrt(
+        np.mean(v.astype(np.float64) ** 2))
+    assert abs(o.rms_fp16(h) - np.sqrt(np.mean(hv ** 2))) <= 1e-4 * np.sqrt(np.mean(hv ** 2))
+    assert abs(o.mean_abs(v) - np.mean(np.abs(v))) <= 1e-4 * np.mean(np.abs(v))
+    assert abs(o.mean_abs_fp16(h) - np.mean(np.abs(hv))) <= 1e-4 * np.mean(np.abs(hv))
+    d = np.mean(np.abs(hv - h2.view(F16).astype(np.float64)))
+    assert abs(o.mean_abs_delta_fp16(h, h2) - d) <= 1e-4 * d
+    assert o.rms(np.zeros(0, np.float32)) == 0.0 and o.mean_abs_fp16(np.zeros(0, np.uint16)) == 0.0
+
+
+def test_loss_percentiles_rank_rule():
+    # loss_percentiles, src/model.rs:3341-3363: finite losses of valid rows,
+    # total order, index min(round(p (n - 1)), n - 1) with f32 rounding half
+    # away from zero
+    rng = np.random.default_rng(22)
+    rows, time = 2048, 512
+    t = rng.integers(0, 50, rows).astype(np.uint32)
+    t[::11] = 7  # ignore id below
+    rl = (rng.standard_normal(rows) * 2 + 5).astype(np.float32)
+    rl[::37] = np.nan
+    rl[::41] = np.inf
+    rl[5] = -0.0
+    rl[6] = 0.0
+    got = o.loss_percentiles(rl, time, t, 7)
+    valid = [r for r in range(rows) if r % time + 1 < time and t[r + 1] != 7]
+    vals = np.sort(np.array([rl[r] for r in valid if np.isfinite(rl[r])], np.float64))
+    n = len(vals)
+    for p, g in zip((0.10, 0.50, 0.90), got):
+        x = np.float32(p) * np.float32(n - 1)
+        at = min(int(np.floor(x + 0.5)), n - 1)  # half away from zero (x >= 0)
+        assert g == vals[at], (p, g, vals[at])
+    assert o.loss_percentiles(rl, time, np.full(rows, 7, np.uint32), 7) == (0.0, 0.0, 0.0)
+
+
+def test_unigram_cross_entropy_float64():
+    # unigram_cross_entropy, src/model.rs:3365-3390
+    from collections import Counter
+
+    rng = np.random.default_rng(23)
+    rows, time = 1000, 100
+    t = rng.integers(0, 40, rows).astype(np.uint32)
+    t[::9] = 99
+    valid = [r for r in range(rows) if r % time + 1 < time and t[r + 1] != 99]
+    c = Counter(int(t[r + 1]) for r in valid)
+    n = len(valid)
+    want = -sum(k * np.log(k / n) for k in c.values()) / n
+    ce, uniq = o.unigram_cross_entropy(t, time, 99)
+    assert uniq == len(c)
+    assert abs(ce - want) <= 1e-5 * want
+    assert o.unigram_cross_entropy(np.full(10, 99, np.uint32), 5, 99) == (0.0, 0)
 
 
 # -------------------------------------------------------- a14 FP16 linear

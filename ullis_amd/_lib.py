@@ -41,6 +41,34 @@ class HeronDims(C.Structure):
     ]
 
 
+class CausalLoss(C.Structure):
+    """ullis_hip_causal_loss: CausalLoss of src/model.rs:58-80 (counts as u32)."""
+    _fields_ = [
+        ("next_token", C.c_float),
+        ("next_token_count", C.c_uint32),
+        ("binary_flip_count", C.c_uint32),
+        ("loss_p10", C.c_float),
+        ("loss_p50", C.c_float),
+        ("loss_p90", C.c_float),
+        ("unigram_ce", C.c_float),
+        ("unique_targets", C.c_uint32),
+        ("flips_head", C.c_uint32),
+        ("flips_cmix", C.c_uint32),
+        ("flips_rosa_o", C.c_uint32),
+        ("embed_grad_rms", C.c_float),
+        ("head_scale_grad_rms", C.c_float),
+        ("head_scale_rms", C.c_float),
+        ("residual_abs_mean", C.c_float),
+        ("cmix_value_rms", C.c_float),
+        ("head_latent_abs_mean", C.c_float),
+        ("head_latent_step_abs", C.c_float),
+        ("head_bias_rms", C.c_float),
+    ]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "ullis_hip_version": (i32, []),
@@ -71,8 +99,8 @@ SIGNATURES = {
     "ullis_hip_transpose_bits": (i32, [vp, vp, sz, sz, vp]),
     "ullis_hip_packed_head_train_sgd": (
         i32,
-        [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, u32, f32, f32,
-         vp, vp, vp, vp, vp, vp]),
+        [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, u32, f32, f32,
+         vp, vp, vp, vp, vp, vp, vp]),
     "ullis_hip_embedding_gather": (i32, [vp, vp, sz, sz, vp, sz, vp, vp]),
     "ullis_hip_embedding_scatter_sgd": (i32, [vp, vp, vp, sz, sz, vp, sz, vp, f32]),
     "ullis_hip_cmix_tape_bytes": (sz, [sz, sz, sz]),
@@ -92,7 +120,8 @@ SIGNATURES = {
     "ullis_hip_heron_destroy": (None, [vp]),
     "ullis_hip_heron_arena": (i32, [vp, C.POINTER(vp), C.POINTER(C.c_uint64)]),
     "ullis_hip_heron_refresh_derived": (i32, [vp]),
-    "ullis_hip_heron_step": (i32, [vp, vp, vp, u32, f32, vp, vp, vp, vp, vp]),
+    "ullis_hip_heron_step": (i32, [vp, vp, vp, u32, f32, vp, vp, vp, vp, vp, vp]),
+    "ullis_hip_heron_causal_loss": (i32, [vp, vp, vp, u32, vp, vp, sz, vp]),
     "ullis_hip_heron_step_tokens": (i32, [vp, vp, vp, sz, vp, vp, u32, f32, vp, vp, vp, vp, vp,
                                          vp, vp]),
     "ullis_hip_heron_set_graph": (i32, [vp, i32]),

@@ -44,12 +44,26 @@ def _compile(src: pathlib.Path) -> pathlib.Path:
     return obj
 
 
-def build(verbose: bool = True) -> pathlib.Path:
+def _stale(src: pathlib.Path) -> bool:
+    """An object is out of date when it is older than its source or any header."""
+    obj = BUILD / (src.stem + ".o")
+    if not obj.exists():
+        return True
+    t = obj.stat().st_mtime
+    headers = list(CSRC.glob("*.hpp")) + list((HERE.parent / "include").glob("*.h"))
+    return any(p.stat().st_mtime > t for p in [src, *headers])
+
+
+def build(verbose: bool = True, incremental: bool = False) -> pathlib.Path:
+    """Compiles every source (incremental: only sources whose object is out of
+    date) and links the library."""
     BUILD.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
-    jobs = min(len(sources), int(os.environ.get("MAX_JOBS", "8")))
+    todo = [s for s in sources if _stale(s)] if incremental else sources
+    jobs = min(max(len(todo), 1), int(os.environ.get("MAX_JOBS", "8")))
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
-        objs = list(pool.map(_compile, sources))
+        list(pool.map(_compile, todo))
+    objs = [BUILD / (s.stem + ".o") for s in sources]
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-o", str(tmp), *map(str, objs)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -62,4 +76,4 @@ def build(verbose: bool = True) -> pathlib.Path:
 
 
 if __name__ == "__main__":
-    build()
+    build(incremental="--incremental" in sys.argv[1:])

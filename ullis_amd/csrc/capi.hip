@@ -412,13 +412,16 @@ int ullis_hip_packed_head_train_sgd(ullis_hip_ctx* c, const uint16_t* hidden16, 
                                     uint16_t* latent, float* latent_residual,
                                     float* scale_residual, float* bias_residual,
                                     const uint32_t* targets, size_t rows, size_t time, size_t d,
-                                    size_t vocab, uint32_t ignore_id, float learning_rate,
-                                    float ste_scale, float* row_loss, float* stats4,
-                                    float* g_hidden, float* g_scale, float* g_bias, float* g_w) {
+                                    size_t vocab, size_t horizon, uint32_t ignore_id,
+                                    float learning_rate, float ste_scale, float* row_loss,
+                                    float* stats4, float* g_hidden, float* g_scale, float* g_bias,
+                                    float* g_w, uint32_t* invalid) {
   if (!c) return ULLIS_HIP_ERR_INVALID;
   if (int rc = check_linear(c, rows, d, vocab)) return rc;
   if (time == 0 || rows % time != 0)
     return c->fail(ULLIS_HIP_ERR_INVALID, "packed head SGD shape mismatch: rows % time != 0");
+  if (vocab > (size_t)UINT32_MAX || horizon > (size_t)INT32_MAX)
+    return c->fail(ULLIS_HIP_ERR_INVALID, "packed head SGD: vocab or horizon out of range");
   NEED(hidden16, "hidden");
   NEED(bits, "bits");
   NEED(scale, "scale");
@@ -459,6 +462,8 @@ int ullis_hip_packed_head_train_sgd(ullis_hip_ctx* c, const uint16_t* hidden16, 
   h.bias = bias;
   h.targets = targets;
   h.ignore_id = ignore_id;
+  h.horizon = (long)horizon;
+  h.invalid = invalid;
   h.row_loss = row_loss;
   h.stats = stats4;
   h.g_hidden = g_hidden;

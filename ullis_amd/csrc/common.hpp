@@ -29,6 +29,10 @@ constexpr float kHeadBiasLrMult = 8.0f;  // src/model.rs:97
 // exact, so dividing it back out in an epilogue is exact.
 constexpr int kGradTargetExp = 6;
 
+// amax is the largest FINITE |value| of the tensor (non-finite values are
+// left out of it and pass through the fp16 conversion as NaN / Inf, so they
+// reach the products and the updates as they do in the reference's fp32
+// arithmetic).
 __device__ __forceinline__ float grad_scale_from_amax(float amax) {
   if (!(amax > 0.0f) || !__builtin_isfinite(amax)) return 1.0f;
   int e;
@@ -36,7 +40,10 @@ __device__ __forceinline__ float grad_scale_from_amax(float amax) {
   return __builtin_ldexpf(1.0f, kGradTargetExp - e);
 }
 
+// Fp16::from_f32 (src/precision.rs:23-55): RNE with subnormals; a NaN becomes
+// the canonical quiet NaN 0x7e00 with the input's sign, whatever its payload.
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
+  if (__builtin_isnan(v)) return (uint16_t)(((__float_as_uint(v) >> 16) & 0x8000u) | 0x7e00u);
   half_t h = (half_t)v;
   return __builtin_bit_cast(uint16_t, h);
 }
@@ -45,10 +52,20 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
   return (float)__builtin_bit_cast(half_t, b);
 }
 
-// Saturating conversion for scaled gradients: never produces inf.
-__device__ __forceinline__ half_t f32_to_f16_sat(float v) {
-  v = __builtin_fminf(__builtin_fmaxf(v, -65504.0f), 65504.0f);
-  return (half_t)v;
+// Finite values clamped to the fp16 range; NaN and +-Inf pass unchanged (so a
+// non-finite gradient stays non-finite in the fp16 operand, as in fp32).
+__device__ __forceinline__ float clamp_f16_range(float v) {
+  return __builtin_isfinite(v) ? __builtin_fminf(__builtin_fmaxf(v, -65504.0f), 65504.0f) : v;
+}
+
+// Conversion of a scaled gradient to its fp16 operand: finite values saturate
+// (a finite value never becomes Inf), NaN and +-Inf are kept.
+__device__ __forceinline__ half_t f32_to_f16_sat(float v) { return (half_t)clamp_f16_range(v); }
+
+// |v| as it enters a gradient's amax: 0 for NaN and +-Inf (see
+// grad_scale_from_amax).
+__device__ __forceinline__ float finite_abs(float v) {
+  return __builtin_isfinite(v) ? __builtin_fabsf(v) : 0.0f;
 }
 
 __device__ __forceinline__ float clampf(float v, float lo, float hi) {
@@ -99,6 +116,12 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += (uint32_t)__shfl_xor((int)v, off, 64);
+  return v;
+}
+
 // Max over the 32 lanes of each half-wave (lanes 0-31 and 32-63 separately).
 __device__ __forceinline__ float halfwave_max(float v) {
 #pragma unroll
@@ -116,9 +139,9 @@ __device__ __forceinline__ float halfwave_sum(float v) {
 // bits is an exact, order-independent max.
 // The slot only grows, so a value not above a (possibly stale) read of it
 // cannot change it: skipping those atomics keeps same-address contention low.
+// Non-finite values are not counted (callers pass maxima of finite_abs).
 __device__ __forceinline__ void atomic_amax(float* slot, float v) {
-  v = __builtin_fabsf(v);
-  if (!(v >= 0.0f)) v = __builtin_inff();  // NaN: poison the scale deliberately
+  v = finite_abs(v);
   unsigned int* p = reinterpret_cast<unsigned int*>(slot);
   if (__float_as_uint(v) > __atomic_load_n(p, __ATOMIC_RELAXED))
     atomicMax(p, __float_as_uint(v));

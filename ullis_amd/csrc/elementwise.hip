@@ -70,7 +70,7 @@ __global__ __launch_bounds__(256) void amax_kernel(const float* x, long n, float
   float m = 0.0f;
   for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (long)gridDim.x * blockDim.x)
-    m = __builtin_fmaxf(m, __builtin_fabsf(x[i]));
+    m = __builtin_fmaxf(m, finite_abs(x[i]));
   m = wave_max(m);
   if ((threadIdx.x & 63) == 0) atomic_amax(slot, m);
 }

@@ -53,8 +53,10 @@ __global__ __launch_bounds__(256) void embedding_scatter_sgd_kernel(uint16_t* ta
                                                                     float* residual, int d,
                                                                     const uint32_t* tokens,
                                                                     int rows, uint32_t vocab,
-                                                                    const float* g, float lr) {
+                                                                    const float* g, float lr,
+                                                                    const uint32_t* abort) {
   const int r = blockIdx.x;
+  if (abort && *abort) return;  // refused step
   const uint32_t id = tokens[r];
   if (id >= vocab) return;
   const int lane = threadIdx.x & 63;
@@ -104,11 +106,11 @@ hipError_t embedding_gather(hipStream_t s, const uint16_t* table, long vocab, lo
 
 hipError_t embedding_scatter_sgd(hipStream_t s, uint16_t* table, float* residual, long vocab,
                                  long d, const uint32_t* tokens, long rows, const float* g,
-                                 float lr) {
+                                 float lr, const uint32_t* abort) {
   if (rows <= 0 || d <= 0) return hipSuccess;
   if (rows > INT32_MAX || vocab > (long)UINT32_MAX) return hipErrorInvalidValue;
   launch(embedding_scatter_sgd_kernel, dim3((unsigned)rows), dim3(256), 0, s, table, residual,
-         (int)d, tokens, (int)rows, (uint32_t)vocab, g, lr);
+         (int)d, tokens, (int)rows, (uint32_t)vocab, g, lr, abort);
   return hipGetLastError();
 }
 

@@ -38,19 +38,30 @@ hipError_t packed_backward_input_ex(hipStream_t s, const uint16_t* gy16, long ld
 
 namespace {
 
-__device__ __forceinline__ bool ce_row_valid(long row, long rows, long time,
-                                             const uint32_t* targets, uint32_t ignore_id) {
-  // causal_ce_row_valid(row, time, horizon = 1, ...), src/model.rs:27-39
-  if (time == 0 || row % time + 1 >= time) return false;
-  return row + 1 < rows && targets[row + 1] != ignore_id;
-}
+// causal_ce_row_valid(row, time, horizon, targets, ignore_id), src/model.rs:27-39,
+// with one addition: a target >= vocab (other than ignore_id) makes no row
+// valid. The reference refuses such a label before the step
+// (src/model.rs:2852-2861); here labels are device data, so those rows are
+// left out of the loss and the gradient, and ce_invalid_labels_kernel counts
+// them for the caller.
+struct CeRows {
+  long rows, time, horizon, vocab;
+  const uint32_t* targets;
+  uint32_t ignore_id;
+  __device__ __forceinline__ bool valid(long row) const {
+    if (time == 0 || row % time + horizon >= time) return false;
+    const long t = row + horizon;
+    if (t >= rows) return false;
+    const uint32_t id = targets[t];
+    return id != ignore_id && (long)id < vocab;
+  }
+  __device__ __forceinline__ long target(long row) const { return (long)targets[row + horizon]; }
+};
 
 struct EpiCeStats {
   const uint16_t* scale;
   const uint16_t* bias;
-  const uint32_t* targets;
-  uint32_t ignore_id;
-  long time;
+  CeRows ce;
   float* part_m;  // [M][nb32], nb32 = ceil(N / 32): one row's blocks contiguous
   float* part_s;
   float* tgt;     // [M]
@@ -79,9 +90,7 @@ struct EpiCeStats {
               part_m[(long)row * nb + cb] = m;
               part_s[(long)row * nb + cb] = ssum;
             }
-            if (colok && ce_row_valid(row, M, time, targets, ignore_id) &&
-                (long)targets[row + 1] == (long)col)
-              tgt[row] = logit;
+            if (colok && ce.valid(row) && ce.target(row) == (long)col) tgt[row] = logit;
           }
         }
       }
@@ -124,8 +133,8 @@ struct EpiCeStats {
       part_m[(long)row * nb + (col >> 5)] = mm;
       part_s[(long)row * nb + (col >> 5)] = ss;
     }
-    if (ce_row_valid(row, M, time, targets, ignore_id)) {
-      const long t = (long)targets[row + 1] - col;
+    if (ce.valid(row)) {
+      const long t = ce.target(row) - col;
       if (t >= 0 && t < 16 && col + t < N) {
 #pragma unroll
         for (int k = 0; k < 16; ++k)
@@ -138,9 +147,7 @@ struct EpiCeStats {
 struct EpiCeGrad {
   const uint16_t* scale;  // chunk-offset
   const uint16_t* bias;   // chunk-offset or null
-  const uint32_t* targets;
-  uint32_t ignore_id;
-  long time;
+  CeRows ce;
   long col_base;          // global vocab index of chunk column 0
   long vocab;
   const float* lse;
@@ -163,10 +170,10 @@ struct EpiCeGrad {
           const int row = row0 + i * 32 + mfma32_row(r, lane);
           if (row < M && colok) {
             float g = 0.0f;
-            if (ce_row_valid(row, M, time, targets, ignore_id)) {
+            if (ce.valid(row)) {
               const float logit = bi + sc * acc[i][j][r];
               const float p = expf(logit - lse[row]);
-              g = (long)targets[row + 1] == vcol ? p - 1.0f : p;
+              g = ce.target(row) == vcol ? p - 1.0f : p;
             }
             gy16[(long)row * N + col] = __builtin_bit_cast(uint16_t, (half_t)g);
             csum += g;
@@ -182,7 +189,7 @@ struct EpiCeGrad {
   __device__ void row16(int row, int col, float (&v)[16], int lane, int M, int N, float* buf,
                         int brow, int bcol) {
     const bool rok = row < M;
-    const bool valid = rok && ce_row_valid(row, M, time, targets, ignore_id);
+    const bool valid = rok && ce.valid(row);
     const bool full = col + 16 <= N && N % 8 == 0;
     float g[16];
     if (valid) {
@@ -195,7 +202,7 @@ struct EpiCeGrad {
         for (int k = 0; k < 16; ++k) bi[k] = 0.0f;
       }
       const float ls = lse[row];
-      const long t = (long)targets[row + 1] - (col_base + col);
+      const long t = ce.target(row) - (col_base + col);
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
         const float p = expf(bi[k] + sc[k] * v[k] - ls);
@@ -231,10 +238,9 @@ struct EpiCeGrad {
 
 // One wave per row: merge the per-block (max, sum-exp) pairs.
 __global__ __launch_bounds__(256) void ce_combine_kernel(const float* part_m, const float* part_s,
-                                                         long nb, long rows, long time,
-                                                         const uint32_t* targets,
-                                                         uint32_t ignore_id, const float* tgt,
+                                                         long nb, CeRows ce, const float* tgt,
                                                          float* lse, float* row_loss) {
+  const long rows = ce.rows;
   const int lane = threadIdx.x & 63;
   const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -252,20 +258,30 @@ __global__ __launch_bounds__(256) void ce_combine_kernel(const float* part_m, co
   if (lane == 0) {
     const float l = m + logf(s);
     lse[row] = l;
-    row_loss[row] = ce_row_valid(row, rows, time, targets, ignore_id) ? l - tgt[row] : 0.0f;
+    row_loss[row] = ce.valid(row) ? l - tgt[row] : 0.0f;
   }
 }
 
+// Adds to *invalid the number of targets that are neither ignore_id nor a
+// vocabulary index (every row, as the reference's check of labels does).
+__global__ __launch_bounds__(256) void ce_invalid_labels_kernel(const uint32_t* targets, long rows,
+                                                                long vocab, uint32_t ignore_id,
+                                                                uint32_t* invalid) {
+  const long r = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool bad = r < rows && targets[r] != ignore_id && (long)targets[r] >= vocab;
+  const unsigned long long m = __ballot(bad);
+  if ((threadIdx.x & 63) == 0 && m) atomicAdd(invalid, (uint32_t)__popcll(m));
+}
+
 // Single block: n_valid, loss sum (fixed-order tree), mean and gscale.
-__global__ __launch_bounds__(1024) void ce_mean_kernel(const float* row_loss, long rows, long time,
-                                                       const uint32_t* targets,
-                                                       uint32_t ignore_id, float* stats,
-                                                       float* stats2) {
+__global__ __launch_bounds__(1024) void ce_mean_kernel(const float* row_loss, CeRows ce,
+                                                       float* stats, float* stats2) {
+  const long rows = ce.rows, time = ce.time;
   __shared__ float ls[1024];
   __shared__ float nv[1024];
   float a = 0.0f, n = 0.0f;
   for (long r = threadIdx.x; r < rows; r += blockDim.x) {
-    if (ce_row_valid(r, rows, time, targets, ignore_id)) {
+    if (ce.valid(r)) {
       a += row_loss[r];
       n += 1.0f;
     }
@@ -388,15 +404,19 @@ hipError_t head_ce(hipStream_t s, const HeadCe& h, void* workspace) {
   hipError_t e;
 
   // 1. forward statistics (fills every part_m/part_s entry and tgt of valid rows)
-  EpiCeStats st{h.scale, h.bias, h.targets, h.ignore_id, h.time, w.part_m, w.part_s, w.tgt};
+  const CeRows ce{rows, h.time, h.horizon, V, h.targets, h.ignore_id};
+  if (h.invalid) {
+    launch(ce_invalid_labels_kernel, dim3((unsigned)cdiv(rows, 256)), dim3(256), 0, s, h.targets,
+           rows, V, h.ignore_id, h.invalid);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  EpiCeStats st{h.scale, h.bias, ce, w.part_m, w.part_s, w.tgt};
   if ((e = logits_gemm(s, h.hidden16, rows, d, h.bits, V, st)) != hipSuccess) return e;
   // 2. combine
   launch(ce_combine_kernel, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, w.part_m,
-                     w.part_s, nb32, rows, h.time, h.targets, h.ignore_id, w.tgt, w.lse,
-                     h.row_loss);
+                     w.part_s, nb32, ce, w.tgt, w.lse, h.row_loss);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  launch(ce_mean_kernel, dim3(1), dim3(1024), 0, s, h.row_loss, rows, h.time, h.targets,
-         h.ignore_id, h.stats, h.stats2);
+  launch(ce_mean_kernel, dim3(1), dim3(1024), 0, s, h.row_loss, ce, h.stats, h.stats2);
   if ((e = hipGetLastError()) != hipSuccess) return e;
 
   // 3. stream the vocabulary in chunks
@@ -408,7 +428,7 @@ hipError_t head_ce(hipStream_t s, const HeadCe& h, void* workspace) {
   for (long c0 = 0, ci = 0; c0 < V; c0 += vc, ++ci) {
     const long n = V - c0 < vc ? V - c0 : vc;
     const uint32_t* bits_rows = h.bits + (c0 * d) / 32;
-    EpiCeGrad gr{h.scale + c0, h.bias ? h.bias + c0 : nullptr, h.targets, h.ignore_id, h.time, c0,
+    EpiCeGrad gr{h.scale + c0, h.bias ? h.bias + c0 : nullptr, ce, c0,
                  V, w.lse, w.gy16, w.part_bias};
     if ((e = logits_gemm(s, h.hidden16, rows, d, bits_rows, n, gr)) != hipSuccess) return e;
     // g_hidden (+)= gscale * gy_chunk . (scale * S)_chunk and G_chunk =

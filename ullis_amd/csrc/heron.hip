@@ -105,6 +105,17 @@ struct ullis_hip_heron {
   float *g_x = nullptr, *g_a = nullptr, *g_b = nullptr;
   float *slots = nullptr, *stats = nullptr;
   float* row_loss = nullptr;
+  // this step's count of token ids >= vocab and labels >= vocab (other than
+  // the ignore id); when non-zero every update launch of the step returns
+  // without changing anything, as train_step_on refuses such a step before
+  // any update (src/model.rs:2852-2861)
+  uint32_t* invalid = nullptr;
+  // per-row diagnostics the packed finishes write (CausalLoss): sign-bit
+  // flips of every key / O / head row, the head rows' summed |latent step|,
+  // and the head's scale gradient
+  uint32_t *flips_key = nullptr, *flips_o = nullptr, *flips_head = nullptr;
+  float *step_head = nullptr, *gscale_head = nullptr;
+  void* diag_ws = nullptr;
   // gradient partials, one buffer per tensor, consumed by the end-of-step updates
   float *gp_value = nullptr, *gp_key = nullptr, *gp_o = nullptr, *gp_head = nullptr;
   float *pt_mix = nullptr, *pt_ln2 = nullptr, *pt_ob = nullptr, *pt_e = nullptr;
@@ -150,13 +161,14 @@ struct ullis_hip_heron {
   // step graph (ullis_hip_heron_set_graph): the launches of one step on both
   // streams, captured once and replayed while the step's arguments repeat
   struct StepArgs {
-    const void* p[7];
+    const void* p[11];
     uint32_t ignore_id;
     float lr;
+    long vocab;  // embedding rows of a step from token ids, else -1
     bool operator==(const StepArgs& o) const {
-      for (int i = 0; i < 7; ++i)
+      for (int i = 0; i < 11; ++i)
         if (p[i] != o.p[i]) return false;
-      return ignore_id == o.ignore_id && lr == o.lr;
+      return ignore_id == o.ignore_id && lr == o.lr && vocab == o.vocab;
     }
   };
   bool graph_on = false;
@@ -298,7 +310,8 @@ int build_update_jobs(ullis_hip_heron* h) {
   // packed latent / scale steps with the repack (rows of in % 32 == 0
   // weights), then the bit transpose
   auto packed = [&](const Packed& k, long row0, long rows, const float* part, int splits,
-                    const float* amax, const float* extra_mul) {
+                    const float* amax, const float* extra_mul, uint32_t* row_flips,
+                    float* row_step = nullptr, float* g_scale = nullptr) {
     PackedFinish f;
     f.part = part;
     f.splits = splits;
@@ -312,11 +325,13 @@ int build_update_jobs(ullis_hip_heron* h) {
     f.lr = 0.0f;
     f.latent = k.latent + row0 * k.in;
     f.latent_res = k.latent_res + row0 * k.in;
-    f.g_scale = nullptr;
+    f.g_scale = g_scale;
     f.g_w = nullptr;
     f.scale_upd = k.scale + row0;
     f.scale_res = k.scale_res + row0;
     f.bits_new = k.bits + row0 * k.in / 32;
+    f.row_flips = row_flips;
+    f.row_step = row_step;
     vec_ok = vec_ok && packed_finish_wave_ok(f);
     pj.push_back(FinishJob{f, pb});
     pb += finish_job_blocks(rows);
@@ -346,8 +361,9 @@ int build_update_jobs(ullis_hip_heron* h) {
     fj.push_back(F16Job{gpv, h->splits_value, nv, h->slots + l + 1, b.value, b.value_res, fb});
     fb += f16_job_blocks(nv);
     packed(b.key, 0, F, h->gp_key + l * h->splits_key * F * D, h->splits_key, h->slots + l + 1,
-           nullptr);
-    packed(b.o, 0, D, h->gp_o + l * h->splits_o * D * D, h->splits_o, h->slots + l, nullptr);
+           nullptr, h->flips_key + l * F);
+    packed(b.o, 0, D, h->gp_o + l * h->splits_o * D * D, h->splits_o, h->slots + l, nullptr,
+           h->flips_o + l * D);
     rebuild(b.key);
     rebuild(b.o);
     close_seg(st);
@@ -362,7 +378,7 @@ int build_update_jobs(ullis_hip_heron* h) {
     const int sp = head_ce_splits(R, D, V);
     for (long c0 = 0, ci = 0; c0 < V; c0 += vc, ++ci)
       packed(h->head, c0, V - c0 < vc ? V - c0 : vc, h->gp_head + ci * sp * vc * D, sp, nullptr,
-             h->stats + 2);
+             h->stats + 2, h->flips_head + c0, h->step_head + c0, h->gscale_head + c0);
   }
   rebuild(h->head);
   close_seg(tail);
@@ -405,11 +421,14 @@ int run_update_seg(ullis_hip_heron* h, hipStream_t s, int l, float lr) {
   ullis_hip_ctx* c = h->ctx;
   const ullis_hip_heron::UpdateSeg& g = h->seg[l];
   // vector steps (LN gamma / beta, x_k, O bias, e, head bias at 8 lr)
-  STEP(run_vec_jobs(s, h->vec_jobs + g.vec.j0, g.vec.n, g.vec.blocks, lr), "vector steps");
-  STEP(run_f16_jobs(s, h->f16_jobs + g.f16.j0, g.f16.n, g.f16.blocks, lr), "value steps");
-  STEP(run_finish_jobs(s, h->fin_jobs + g.fin.j0, g.fin.n, g.fin.blocks, lr),
+  STEP(run_vec_jobs(s, h->vec_jobs + g.vec.j0, g.vec.n, g.vec.blocks, lr, h->invalid),
+       "vector steps");
+  STEP(run_f16_jobs(s, h->f16_jobs + g.f16.j0, g.f16.n, g.f16.blocks, lr, h->invalid),
+       "value steps");
+  STEP(run_finish_jobs(s, h->fin_jobs + g.fin.j0, g.fin.n, g.fin.blocks, lr, h->invalid),
        "latent / scale steps");
-  STEP(run_trans_jobs(s, h->trans_jobs + g.trans.j0, g.trans.n, g.trans.blocks), "bits_t");
+  STEP(run_trans_jobs(s, h->trans_jobs + g.trans.j0, g.trans.n, g.trans.blocks, h->invalid),
+       "bits_t");
   return 0;
 }
 
@@ -529,6 +548,13 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
   add(4ul * R);              // row_loss
   add(4ul * words * 3 * L);  // qkv bit-planes
   add(head_ws);
+  add(4);                    // invalid
+  add(4ul * F * L);          // flips_key
+  add(4ul * D * L);          // flips_o
+  add(4ul * V);              // flips_head
+  add(4ul * V);              // step_head
+  add(4ul * V);              // gscale_head
+  add(diag_workspace_bytes(V));
   if (hipMalloc(&h->act, bytes) != hipSuccess) {
     (void)hipFree(h->arena);
     delete h;
@@ -571,6 +597,13 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
   h->row_loss = cv.take<float>(R);
   h->qkv = cv.take<uint32_t>(words * 3 * L);
   h->head_ws = cv.take<char>(head_ws);
+  h->invalid = cv.take<uint32_t>(1);
+  h->flips_key = cv.take<uint32_t>(F * L);
+  h->flips_o = cv.take<uint32_t>(D * L);
+  h->flips_head = cv.take<uint32_t>(V);
+  h->step_head = cv.take<float>(V);
+  h->gscale_head = cv.take<float>(V);
+  h->diag_ws = cv.take<char>(diag_workspace_bytes(V));
   if (int rc = build_update_jobs(h)) {
     ullis_hip_heron_destroy(h);
     return rc;
@@ -728,7 +761,7 @@ struct EmbedArgs {
 // the second stream's last updates.
 int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels,
                   uint32_t ignore_id, float lr, const uint8_t* rosa_idx, float* g_emb,
-                  float* row_loss, float* stats4, uint32_t* qkv_bits,
+                  float* row_loss, float* stats4, uint32_t* qkv_bits, uint32_t* invalid_out,
                   const EmbedArgs* emb = nullptr) {
   ullis_hip_ctx* c = h->ctx;
   hipStream_t s = c->stream;
@@ -742,6 +775,8 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
   bool ln0_now = false;
 
   STEP(fill_f32(s, h->slots, L + 2, 0.0f), "clear amax slots");
+  // a step from token ids has cleared the counter before its gather
+  if (!emb) STEP(fill_f32(s, reinterpret_cast<float*>(h->invalid), 1, 0.0f), "clear invalid");
   // y = (2 idx - 1) e (e is not updated before the step's end): layer 0's
   // here, the other layers' on the second stream after layer 0's O product
   STEP(rosa_expand_layers(s, rosa_idx, h->e_host.data(), h->e_dev, 1, B, T, D, h->y16, h->idx_rm),
@@ -845,6 +880,7 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
     hc.g_hidden = h->g_a;
     hc.ste = ste;
     hc.gpart_all = h->gp_head;
+    hc.invalid = h->invalid;  // labels >= vocab refuse the step's updates
     PROBED_SPAN(ULLIS_HIP_PROBE_HEAD_CE, head_ce(s, hc, h->head_ws), "head ce");
   }
   // LN_out backward (src/model.rs:2932-2937)
@@ -944,7 +980,7 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
         // and leave its batched job out
         ln0_now = true;
         STEP(layer_norm_param_finish(s, h->pt_ln0, nb, D, nullptr, nullptr, lr, b.ln0.w,
-                                     b.ln0.w_res, b.ln0.b, b.ln0.b_res),
+                                     b.ln0.w_res, b.ln0.b, b.ln0.b_res, h->invalid),
              "ln0 step");
       }
     } else if (l == 0) {
@@ -954,7 +990,7 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
 
   if (emb)
     STEP(embedding_scatter_sgd(s, emb->table, emb->residual, emb->vocab, D, emb->tokens, R, g_emb,
-                               lr),
+                               lr, h->invalid),
          "embedding scatter sgd");
   // the second stream's work is done before the updates and the step's end
   STEP(hipEventRecord(h->ev_join, h->side), "event");
@@ -966,6 +1002,88 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
     if (int rc = run_update_seg(h, s, (int)L + 1, lr)) return rc;
   for (const Packed* k : h->trans_generic)
     STEP(transpose_bits(s, k->bits, k->out, k->in, k->bits_t), "bits_t");
+  if (invalid_out) STEP(copy_device(s, invalid_out, h->invalid, sizeof(uint32_t)), "invalid");
+  return 0;
+}
+
+// One step's arguments: a step from gathered rows (ullis_hip_heron_step) or
+// from token ids (emb set: gather, step, scatter-SGD).
+struct StepCall {
+  const float* x_emb;
+  const uint32_t* labels;
+  uint32_t ignore_id;
+  float lr;
+  const uint8_t* rosa_idx;
+  float* g_emb;
+  float* row_loss;
+  float* stats4;
+  uint32_t* qkv_bits;
+  uint32_t* invalid;
+  bool from_tokens;
+  EmbedArgs emb;
+  ullis_hip_heron::StepArgs key() const {
+    ullis_hip_heron::StepArgs k{};
+    const void* p[] = {x_emb,    labels,   rosa_idx,     g_emb,           row_loss,
+                       stats4,   qkv_bits, invalid,      emb.table,       emb.residual,
+                       emb.tokens};
+    static_assert(sizeof(p) / sizeof(p[0]) == sizeof(k.p) / sizeof(k.p[0]), "step key");
+    for (size_t i = 0; i < sizeof(p) / sizeof(p[0]); ++i) k.p[i] = p[i];
+    k.ignore_id = ignore_id;
+    k.lr = lr;
+    k.vocab = from_tokens ? emb.vocab : -1;
+    return k;
+  }
+};
+
+int step_call_launches(ullis_hip_heron* h, const StepCall& sc) {
+  ullis_hip_ctx* c = h->ctx;
+  if (!sc.from_tokens)
+    return step_launches(h, sc.x_emb, sc.labels, sc.ignore_id, sc.lr, sc.rosa_idx, sc.g_emb,
+                         sc.row_loss, sc.stats4, sc.qkv_bits, sc.invalid);
+  // the refused-step counter starts the step here: the gather adds the token
+  // ids >= vocab, the head the labels >= vocab
+  STEP(fill_f32(c->stream, reinterpret_cast<float*>(h->invalid), 1, 0.0f), "clear invalid");
+  STEP(embedding_gather(c->stream, sc.emb.table, sc.emb.vocab, h->D, sc.emb.tokens, h->rows,
+                        const_cast<float*>(sc.x_emb), h->invalid),
+       "embedding gather");
+  return step_launches(h, sc.x_emb, sc.labels, sc.ignore_id, sc.lr, sc.rosa_idx, sc.g_emb,
+                       sc.row_loss, sc.stats4, sc.qkv_bits, sc.invalid, &sc.emb);
+}
+
+// Eager launches, or (step graph on) the captured graph of them, captured
+// again whenever the step's arguments change.
+int run_step(ullis_hip_heron* h, const StepCall& sc) {
+  ullis_hip_ctx* c = h->ctx;
+  // probed steps run eagerly: the probe times individual launches
+  if (!h->graph_on || h->probe != ULLIS_HIP_PROBE_NONE || t_launch_probe)
+    return step_call_launches(h, sc);
+  const ullis_hip_heron::StepArgs args = sc.key();
+  hipStream_t s = c->stream;
+  if (!h->graph_exec || !(args == h->graph_args)) {
+    if (h->graph_exec) {
+      // the previous graph may still be running
+      STEP(hipStreamSynchronize(s), "graph sync");
+      STEP(hipGraphExecDestroy(h->graph_exec), "graph destroy");
+      h->graph_exec = nullptr;
+    }
+    STEP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "graph capture");
+    const int rc = step_call_launches(h, sc);
+    hipGraph_t g = nullptr;
+    const hipError_t end = hipStreamEndCapture(s, &g);
+    if (rc) {
+      if (g) (void)hipGraphDestroy(g);
+      return rc;
+    }
+    if (int rc2 = c->hip(end, "graph capture end")) return rc2;
+    const hipError_t inst = hipGraphInstantiate(&h->graph_exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (int rc2 = c->hip(inst, "graph instantiate")) {
+      h->graph_exec = nullptr;
+      return rc2;
+    }
+    h->graph_args = args;
+  }
+  STEP(hipGraphLaunch(h->graph_exec, s), "graph launch");
   return 0;
 }
 
@@ -989,11 +1107,10 @@ int ullis_hip_heron_step_tokens(ullis_hip_heron* h, uint16_t* table, float* tabl
   if (!(lr > 0.0f) || !__builtin_isfinite(lr))
     return c->fail(ULLIS_HIP_ERR_INVALID,
                    "train step requires a positive learning rate and time >= 2");
-  STEP(embedding_gather(c->stream, table, (long)vocab, h->D, tokens, h->rows, x_emb, invalid),
-       "embedding gather");
-  const EmbedArgs emb{table, table_residual, (long)vocab, tokens};
-  return step_launches(h, x_emb, labels, ignore_id, lr, rosa_idx, g_emb, row_loss, stats4,
-                       qkv_bits, &emb);
+  const StepCall sc{x_emb,    labels, ignore_id, lr,   rosa_idx,
+                    g_emb,    row_loss, stats4, qkv_bits, invalid,
+                    true,     EmbedArgs{table, table_residual, (long)vocab, tokens}};
+  return run_step(h, sc);
 }
 
 int ullis_hip_heron_set_graph(ullis_hip_heron* h, int enable) {
@@ -1010,7 +1127,7 @@ int ullis_hip_heron_set_graph(ullis_hip_heron* h, int enable) {
 
 int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels,
                          uint32_t ignore_id, float lr, const uint8_t* rosa_idx, float* g_emb,
-                         float* row_loss, float* stats4, uint32_t* qkv_bits) {
+                         float* row_loss, float* stats4, uint32_t* qkv_bits, uint32_t* invalid) {
   if (!h) return ULLIS_HIP_ERR_INVALID;
   ullis_hip_ctx* c = h->ctx;
   if (!x_emb || !labels || !rosa_idx || !g_emb)
@@ -1018,39 +1135,42 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
   if (!(lr > 0.0f) || !__builtin_isfinite(lr))
     return c->fail(ULLIS_HIP_ERR_INVALID,
                    "train step requires a positive learning rate and time >= 2");
-  // probed steps run eagerly: the probe times individual launches
-  if (!h->graph_on || h->probe != ULLIS_HIP_PROBE_NONE || t_launch_probe)
-    return step_launches(h, x_emb, labels, ignore_id, lr, rosa_idx, g_emb, row_loss, stats4,
-                         qkv_bits);
-  const ullis_hip_heron::StepArgs args{
-      {x_emb, labels, rosa_idx, g_emb, row_loss, stats4, qkv_bits}, ignore_id, lr};
-  hipStream_t s = c->stream;
-  if (!h->graph_exec || !(args == h->graph_args)) {
-    if (h->graph_exec) {
-      // the previous graph may still be running
-      STEP(hipStreamSynchronize(s), "graph sync");
-      STEP(hipGraphExecDestroy(h->graph_exec), "graph destroy");
-      h->graph_exec = nullptr;
-    }
-    STEP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "graph capture");
-    const int rc = step_launches(h, x_emb, labels, ignore_id, lr, rosa_idx, g_emb, row_loss,
-                                 stats4, qkv_bits);
-    hipGraph_t g = nullptr;
-    const hipError_t end = hipStreamEndCapture(s, &g);
-    if (rc) {
-      if (g) (void)hipGraphDestroy(g);
-      return rc;
-    }
-    if (int rc2 = c->hip(end, "graph capture end")) return rc2;
-    const hipError_t inst = hipGraphInstantiate(&h->graph_exec, g, nullptr, nullptr, 0);
-    (void)hipGraphDestroy(g);
-    if (int rc2 = c->hip(inst, "graph instantiate")) {
-      h->graph_exec = nullptr;
-      return rc2;
-    }
-    h->graph_args = args;
-  }
-  STEP(hipGraphLaunch(h->graph_exec, s), "graph launch");
+  const StepCall sc{x_emb,  labels,   ignore_id, lr,    rosa_idx, g_emb,
+                    row_loss, stats4, qkv_bits,  invalid, false,  EmbedArgs{}};
+  return run_step(h, sc);
+}
+
+int ullis_hip_heron_causal_loss(ullis_hip_heron* h, const float* g_emb, const uint32_t* labels,
+                                uint32_t ignore_id, const float* row_loss,
+                                const float* table_residual, size_t table_elems,
+                                ullis_hip_causal_loss* out) {
+  if (!h) return ULLIS_HIP_ERR_INVALID;
+  ullis_hip_ctx* c = h->ctx;
+  if (!g_emb || !labels || !out)
+    return c->fail(ULLIS_HIP_ERR_INVALID, "causal_loss needs g_emb, labels and out");
+  if (table_elems > 0 && !table_residual)
+    return c->fail(ULLIS_HIP_ERR_INVALID, "causal_loss: table_elems without table_residual");
+  const long R = h->rows, D = h->D, F = h->F, V = h->V, L = h->L;
+  auto task = [](int kind, int field, int rms, const void* p, long n, long denom) {
+    return DiagTask{kind, field, rms, p, n, denom};
+  };
+  const DiagTask tasks[] = {
+      task(DiagTask::kSqF32, kDiagEmbedGradRms, 1, g_emb, R * D, R * D),
+      task(DiagTask::kSqF32, kDiagHeadScaleGradRms, 1, h->gscale_head, V, V),
+      task(DiagTask::kSqF16, kDiagHeadScaleRms, 1, h->head.scale, V, V),
+      task(DiagTask::kAbsF32, kDiagResidualAbsMean, 0, table_residual, (long)table_elems,
+           (long)table_elems),
+      task(DiagTask::kSqF16, kDiagCmixValueRms, 1, h->blocks[0].value, D * F, D * F),
+      task(DiagTask::kAbsF16, kDiagHeadLatentAbsMean, 0, h->head.latent, V * D, V * D),
+      task(DiagTask::kSumF32, kDiagHeadLatentStepAbs, 0, h->step_head, V, V * D),
+      task(DiagTask::kSqF16, kDiagHeadBiasRms, 1, h->head.bias, V, V),
+      task(DiagTask::kSumU32, kDiagFlipsHead, 0, h->flips_head, V, V),
+      task(DiagTask::kSumU32, kDiagFlipsCmix, 0, h->flips_key, L * F, L * F),
+      task(DiagTask::kSumU32, kDiagFlipsRosaO, 0, h->flips_o, L * D, L * D),
+  };
+  DiagArgs a{row_loss ? row_loss : h->row_loss, labels, R, h->time, V, ignore_id, h->stats, out};
+  STEP(causal_loss_diag(c->stream, a, tasks, (int)(sizeof(tasks) / sizeof(tasks[0])), h->diag_ws),
+       "causal loss");
   return 0;
 }
 

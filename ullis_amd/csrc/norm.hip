@@ -267,7 +267,7 @@ __global__ __launch_bounds__(256) void ln_bwd_vec_kernel(const float* __restrict
         }
         *dst = o;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) local_max = __builtin_fmaxf(local_max, __builtin_fabsf(o[e]));
+        for (int e = 0; e < 4; ++e) local_max = __builtin_fmaxf(local_max, finite_abs(o[e]));
       }
     }
   }
@@ -408,7 +408,7 @@ __global__ __launch_bounds__(256) void ln_bwd_row_kernel(const float* __restrict
         const float dxhat = g[j][e] * wv[j][e];
         o[e] = inv_n * ((float)ch * dxhat - sum_dxhat - v[j][e] * sum_dxhat_xhat);
         if (accumulate) o[e] = old[j][e] + o[e];
-        local_max = __builtin_fmaxf(local_max, __builtin_fabsf(o[e]));
+        local_max = __builtin_fmaxf(local_max, finite_abs(o[e]));
       }
       *reinterpret_cast<floatx4*>(gx + row * ch + c) = o;
     }
@@ -493,7 +493,7 @@ __global__ __launch_bounds__(64) void ln_bwd_any_kernel(const float* x, const fl
       float o = inv_n * ((float)ch * dxhat - sum_dxhat - xhat * sum_dxhat_xhat);
       if (accumulate) o = gx[row * ch + c] + o;
       gx[row * ch + c] = o;
-      local_max = __builtin_fmaxf(local_max, __builtin_fabsf(o));
+      local_max = __builtin_fmaxf(local_max, finite_abs(o));
     }
   }
   if (amax) {
@@ -654,12 +654,12 @@ hipError_t layer_norm_mix_backward_rows(hipStream_t s, const float* x, const flo
 
 hipError_t layer_norm_param_finish(hipStream_t s, const float* part, int nblk, long ch, float* gw,
                                    float* gb, float lr, uint16_t* w, float* w_res, uint16_t* b,
-                                   float* b_res) {
+                                   float* b_res, const uint32_t* abort) {
   if (ch <= 0) return hipSuccess;
   // part is [nblk][2][ch]: columns [0, ch) are gamma sums, [ch, 2 ch) beta sums.
   // LayerNorm::apply_clipped_sgd, src/model.rs:318-332.
-  VecTarget a{gw, lr > 0.0f ? w : nullptr, w_res, lr, nullptr};
-  VecTarget bt{gb, lr > 0.0f ? b : nullptr, b_res, lr, nullptr};
+  VecTarget a{gw, lr > 0.0f ? w : nullptr, w_res, lr, nullptr, abort};
+  VecTarget bt{gb, lr > 0.0f ? b : nullptr, b_res, lr, nullptr, abort};
   return partial_reduce(s, part, nblk, 2 * ch, ch, a, bt);
 }
 

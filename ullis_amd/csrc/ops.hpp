@@ -82,6 +82,13 @@ struct PackedFinish {
   uint16_t* scale_upd = nullptr;
   float* scale_res = nullptr;
   uint32_t* bits_new = nullptr;
+  // Optional diagnostics of the one-wave-per-row finish (CausalLoss,
+  // src/model.rs:58-80): row_flips[o] = sign bits of row o the repack
+  // changed (bit_flip_count, src/model.rs:150-156); row_step[o] = sum over
+  // row o of |latent_new - latent_old| (mean_abs_delta_fp16's terms,
+  // src/model.rs:3329-3339).
+  uint32_t* row_flips = nullptr;
+  float* row_step = nullptr;
 };
 hipError_t packed_weight_finish(hipStream_t s, const PackedFinish& f);
 
@@ -217,9 +224,10 @@ int layer_norm_mix_backward_mix_nblk(long rows, long ch);
 
 // Sums part[nblk][2][ch] -> gw, gb (optional outputs) and, when lr > 0,
 // clipped SGD on (w, b) with their carries.
+// abort (device, optional): when *abort != 0 no step is applied.
 hipError_t layer_norm_param_finish(hipStream_t s, const float* part, int nblk, long ch, float* gw,
                                    float* gb, float lr, uint16_t* w, float* w_res, uint16_t* b,
-                                   float* b_res);
+                                   float* b_res, const uint32_t* abort = nullptr);
 
 // ---------------------------------------------------------------- elementwise
 
@@ -273,6 +281,8 @@ struct VecTarget {
   float* residual;
   float lr;
   const float* mul;
+  // optional (device): when *abort != 0 the step is skipped (refused step)
+  const uint32_t* abort = nullptr;
 };
 // Fixed-order sum of part[nblk][ncols] over nblk; columns [0, split) go to a,
 // [split, ncols) to b (index relative to split).
@@ -296,9 +306,10 @@ hipError_t rosa_expand_layers(hipStream_t s, const uint8_t* idx_cm, const uint16
 hipError_t embedding_gather(hipStream_t s, const uint16_t* table, long vocab, long d,
                             const uint32_t* tokens, long rows, float* x, uint32_t* invalid);
 // Clipped SGD of table rows with g, rows sharing a token applied in row order.
+// abort (device, optional): when *abort != 0 nothing is applied.
 hipError_t embedding_scatter_sgd(hipStream_t s, uint16_t* table, float* residual, long vocab,
                                  long d, const uint32_t* tokens, long rows, const float* g,
-                                 float lr);
+                                 float lr, const uint32_t* abort = nullptr);
 
 // --------------------------------------------------------------- head + CE
 
@@ -311,6 +322,10 @@ struct HeadCe {
   const uint16_t* bias;      // [vocab] or null
   const uint32_t* targets;   // [rows]
   uint32_t ignore_id;
+  long horizon = 1;          // target of row r is targets[r + horizon]
+  // optional (device): += the number of targets >= vocab other than ignore_id
+  // (their rows are left out of the loss and the gradient)
+  uint32_t* invalid = nullptr;
   // outputs
   float* row_loss;      // [rows]
   float* stats;         // [4]: mean_loss, n_valid, gscale, loss_sum
@@ -342,6 +357,58 @@ long head_ce_chunk_cols(long vocab, long d);
 int head_ce_splits(long rows, long d, long vocab);
 // g_bias partials [ceil(rows/32)][vocab] (unscaled: multiply by gscale).
 float* head_ce_bias_partials(void* workspace, long rows, long d, long vocab);
+
+// ------------------------------------------------------- step diagnostics
+// CausalLoss of a train step (src/model.rs:58-80): word indices of the fields
+// of ullis_hip_causal_loss (include/ullis_hip.h), all 4 bytes wide.
+enum DiagField : int {
+  kDiagNextToken = 0,
+  kDiagNextTokenCount,
+  kDiagFlipsTotal,
+  kDiagP10,
+  kDiagP50,
+  kDiagP90,
+  kDiagUnigramCe,
+  kDiagUniqueTargets,
+  kDiagFlipsHead,
+  kDiagFlipsCmix,
+  kDiagFlipsRosaO,
+  kDiagEmbedGradRms,
+  kDiagHeadScaleGradRms,
+  kDiagHeadScaleRms,
+  kDiagResidualAbsMean,
+  kDiagCmixValueRms,
+  kDiagHeadLatentAbsMean,
+  kDiagHeadLatentStepAbs,
+  kDiagHeadBiasRms,
+  kDiagFields
+};
+// One reduction of the diagnostics: field = sum / denom (sqrt of it for an
+// rms), or, for kSumU32, the integer sum (a flip count).
+struct DiagTask {
+  enum Kind : int { kSqF32, kAbsF32, kSqF16, kAbsF16, kSumF32, kSumU32 };
+  int kind;
+  int field;
+  int rms;
+  const void* p;
+  long n;
+  long denom;
+};
+constexpr int kDiagMaxTasks = 16;
+struct DiagOut {
+  void* dst;  // device ullis_hip_causal_loss
+};
+struct DiagArgs {
+  const float* row_loss;    // [rows]
+  const uint32_t* targets;  // [rows] labels
+  long rows, time, vocab;
+  uint32_t ignore_id;
+  const float* stats;       // the step's {mean_loss, n_valid, gscale, loss_sum}
+  void* out;                // device ullis_hip_causal_loss
+};
+size_t diag_workspace_bytes(long vocab);
+hipError_t causal_loss_diag(hipStream_t s, const DiagArgs& a, const DiagTask* tasks, int ntasks,
+                            void* workspace);
 
 // ------------------------------------------- batched end-of-step updates
 // A train step can defer every parameter update to its end (no later kernel
@@ -389,9 +456,15 @@ struct TransJob {
   int block0;
 };
 
-hipError_t run_vec_jobs(hipStream_t s, const VecJob* jobs, int njobs, int nblocks, float lr);
-hipError_t run_finish_jobs(hipStream_t s, const FinishJob* jobs, int njobs, int nblocks, float lr);
-hipError_t run_f16_jobs(hipStream_t s, const F16Job* jobs, int njobs, int nblocks, float lr);
-hipError_t run_trans_jobs(hipStream_t s, const TransJob* jobs, int njobs, int nblocks);
+// abort (device, optional): when *abort != 0 the launches change nothing (a
+// refused step); the finish then writes zero row flips / steps.
+hipError_t run_vec_jobs(hipStream_t s, const VecJob* jobs, int njobs, int nblocks, float lr,
+                        const uint32_t* abort = nullptr);
+hipError_t run_finish_jobs(hipStream_t s, const FinishJob* jobs, int njobs, int nblocks, float lr,
+                           const uint32_t* abort = nullptr);
+hipError_t run_f16_jobs(hipStream_t s, const F16Job* jobs, int njobs, int nblocks, float lr,
+                        const uint32_t* abort = nullptr);
+hipError_t run_trans_jobs(hipStream_t s, const TransJob* jobs, int njobs, int nblocks,
+                          const uint32_t* abort = nullptr);
 
 }  // namespace ullis

@@ -61,6 +61,8 @@ __device__ __forceinline__ void packed_finish_row(const PackedFinish& f, long o,
 // loads; requires packed_finish_wave_ok. The repack assembles each 32-bit
 // word from four lanes, so whole words of row o (in % 32 == 0) are written
 // after the wave has read them.
+// With f.row_flips / f.row_step it also records row o's bit flips and summed
+// |latent step| (no effect on the update).
 __device__ __forceinline__ void packed_finish_row_wave(const PackedFinish& f, long o, float lr) {
   float gmul = f.amax ? 1.0f / grad_scale_from_amax(*f.amax) : 1.0f;
   if (f.extra_mul) gmul *= *f.extra_mul;
@@ -68,6 +70,8 @@ __device__ __forceinline__ void packed_finish_row_wave(const PackedFinish& f, lo
   const long wn = f.out * f.in;
   const int lane = threadIdx.x & 63;
   float gs = 0.0f;
+  uint32_t flips = 0;
+  float step = 0.0f;
   for (long i0 = lane * 8; i0 < f.in; i0 += 512) {
     const long w = o * f.in + i0;
     floatx4 g0 = {0.0f, 0.0f, 0.0f, 0.0f}, g1 = g0;
@@ -77,7 +81,8 @@ __device__ __forceinline__ void packed_finish_row_wave(const PackedFinish& f, lo
       g1 += p[1];
     }
     float G[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
-    const uint32_t signs = f.bits_old[w >> 5] >> (w & 31);
+    const uint32_t old_word = f.bits_old[w >> 5];
+    const uint32_t signs = old_word >> (w & 31);
     float gw[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -100,8 +105,10 @@ __device__ __forceinline__ void packed_finish_row_wave(const PackedFinish& f, lo
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         v[j] = (uint16_t)(lat[j >> 1] >> (16 * (j & 1)));
+        const uint16_t before = v[j];
         binaryconnect_sgd_one(v[j], r[j], gw[j] * f.ste, lr);
         plus |= (latent_is_plus(v[j]) ? 1u : 0u) << j;
+        if (f.row_step) step += __builtin_fabsf(f16_bits_to_f32(before) - f16_bits_to_f32(v[j]));
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) lat[j] = (uint32_t)v[2 * j] | ((uint32_t)v[2 * j + 1] << 16);
@@ -112,11 +119,22 @@ __device__ __forceinline__ void packed_finish_row_wave(const PackedFinish& f, lo
         uint32_t word = plus << (8 * (lane & 3));
         word |= __shfl_xor(word, 1, 64);
         word |= __shfl_xor(word, 2, 64);
-        if ((lane & 3) == 0) f.bits_new[w >> 5] = word;
+        if ((lane & 3) == 0) {
+          f.bits_new[w >> 5] = word;
+          flips += (uint32_t)__builtin_popcount(word ^ old_word);
+        }
       }
     }
   }
   gs = wave_sum(gs);
+  if (f.row_flips) {
+    const uint32_t n = wave_sum_u32(flips);
+    if (lane == 0) f.row_flips[o] = n;
+  }
+  if (f.row_step) {
+    step = wave_sum(step);
+    if (lane == 0) f.row_step[o] = step;
+  }
   if (lane == 0) {
     if (f.g_scale) f.g_scale[o] = gs;
     if (f.scale_upd && lr > 0.0f) clipped_sgd_one(f.scale_upd[o], f.scale_res[o], gs, lr);
@@ -223,7 +241,8 @@ __device__ __forceinline__ void vec_reduce_block(const float* part, int nblk, lo
     float v = red[0][threadIdx.x];
     if (t.mul) v *= *t.mul;
     if (t.out) t.out[i] = v;
-    if (t.values && lr > 0.0f) clipped_sgd_one(t.values[i], t.residual[i], v, lr);
+    if (t.values && lr > 0.0f && !(t.abort && *t.abort))
+      clipped_sgd_one(t.values[i], t.residual[i], v, lr);
   }
 }
 

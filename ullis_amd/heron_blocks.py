@@ -183,9 +183,9 @@ class HeronBlockStep:
         self._call("packed_head_train_sgd", lib.ullis_hip_packed_head_train_sgd(
             rt.ctx, hidden16.ptr, self.p("head.bits"), self.p("head.bits_t"), self.p("head.scale"),
             self.p("head.bias"), self.p("head.latent"), self.p("head.latent.residual"),
-            self.p("head.scale.residual"), self.p("head.bias.residual"), dl.ptr, R, T, D, V,
+            self.p("head.scale.residual"), self.p("head.bias.residual"), dl.ptr, R, T, D, V, 1,
             ignore_id, lr, ste, row_loss.ptr, stats.ptr, g_hidden.ptr, g_scale.ptr, g_bias.ptr,
-            None))
+            None, None))
         g_x = self._ln_backward_sgd("ln_out", pre_ln_out, g_hidden, lr)
 
         # ------------------------------------------------------ backward

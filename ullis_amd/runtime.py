@@ -258,8 +258,10 @@ class HipRuntime:
 
     def packed_head_train_sgd(self, hidden16_bits, bits, scale_bits, bias_bits, latent_bits,
                               latent_res, scale_res, bias_res, targets, rows, time, d, vocab,
-                              ignore_id, lr, ste, want_g_w=False):
-        """Head + streamed CE (+ update when lr > 0). Returns a dict of host arrays."""
+                              ignore_id, lr, ste, want_g_w=False, horizon=1):
+        """Head + streamed CE (+ update when lr > 0). Returns a dict of host arrays;
+        "invalid" counts targets >= vocab other than ignore_id (left out of the
+        loss and the gradient)."""
         words = (vocab * d + 31) // 32
         dh = self.put(np.asarray(hidden16_bits, np.uint16))
         db = self.put(np.asarray(bits, np.uint32))
@@ -279,13 +281,15 @@ class HipRuntime:
         g_scale = self.buffer(4 * vocab)
         g_bias = self.buffer(4 * vocab)
         g_w = self.buffer(4 * vocab * d) if want_g_w else None
+        invalid = self.zeros(np.uint32, 1)
         self._check(self.lib.ullis_hip_packed_head_train_sgd(
             self.ctx, dh.ptr, db.ptr, dbt.ptr, ds.ptr, dbias.ptr if dbias else None, dl.ptr,
-            dlr.ptr, dsr.ptr, dbr.ptr if dbr else None, dt.ptr, rows, time, d, vocab, ignore_id,
-            lr, ste, row_loss.ptr, stats.ptr, g_hidden.ptr, g_scale.ptr, g_bias.ptr,
-            g_w.ptr if g_w else None), "packed_head_train_sgd")
+            dlr.ptr, dsr.ptr, dbr.ptr if dbr else None, dt.ptr, rows, time, d, vocab, horizon,
+            ignore_id, lr, ste, row_loss.ptr, stats.ptr, g_hidden.ptr, g_scale.ptr, g_bias.ptr,
+            g_w.ptr if g_w else None, invalid.ptr), "packed_head_train_sgd")
         st = stats.download(np.float32, 4)
         out = {
+            "invalid": int(invalid.download(np.uint32, 1)[0]),
             "mean_loss": float(st[0]), "n_valid": int(st[1]), "gradient_scale": float(st[2]),
             "row_loss": row_loss.download(np.float32, rows),
             "hidden_gradient": g_hidden.download(np.float32, rows * d),
@@ -569,11 +573,27 @@ class HeronTrainer:
 
     def step(self, x_emb: DeviceBuffer, labels: DeviceBuffer, ignore_id: int, lr: float,
              rosa_idx: DeviceBuffer, g_emb: DeviceBuffer, row_loss: DeviceBuffer | None = None,
-             stats: DeviceBuffer | None = None, qkv_bits: DeviceBuffer | None = None):
+             stats: DeviceBuffer | None = None, qkv_bits: DeviceBuffer | None = None,
+             invalid: DeviceBuffer | None = None):
+        """ullis_hip_heron_step; invalid (optional u32) receives the count of labels
+        >= vocab other than ignore_id (non-zero: the step changed no parameter)."""
         self.rt._check(self.rt.lib.ullis_hip_heron_step(
             self.h, x_emb.ptr, labels.ptr, ignore_id, lr, rosa_idx.ptr, g_emb.ptr,
             row_loss.ptr if row_loss else None, stats.ptr if stats else None,
-            qkv_bits.ptr if qkv_bits else None), "heron_step")
+            qkv_bits.ptr if qkv_bits else None, invalid.ptr if invalid else None), "heron_step")
+
+    def causal_loss(self, g_emb: DeviceBuffer, labels: DeviceBuffer, ignore_id: int,
+                    row_loss: DeviceBuffer | None = None, table_res: DeviceBuffer | None = None
+                    ) -> dict:
+        """CausalLoss of the last step (src/model.rs:58-80, train_step_on's return
+        value): ullis_hip_heron_causal_loss into a device struct, downloaded."""
+        out = self.rt.zeros(np.uint8, C.sizeof(_lib.CausalLoss))
+        n = self.shape.vocab * self.shape.d_model if table_res is not None else 0
+        self.rt._check(self.rt.lib.ullis_hip_heron_causal_loss(
+            self.h, g_emb.ptr, labels.ptr, ignore_id, row_loss.ptr if row_loss else None,
+            table_res.ptr if table_res is not None else None, n, out.ptr), "heron_causal_loss")
+        cl = _lib.CausalLoss.from_buffer_copy(out.download(np.uint8).tobytes())
+        return cl.as_dict()
 
     def step_tokens(self, table: DeviceBuffer, table_res: DeviceBuffer, tokens: DeviceBuffer,
                     labels: DeviceBuffer, ignore_id: int, lr: float, rosa_idx: DeviceBuffer,
@@ -584,7 +604,8 @@ class HeronTrainer:
         embedding gather, the step and the embedding scatter-SGD, all
         stream-ordered on the device. table / table_res: f16 [vocab, d] and its
         fp32 carry; x_emb / g_emb: fp32 [rows, d] work buffers; invalid
-        (optional u32) counts token ids >= vocab."""
+        (optional u32) receives the count of token ids >= vocab and labels >=
+        vocab other than ignore_id (non-zero: the step changed nothing)."""
         self.rt._check(self.rt.lib.ullis_hip_heron_step_tokens(
             self.h, table.ptr, table_res.ptr, self.shape.vocab, tokens.ptr, labels.ptr, ignore_id,
             lr, rosa_idx.ptr, x_emb.ptr, g_emb.ptr, row_loss.ptr if row_loss else None,
