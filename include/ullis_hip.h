@@ -81,6 +81,20 @@ int ullis_hip_layer_norm_backward(ullis_hip_ctx* ctx, const float* x, const floa
                                   const uint16_t* weight, size_t rows, size_t channels, float* gx,
                                   float* gw, float* gb);
 
+/* No counterpart in the reference: ullis_hip_layer_norm_backward for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). It calls no allocator: the
+ * gamma / beta column partials live in a static 8 MiB device array that the
+ * library holds on every GPU it runs on until the process ends, which limits
+ * channels to 4096 (larger values are rejected with ULLIS_HIP_ERR_INVALID).
+ * gx, gw and gb are the same quantities as ullis_hip_layer_norm_backward's
+ * (the partials are grouped differently, so gw / gb may differ in the last
+ * bits). Calls on one GPU share the array: calls that overlap on that GPU
+ * (other streams, other threads) race. */
+int ullis_hip_layer_norm_backward_static(ullis_hip_ctx* ctx, const float* x, const float* gy,
+                                         const uint16_t* weight, size_t rows, size_t channels,
+                                         float* gx, float* gw, float* gb);
+
 /* MetalRuntime::binary_linear, src/metal.rs:1705-1751:
  * y = bias + scale * (x . S^T). x is [rows, in] of x_dtype (ULLIS_HIP_F16 or
  * ULLIS_HIP_F32); bias may be NULL; y32 / y16 may be NULL. */

@@ -87,6 +87,7 @@ SIGNATURES = {
     "ullis_hip_time_next_launch": (i32, [vp, i32, i32]),
     "ullis_hip_layer_norm": (i32, [vp, vp, vp, vp, sz, sz, vp, vp]),
     "ullis_hip_layer_norm_backward": (i32, [vp, vp, vp, vp, sz, sz, vp, vp, vp]),
+    "ullis_hip_layer_norm_backward_static": (i32, [vp, vp, vp, vp, sz, sz, vp, vp, vp]),
     "ullis_hip_binary_linear": (i32, [vp, vp, i32, vp, vp, vp, sz, sz, sz, vp, vp]),
     "ullis_hip_binary_linear_backward": (
         i32, [vp, vp, vp, vp, vp, i32, sz, sz, sz, vp, vp, vp, vp]),

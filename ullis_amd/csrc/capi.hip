@@ -76,6 +76,12 @@ int ullis_hip_create(int device, ullis_hip_ctx** out) {
       return ULLIS_HIP_ERR_RUNTIME;
     }
   }
+  // the no-allocation entry points' scratch: its address on this device
+  const hipError_t se = static_scratch_address(device, &c->static_scratch);
+  if (se != hipSuccess) {
+    c->static_scratch = nullptr;
+    c->static_scratch_err = hipGetErrorString(se);
+  }
   *out = c;
   return 0;
 }

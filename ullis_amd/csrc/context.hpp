@@ -16,6 +16,10 @@ struct ullis_hip_ctx {
   size_t scratch_bytes = 0;
   hipEvent_t events[16] = {};
   ullis::LaunchProbe next_launch;  // armed by ullis_hip_time_next_launch
+  // device address of the static scratch array on this context's device
+  // (ullis_hip_layer_norm_backward_static), looked up at create
+  void* static_scratch = nullptr;
+  std::string static_scratch_err;
 
   int fail(int code, const std::string& msg) {
     err = msg;
@@ -48,6 +52,10 @@ struct ullis_hip_ctx {
 };
 
 namespace ullis {
+
+// noalloc.hip: device address of the library's static scratch array on
+// `device` (the current device), looked up once per device.
+hipError_t static_scratch_address(int device, void** out);
 
 // Carves 256-byte aligned sub-buffers from one allocation.
 struct Carver {

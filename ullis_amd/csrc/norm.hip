@@ -619,6 +619,29 @@ hipError_t layer_norm_backward_rows(hipStream_t s, const float* x, const float* 
   return hipGetLastError();
 }
 
+int layer_norm_backward_capped_nblk(long rows) { return ln_bwd_blocks_any(rows); }
+
+hipError_t layer_norm_backward_rows_capped(hipStream_t s, const float* x, const float* gy,
+                                           long rows, long ch, const uint16_t* w, float* gx,
+                                           float* part, int* nblk_out) {
+  if (rows <= 0 || ch <= 0) {
+    if (nblk_out) *nblk_out = 0;
+    return hipSuccess;
+  }
+  const int nblk = ln_bwd_blocks_any(rows);
+  if (nblk_out) *nblk_out = nblk;
+  if (ln_bwd_vec_path(ch) && vec_ok(x) && vec_ok(gy) && vec_ok(gx)) {
+    return by_nv(ch, [&](auto nv) {
+      launch(ln_bwd_vec_kernel<decltype(nv)::value>, dim3(nblk), dim3(256), 0, s, x, gy, rows,
+             (int)ch, w, gx, 0, (float*)nullptr, part);
+      return hipGetLastError();
+    });
+  }
+  launch(ln_bwd_any_kernel, dim3(nblk), dim3(64), 0, s, x, gy, rows, (int)ch, w, gx, 0,
+         (float*)nullptr, part);
+  return hipGetLastError();
+}
+
 int layer_norm_mix_backward_mix_nblk(long rows, long ch) {
   return ln_bwd_row_path(rows, ch) ? (int)cdiv(rows, kRowsPerBlock) : (int)cdiv(rows, 16);
 }

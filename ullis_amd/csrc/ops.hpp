@@ -207,6 +207,13 @@ hipError_t layer_norm_backward_rows(hipStream_t s, const float* x, const float* 
                                     long ch, const uint16_t* w, float* gx, int accumulate,
                                     float* amax, float* part, int* nblk_out);
 int layer_norm_backward_blocks(long rows);
+// The same backward with at most 256 column-partial blocks whatever the row
+// count (rows are strided over a fixed grid): part[nblk][2][ch] with
+// nblk = layer_norm_backward_capped_nblk(rows) <= 256.
+hipError_t layer_norm_backward_rows_capped(hipStream_t s, const float* x, const float* gy,
+                                           long rows, long ch, const uint16_t* w, float* gx,
+                                           float* part, int* nblk_out);
+int layer_norm_backward_capped_nblk(long rows);
 // Partial blocks layer_norm_backward_rows uses for 16-byte aligned x / gy / gx.
 int layer_norm_backward_nblk(long rows, long ch);
 // LayerNorm backward fed by the backward of the time-shift mix that read its

@@ -151,6 +151,14 @@ class HipRuntime:
         return (gx.download(np.float32, rows * channels), gw.download(np.float32, channels),
                 gb.download(np.float32, channels))
 
+    def layer_norm_backward_static_dev(self, x: DeviceBuffer, gy: DeviceBuffer,
+                                       weight: DeviceBuffer, rows, channels, gx: DeviceBuffer,
+                                       gw: DeviceBuffer | None, gb: DeviceBuffer | None):
+        """ullis_hip_layer_norm_backward_static on device buffers (allocates nothing)."""
+        self._check(self.lib.ullis_hip_layer_norm_backward_static(
+            self.ctx, x.ptr, gy.ptr, weight.ptr, rows, channels, gx.ptr,
+            gw.ptr if gw else None, gb.ptr if gb else None), "layer_norm_backward_static")
+
     def binary_linear(self, x, bits, scale_bits, bias_bits, rows, in_f, out_f, x_dtype=F16,
                       out_dtype=np.float32):
         xa = np.asarray(x)
