@@ -11,15 +11,18 @@ embedding scatter-SGD (HeronTrainer.step_tokens). The timed
 region is bracketed by stream synchronisation; HIP events on the library's
 stream give the step time.
 
-Prints ONE JSON line. `roofline` is for the kernel that dominates the step,
-timed over a second pass of the same number of steps right after the
-reported one (ullis_hip_heron_probe): every workgroup of a probed launch
-writes its start and end on the device wall clock, and a launch lasts from
-the earliest start to the latest end. The probe pass is kept out of the
-reported steps because the stamps themselves cost a little.
-`cpu_baseline` times the CPU oracle (a port of the
-reference's CPU backend) single-threaded on a bounded sample of the same
-workload (fewer rows, same widths and depth), scaled per token.
+Prints ONE JSON line. `roofline` is for the launch that dominates the step
+(the value backward pair) and `roofline_packed` for the dominant packed +-1
+launch (the key backward pair), which the metric names. Each is timed over
+its own passes of the same number of steps right after the reported ones
+(ullis_hip_heron_probe): `avg_us` from kernel-timestamp events per launch
+(the dispatch interval rocprofv3's kernel trace reports), `avg_us_stamps`
+from every workgroup's start / end on the device wall clock (earliest start
+to latest end). The probe passes are kept out of the reported steps.
+`cpu_baseline` times the CPU oracle (a port of the reference's CPU backend)
+single-threaded on windows of 256 tokens at full widths and depth (three
+runs in child processes started before the GPU is touched; the median),
+scaled per token.
 """
 from __future__ import annotations
 
@@ -49,8 +52,16 @@ TRAFFIC_BYTES = {
     "value_backward": (21648.5 * 2.0 + 12649.5 * 1.0) * 1024,
 }
 
+# Launch classes with a roofline object in the bench line: the step's dominant
+# launch (the value backward pair, fp16) and its dominant packed +-1 launch
+# (the key backward pair), which BASELINE.json's metric names.
+ROOFLINE_PROBES = (("roofline", "value_backward"), ("roofline_packed", "key_backward"))
 
-def cpu_baseline(rows: int) -> dict:
+
+def cpu_sample(rows: int) -> None:
+    """One oracle train step (config 4's widths and depth, a window of `rows`
+    tokens), single-threaded; prints its wall time as JSON. Run as a child
+    process of bench.py, started before bench.py touches the GPU."""
     from oracle import cpu_ref as o
     from ullis_amd.synth import heron_arena, step_inputs
 
@@ -61,16 +72,48 @@ def cpu_baseline(rows: int) -> dict:
     x, labels, idx = step_inputs(rows, c["d_model"], c["vocab"], c["n_layers"], 1, rows, seed=7)
     t0 = time.perf_counter()
     o.heron_train_step(dims, arena, x, labels, NO_IGNORE, 1, rows, LR, idx, want_qkv=True)
-    dt = time.perf_counter() - t0
+    print(json.dumps({"rows": rows, "seconds": time.perf_counter() - t0}), flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(rows: int, runs: int) -> dict:
+    """The oracle's heron step (a port of the reference's CPU backend) timed on
+    `runs` windows of `rows` tokens, each single-threaded in its own child
+    process (run side by side), median of the runs, scaled per token."""
+    import subprocess
+
+    py = [sys.executable, os.path.abspath(__file__), "--cpu-sample", str(rows)]
+    procs = [subprocess.Popen(py, stdout=subprocess.PIPE, text=True) for _ in range(runs)]
+    secs = []
+    for pr in procs:
+        out, _ = pr.communicate()
+        if pr.returncode != 0:
+            raise RuntimeError("cpu sample failed")
+        secs.append(json.loads(out.strip().splitlines()[-1])["seconds"])
+    med = float(np.median(secs))
     return {
-        "value": rows / dt,
+        "value": round(rows / med, 2),
         "unit": "tokens/s",
         "cores": 1,
         "kind": "port",
-        "sample": (f"oracle/cpu_ref.c heron step D512 L12 F2048 V8192, one window of T={rows} "
-                   f"tokens (full widths and depth), single thread, {dt:.1f} s; tokens/s scales "
-                   "linearly in T for every op except the per-weight SGD, which this sample "
-                   "charges to fewer tokens"),
+        "sample": (f"oracle/cpu_ref.c heron step D512 L12 F2048 V8192 (full widths and depth) on "
+                   f"a window of T={rows} tokens, single-threaded; median of {runs} runs "
+                   f"({', '.join(f'{t:.1f}' for t in sorted(secs))} s), each in its own process, "
+                   f"run side by side; host: {os.cpu_count()} logical CPUs, {cpu_model()}. "
+                   "Tokens/s scales linearly in T for every op except the per-weight SGD, which "
+                   "this window charges to fewer tokens than a T=2048 step"),
+        "host_cpus": os.cpu_count(),
+        "host_cpu_model": cpu_model(),
+        "run_seconds": [round(t, 2) for t in secs],
     }
 
 
@@ -296,11 +339,14 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--cpu-rows", type=int, default=64,
-                    help="rows of the CPU-baseline sample (0 disables it)")
-    ap.add_argument("--probe", default="value_backward",
-                    help="launch class timed for the roofline object ('none': no probe, "
-                         "no roofline object)")
+    ap.add_argument("--cpu-rows", type=int, default=256,
+                    help="tokens of each CPU-baseline window (0 disables it)")
+    ap.add_argument("--cpu-runs", type=int, default=3,
+                    help="CPU-baseline windows, run side by side; the median is reported")
+    ap.add_argument("--cpu-sample", type=int, default=0, help=argparse.SUPPRESS)
+    ap.add_argument("--probe", default="auto",
+                    help="'auto': roofline objects for the value and key backward pairs; a "
+                         "launch class name: that class only; 'none': no roofline object")
     ap.add_argument("--decode-gemv", type=int, default=0, metavar="REPS",
                     help="instead of the train step, time the few-row (T = 1 decode) forward "
                          "products over REPS launches each and print one JSON line per product")
@@ -316,11 +362,18 @@ def main() -> int:
                     help="after the timed region, run one plain device copy kernel of this many "
                          "MiB (read + write) so HBM counters can be scaled against known bytes")
     args = ap.parse_args()
+    if args.cpu_sample > 0:
+        cpu_sample(args.cpu_sample)
+        return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py: this build measures one MI355X only (no multi-GPU path); "
               "run with --gpus 1", file=sys.stderr)
         return 2
+    plain = args.decode_gemv == 0 and not args.stress and args.ln_isolated == 0
+    # the CPU baseline's child processes start before this process touches the GPU
+    baseline = (cpu_baseline(args.cpu_rows, max(1, args.cpu_runs))
+                if plain and args.cpu_rows > 0 else None)
 
     from ullis_amd.runtime import HeronShape, HeronTrainer, HipRuntime
     from ullis_amd.synth import heron_arena, step_inputs
@@ -387,31 +440,45 @@ def main() -> int:
     tokens = shape.rows * args.steps
     value = tokens / (total_ms / 1e3)
     loss = float(st.download(np.float32, 4)[0])
-    # the roofline object: K more steps with the probe armed (the stamping
-    # launches are kept out of the reported steps)
-    kernel, probe_ms = None, None
-    if args.probe != "none":
-        probe = trainer.probe_begin(args.probe)
-        probe_ms, _ = timed(args.steps)
-        kernel = trainer.probe_end(probe)
+    # the roofline objects: for each probed launch class, K more steps with
+    # its launches timed by kernel-timestamp events (the dispatch interval
+    # rocprofv3's kernel trace reports), then K with workgroup wall-clock
+    # stamps; both passes are kept out of the reported steps
+    if args.probe == "auto":
+        probes = ROOFLINE_PROBES
+    elif args.probe == "none":
+        probes = ()
+    else:
+        probes = (("roofline", args.probe),)
+    rooflines = {}
+    for key, name in probes:
+        trainer.probe_begin(name, events=True)
+        ev_ms, _ = timed(args.steps)
+        ev = trainer.probe_end(name)
+        trainer.probe_begin(name)
+        st_ms, _ = timed(args.steps)
+        stp = trainer.probe_end(name)
+        if not ev["count"]:
+            continue
+        avg_s = ev["total_ms"] / ev["count"] / 1e3
+        st_s = stp["total_ms"] / stp["count"] / 1e3 if stp["count"] else None
+        mfma = ev["bound"] == "mfma"
+        scale = 1e12 if mfma else 1e9
+        peak = FP16_PEAK_TFLOPS if mfma else HBM_PEAK_GBS
+        achieved = ev["work"] / avg_s / scale
+        rooflines[key] = {
+            "bound": ev["bound"], "achieved": round(achieved, 2), "peak": peak,
+            "unit": "TFLOP/s" if mfma else "GB/s", "frac": round(achieved / peak, 4),
+            "traffic": TRAFFIC_BYTES.get(name), "kernel": ev["name"], "probe": name,
+            "avg_us": round(avg_s * 1e6, 2), "launches": ev["count"],
+            "timing": "kernel-timestamp events per launch (dispatch start to end)",
+            "avg_us_stamps": round(st_s * 1e6, 2) if st_s else None,
+            "frac_stamps": round(ev["work"] / st_s / scale / peak, 4) if st_s else None,
+            "probe_pass_ms_per_step": round(ev_ms / args.steps, 4),
+        }
     if args.copy_mib > 0:
         copy_calibration(rt, args.copy_mib)
 
-    roofline = None
-    if kernel and kernel["count"]:
-        avg_s = kernel["total_ms"] / kernel["count"] / 1e3
-        achieved = kernel["work"] / avg_s / (1e12 if kernel["bound"] == "mfma" else 1e9)
-        peak = FP16_PEAK_TFLOPS if kernel["bound"] == "mfma" else HBM_PEAK_GBS
-        roofline = {
-            "bound": kernel["bound"], "achieved": round(achieved, 2), "peak": peak,
-            "unit": "TFLOP/s" if kernel["bound"] == "mfma" else "GB/s",
-            "frac": round(achieved / peak, 4), "traffic": TRAFFIC_BYTES.get(args.probe),
-            "kernel": kernel["name"], "avg_us": round(avg_s * 1e6, 2),
-            "launches": kernel["count"],
-            "probe_pass_ms_per_step": round(probe_ms / args.steps, 4),
-        }
-
-    baseline = cpu_baseline(args.cpu_rows) if args.cpu_rows > 0 else None
     line = {
         "metric": "train tokens/s (heron D512 L12 T2048)",
         "value": round(value, 1),
@@ -431,7 +498,8 @@ def main() -> int:
                    "global_batch": c["batch"], "seq_len": c["time"], "parallelism": "none (1 GPU)"},
         "wall_s": round(wall, 3),
         "loss_last_step": round(loss, 5),
-        "roofline": roofline,
+        "roofline": rooflines.get("roofline"),
+        "roofline_packed": rooflines.get("roofline_packed"),
         "cpu_baseline": baseline,
     }
     print(json.dumps(line), flush=True)

@@ -367,7 +367,8 @@ int ullis_hip_heron_set_graph(ullis_hip_heron* h, int enable);
  * TrainStepProfile (src/model.rs:101-124): while a probe id is set, every
  * launch of that class inside ullis_hip_heron_step records its execution
  * interval: a streamed-LDS GEMM launch has each workgroup write its start and
- * end on the device wall clock (earliest start to latest end), other kernels
+ * end on the device wall clock (earliest start to latest end; with
+ * ULLIS_HIP_PROBE_EVENTS, kernel-timestamp events as below), other kernels
  * use kernel-timestamp events (hipExtLaunchKernel); HEAD_CE, which is several
  * kernels, is bracketed by event records on the step's stream. At most 512
  * launches are recorded. probe_read waits for the step and returns the summed
@@ -383,6 +384,10 @@ int ullis_hip_heron_set_graph(ullis_hip_heron* h, int enable);
 #define ULLIS_HIP_PROBE_LN_FORWARD 7        /* ln2 forward fused with the CMix time-shift mix */
 #define ULLIS_HIP_PROBE_LN_BACKWARD 8       /* CMix mix backward fused with the ln2 backward */
 #define ULLIS_HIP_PROBE_COUNT 9
+/* OR-ed into probe_id: time the GEMM launches of the class by kernel-timestamp
+ * events as well (the start / end of the dispatch that rocprofv3's kernel
+ * trace reports) instead of workgroup wall-clock stamps. */
+#define ULLIS_HIP_PROBE_EVENTS 0x100
 int ullis_hip_heron_probe(ullis_hip_heron* h, int probe_id);
 int ullis_hip_heron_probe_read(ullis_hip_heron* h, float* total_ms, int* launches);
 

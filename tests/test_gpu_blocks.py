@@ -7,11 +7,14 @@ which it must match bit for bit.
 
 Bounds: a block chains GEMMs through fp16 operands where the oracle keeps
 fp32 (the mixed input, ReLU^2, the scaled gradient), so composed outputs and
-gradients are compared as max|gpu - ref| / max|ref| <= BLOCK_REL (two fp16
-roundings of ~2^-11 each, with margin); updates are compared as the change of
-the effective parameter (f16 value + fp32 carry), which is -lr * clip(g);
-sign bits as mismatch fractions (an output or latent within rounding of zero
-may land on either side).
+gradients are compared as max|gpu - ref| / max|ref| <= BLOCK_REL; updates are
+compared as the change of the effective parameter (f16 value + fp32 carry),
+which is -lr * clip(g), <= UPDATE_REL; sign bits as mismatch fractions (an
+output or latent within rounding of zero may land on either side). Each case
+writes its measured drift to gpurun_out/block_drift/<case>.json; the maxima
+over the cases were 9.1e-4 (the key scale gradient), 7.6e-4 (the key latent
+step) and 5.8e-4 for everything else, and no updated weight sign bit
+differed. The bounds are those maxima with a margin under 2x.
 """
 import numpy as np
 import pytest
@@ -24,9 +27,9 @@ from ullis_amd.synth import f16, heron_arena, pack_bits, step_inputs, tensor_vie
 pytestmark = pytest.mark.gpu
 
 NO_IGNORE = 0xFFFFFFFF
-BLOCK_REL = 2e-3
-UPDATE_REL = 5e-3
-BITS_FRAC = 2e-3
+BLOCK_REL = 1.5e-3
+UPDATE_REL = 1.5e-3
+BITS_FRAC = 2e-3  # Q/K/V projection sign bit-planes
 
 
 def h2f(bits):

@@ -156,11 +156,11 @@ __device__ __forceinline__ int mfma32_row(int r, int lane) {
 // ------------------------------------------------------------ launching
 // Launch probe, armed on the launching thread for the next launch:
 //  - kernels that take a stamps slot (the streamed-LDS GEMMs) get `stamps`
-//    as an argument: every block records the device wall clock
-//    (s_memrealtime) at its start (atomic min into stamps[0]) and end
-//    (atomic max into stamps[1]), i.e. the launch's execution interval, which
-//    waiting for CUs held by another stream's kernels does not inflate; the
-//    launcher sets used_stamps;
+//    as an argument: every block writes the device wall clock
+//    (s_memrealtime) at its start and end into its own (start, end) pair, and
+//    the host takes the earliest start and the latest end, i.e. the launch's
+//    execution interval, which waiting for CUs held by another stream's
+//    kernels does not inflate; the launcher sets used_stamps;
 //  - any other launch() records its kernel into the events
 //    (hipExtLaunchKernelGGL).
 // The launcher that consumes the probe disarms it.

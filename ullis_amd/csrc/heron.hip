@@ -151,6 +151,7 @@ struct ullis_hip_heron {
   int splits_o = 1, splits_key = 1, splits_value = 1;
   // kernel probe: events around every launch of one launch class
   int probe = 0;
+  bool probe_events_only = false;  // ULLIS_HIP_PROBE_EVENTS: GEMMs timed by events too
   int probe_used = 0;
   std::vector<hipEvent_t> probe_events;
   unsigned long long* probe_stamps = nullptr;  // device [kStampTotal][2], lazily
@@ -237,7 +238,7 @@ __global__ void probe_stamps_clear_kernel(unsigned long long* st, long n) {
     if (on_) {                                                                     \
       lp_.start = h->probe_events[2 * h->probe_used];                              \
       lp_.stop = h->probe_events[2 * h->probe_used + 1];                           \
-      lp_.stamps = h->probe_stamps + 2 * h->stamp_used;                            \
+      lp_.stamps = h->probe_events_only ? nullptr : h->probe_stamps + 2 * h->stamp_used; \
       lp_.stamp_cap = kStampTotal - h->stamp_used;                                 \
       t_launch_probe = &lp_;                                                       \
     }                                                                              \
@@ -679,8 +680,12 @@ int ullis_hip_heron_arena(ullis_hip_heron* h, void** device_ptr, uint64_t* bytes
 }
 
 int ullis_hip_heron_probe(ullis_hip_heron* h, int probe_id) {
-  if (!h || probe_id < 0 || probe_id >= ULLIS_HIP_PROBE_COUNT) return ULLIS_HIP_ERR_INVALID;
+  if (!h) return ULLIS_HIP_ERR_INVALID;
+  const bool events_only = (probe_id & ULLIS_HIP_PROBE_EVENTS) != 0;
+  probe_id &= ~ULLIS_HIP_PROBE_EVENTS;
+  if (probe_id < 0 || probe_id >= ULLIS_HIP_PROBE_COUNT) return ULLIS_HIP_ERR_INVALID;
   h->probe = probe_id;
+  h->probe_events_only = events_only;
   h->probe_used = 0;
   h->stamp_used = 0;
   if (probe_id != ULLIS_HIP_PROBE_NONE) {

@@ -546,8 +546,13 @@ class HeronTrainer:
                             "mix bwd + LayerNorm bwd rows (ln2, += g_x)"),
         }
 
-    def probe_begin(self, name: str = "key_forward") -> str:
-        pid = self.probes()[name][0]
+    PROBE_EVENTS = 0x100  # ULLIS_HIP_PROBE_EVENTS
+
+    def probe_begin(self, name: str = "key_forward", events: bool = False) -> str:
+        """Arms the probe for a launch class; events=True times its GEMM launches by
+        kernel-timestamp events (what rocprofv3's kernel trace reports) instead of
+        workgroup wall-clock stamps."""
+        pid = self.probes()[name][0] | (self.PROBE_EVENTS if events else 0)
         self.rt._check(self.rt.lib.ullis_hip_heron_probe(self.h, pid), "probe")
         return name
 
