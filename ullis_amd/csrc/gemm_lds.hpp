@@ -9,9 +9,11 @@
 // of stage t+NS-1 go out right after that barrier, into the buffer that stage
 // t-1 used.
 //
-// Block = 256 threads = 4 wave64s in a 2x2 grid, each owning a (BM/2) x (BN/2)
-// sub-tile of 32x32 v_mfma_f32_32x32x16_f16 tiles with fp32 accumulation
-// (the same accumulator layout and epilogue interface as gemm.hpp).
+// Block = NW wave64s (4 or 8) in a 2 x (NW/2) grid, each owning a (BM/2) x
+// (BN/(NW/2)) sub-tile of 32x32 v_mfma_f32_32x32x16_f16 tiles with fp32
+// accumulation (the same accumulator layout and epilogue interface as
+// gemm.hpp). With 8 waves two run on each SIMD, so one wave's LDS reads and
+// waits overlap the other's MFMAs.
 //
 // Operand layouts in LDS (one stage):
 //   OpMK    fp16 [row][k], k contiguous in HBM. LDS rows of BK halves with the
@@ -67,15 +69,15 @@ __device__ __forceinline__ void wait_barrier() {
 }
 
 // fp16 [row][k] with k contiguous.
-template <int ROWS, int BK>
+template <int ROWS, int BK, int NW = 4>
 struct OpMK {
   const half_t* p;
   long ld;   // halves between rows
   int rows;  // valid rows (tile rows past it are clamped)
   static constexpr int CPR = BK / 8;  // 16-byte chunks per row
   static constexpr int kBytes = ROWS * BK * 2;
-  static_assert(kBytes % 4096 == 0, "a stage must be whole wave-loads for 4 waves");
-  static constexpr int kInst = kBytes / 4096;  // loads per wave per stage
+  static_assert(kBytes % (NW * 1024) == 0, "a stage must be whole wave-loads for NW waves");
+  static constexpr int kInst = kBytes / (NW * 1024);  // loads per wave per stage
   static constexpr int kExtra = 0;
   static_assert(CPR == 4 || CPR == 8 || CPR == 16 || CPR == 32, "BK 32, 64, 128 or 256");
   // LDS serves 16 lanes of a ds_read_b128 per cycle from a 256-byte bank
@@ -123,7 +125,7 @@ struct OpMK {
 };
 
 // fp16 [k][row] with rows contiguous (a transposed operand).
-template <int ROWS, int BK>
+template <int ROWS, int BK, int NW = 4>
 struct OpKM {
   const half_t* p;
   long ld;   // halves between k rows
@@ -131,8 +133,8 @@ struct OpKM {
   static constexpr int CPR = ROWS / 8;  // chunks per k row
   static_assert(CPR >= 8, "OpKM needs at least 64 rows per tile");
   static constexpr int kBytes = ROWS * BK * 2;
-  static_assert(kBytes % 4096 == 0, "a stage must be whole wave-loads for 4 waves");
-  static constexpr int kInst = kBytes / 4096;
+  static_assert(kBytes % (NW * 1024) == 0, "a stage must be whole wave-loads for NW waves");
+  static constexpr int kInst = kBytes / (NW * 1024);
   static constexpr int kExtra = 0;
   __device__ static int swz(int k) { return 2 * (k & 3); }
   __device__ void prepare(char*, int, int) const {}
@@ -177,7 +179,7 @@ struct OpKM {
 // Packed sign bits [row][k/32] (LSB-first u32 words, row pitch `ldw` words).
 // With `scale` (fp16 bits, indexed by k), bit b becomes +-scale[k] instead of
 // +-1. The block's scale range is staged in LDS by prepare().
-template <int ROWS, int BK, bool SCALED>
+template <int ROWS, int BK, bool SCALED, int NW = 4>
 struct OpBits {
   const uint32_t* p;
   long ldw;  // words between rows
@@ -186,10 +188,11 @@ struct OpBits {
   int kofs;               // k offset into the rows (multiple of 32)
   static constexpr int WPR = BK / 32;  // words per row per stage
   static constexpr int kWords = ROWS * WPR;
-  static constexpr int kInst = kWords <= 256 ? 1 : kWords / 256;  // one word per lane per load
-  static_assert(kWords % 4 == 0 && (kInst == 1 || kWords % 256 == 0),
+  // one word per lane per load
+  static constexpr int kInst = kWords <= NW * 64 ? 1 : kWords / (NW * 64);
+  static_assert(kWords % NW == 0 && (kInst == 1 || kWords % (NW * 64) == 0),
                 "bit tile must split into whole wave loads");
-  static constexpr int kWordsPerWave = kWords / 4;
+  static constexpr int kWordsPerWave = kWords / NW;
   static constexpr int kBytes = ((kWords * 4 + 255) / 256) * 256;
   static constexpr int kMaxScaleK = 8192;
   // extra: 16-entry sign table (128 B), then the scale range when SCALED.
@@ -217,7 +220,7 @@ struct OpBits {
     }
     if constexpr (SCALED) {
       uint16_t* s = reinterpret_cast<uint16_t*>(extra + kLut);
-      for (int k = kbeg + (int)threadIdx.x; k < kend; k += kThreads) s[k - kbeg] = scale[kofs + k];
+      for (int k = kbeg + (int)threadIdx.x; k < kend; k += NW * 64) s[k - kbeg] = scale[kofs + k];
     }
   }
   __device__ __forceinline__ void issue(char* stage, int row0, int k0, int wave, int lane) const {
@@ -293,23 +296,24 @@ struct OpBits {
 // stage's fp16 tile (laid out and swizzled as OpMK's), and the fragments are
 // then plain ds_read_b128 reads. One expansion serves every wave that reads
 // the tile, which pays for 256-row tiles (four waves share each column).
-template <int ROWS, int BK>
+template <int ROWS, int BK, int NW = 4>
 struct OpBitsX {
   const uint32_t* p;
   long ldw;  // words between rows
   int rows;
   static constexpr int WPR = BK / 32;  // words per row per stage
   static constexpr int kWords = ROWS * WPR;
-  static constexpr int kInst = kWords <= 256 ? 1 : kWords / 256;  // one word per lane per load
-  static_assert(kWords % 256 == 0, "the stage's words must be whole block loads");
-  static constexpr int kWordsPerWave = kWords / 4;
+  // one word per lane per load
+  static constexpr int kInst = kWords <= NW * 64 ? 1 : kWords / (NW * 64);
+  static_assert(kWords % (NW * 64) == 0, "the stage's words must be whole block loads");
+  static constexpr int kWordsPerWave = kWords / NW;
   static constexpr int kWordBytes = ((kWords * 4 + 1023) / 1024) * 1024;
   static constexpr int CPR = BK / 8;  // 16-byte chunks per tile row
   static constexpr int kBytes = kWordBytes + ROWS * BK * 2;
   static constexpr int kExtra = 0;
   static constexpr bool kExpand = true;
   static_assert(CPR == 4 || CPR == 8 || CPR == 16 || CPR == 32, "BK 32, 64, 128 or 256");
-  __device__ static int swz(int row) { return OpMK<ROWS, BK>::swz(row); }
+  __device__ static int swz(int row) { return OpMK<ROWS, BK, NW>::swz(row); }
   __device__ void prepare(char*, int, int) const {}
   __device__ __forceinline__ void issue(char* stage, int row0, int k0, int wave, int lane) const {
 #pragma unroll
@@ -325,8 +329,8 @@ struct OpBitsX {
   __device__ __forceinline__ void expand(char* stage) const {
     char* tile = stage + kWordBytes;
 #pragma unroll
-    for (int t = 0; t < kWords / 256; ++t) {
-      const int id = t * 256 + (int)threadIdx.x;
+    for (int t = 0; t < kWords / (NW * 64); ++t) {
+      const int id = t * NW * 64 + (int)threadIdx.x;
       const uint32_t word = reinterpret_cast<const uint32_t*>(stage)[id];
       const int row = id / WPR, w = id % WPR;
 #pragma unroll
@@ -542,37 +546,38 @@ constexpr int ring_ns() {
 
 // LDS bytes of one block of the streamed-LDS GEMM: the stage ring (which the
 // epilogue reuses) and the operands' extra tables.
-template <int BM, int BN, int BK, int NS_CFG, class OA, class OB>
+template <int BM, int BN, int BK, int NS_CFG, class OA, class OB, int NW = 4>
 constexpr int lds_ring_bytes() {
   constexpr int STAGE = OA::kBytes + OB::kBytes;
   constexpr int NS = ring_ns<NS_CFG, OA, OB>();
-  return NS * STAGE > 4 * kBufFloats * 4 ? NS * STAGE : 4 * kBufFloats * 4;
+  return NS * STAGE > NW * kBufFloats * 4 ? NS * STAGE : NW * kBufFloats * 4;
 }
-template <int BM, int BN, int BK, int NS, class OA, class OB>
+template <int BM, int BN, int BK, int NS, class OA, class OB, int NW = 4>
 constexpr int lds_smem_bytes() {
-  return lds_ring_bytes<BM, BN, BK, NS, OA, OB>() + OA::kExtra + OB::kExtra;
+  return lds_ring_bytes<BM, BN, BK, NS, OA, OB, NW>() + OA::kExtra + OB::kExtra;
 }
 
 // One output tile (bid: tile index, kz: K split) of C = A . B^T in the block's
 // LDS (smem: lds_smem_bytes, 1024-byte aligned).
-template <int BM, int BN, int BK, int NS_CFG, class OA, class OB, class Epi>
+template <int BM, int BN, int BK, int NS_CFG, class OA, class OB, class Epi, int NW = 4>
 __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const OA& a,
                                               const OB& b, Epi& epi, int M, int N, int K,
                                               int k_split, const TileMap& map) {
   constexpr int NS = ring_ns<NS_CFG, OA, OB>();
-  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int WGN = NW / 2;  // waves along N
+  constexpr int WM = BM / 2, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int STAGE = OA::kBytes + OB::kBytes;
   constexpr int IPS = OA::kInst + OB::kInst;  // loads per wave per stage
   static_assert(TM >= 1 && TN >= 1, "tile too small");
   static_assert(NS >= 2 && IPS * (NS - 2) < 64, "pipeline depth");
-  constexpr int RING = lds_ring_bytes<BM, BN, BK, NS_CFG, OA, OB>();
+  constexpr int RING = lds_ring_bytes<BM, BN, BK, NS_CFG, OA, OB, NW>();
   char* extra_a = smem + RING;
   char* extra_b = extra_a + OA::kExtra;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   int tm, tn;
   tile_of_block_map(bid, tiles_n, map, tm, tn);
@@ -620,7 +625,11 @@ __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const
     // of the steps in between: at these tile sizes a wave runs alone on its
     // SIMD, and nothing else would hide it.
     constexpr int S = BK / 16;
-    constexpr int kLut = S > 3 ? 3 : S - 1;
+    // how many steps ahead a sign-bit fragment's table lookup runs: with one
+    // wave per SIMD the pipeline alone hides the LDS latency; with two, the
+    // other wave does, and a deep register ring would only cut occupancy
+    constexpr int kDepth = NW == 4 ? 3 : 1;
+    constexpr int kLut = S > kDepth ? kDepth : S - 1;
     constexpr int kPre = kLut + 1;
     constexpr int RP = kPre + 1, RR = kLut + 1;  // ring sizes
     typename OA::Pre pa[RP][TM];
@@ -669,13 +678,15 @@ __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const
                 n0 + wn * WN, lane, M, N);
 }
 
-template <int BM, int BN, int BK, int NS, class OA, class OB, class Epi>
-__global__ __launch_bounds__(256) void gemm_lds_kernel(OA a, OB b, Epi epi, int M, int N, int K,
-                                                       int k_split, TileMap map,
-                                                       unsigned long long* stamps) {
-  __shared__ __attribute__((aligned(1024))) char smem[lds_smem_bytes<BM, BN, BK, NS, OA, OB>()];
+template <int BM, int BN, int BK, int NS, class OA, class OB, class Epi, int NW = 4>
+__global__ __launch_bounds__(NW * 64) void gemm_lds_kernel(OA a, OB b, Epi epi, int M, int N,
+                                                           int K, int k_split, TileMap map,
+                                                           unsigned long long* stamps) {
+  __shared__ __attribute__((aligned(1024)))
+  char smem[lds_smem_bytes<BM, BN, BK, NS, OA, OB, NW>()];
   stamp_block_start(stamps);
-  gemm_lds_body<BM, BN, BK, NS>(smem, blockIdx.x, blockIdx.z, a, b, epi, M, N, K, k_split, map);
+  gemm_lds_body<BM, BN, BK, NS, OA, OB, Epi, NW>(smem, blockIdx.x, blockIdx.z, a, b, epi, M, N, K,
+                                                 k_split, map);
   stamp_block_end(stamps);
 }
 
@@ -685,16 +696,17 @@ struct Group {
 };
 
 // G independent problems of one shape in one launch (blockIdx.y = problem).
-template <int BM, int BN, int BK, int NS, class OA, class OB, class Epi, int G>
-__global__ __launch_bounds__(256) void gemm_lds_group_kernel(Group<OA, G> a, Group<OB, G> b,
-                                                             Group<Epi, G> epi, int M, int N,
-                                                             int K, int k_split, TileMap map,
-                                                             unsigned long long* stamps) {
-  __shared__ __attribute__((aligned(1024))) char smem[lds_smem_bytes<BM, BN, BK, NS, OA, OB>()];
+template <int BM, int BN, int BK, int NS, class OA, class OB, class Epi, int G, int NW = 4>
+__global__ __launch_bounds__(NW * 64) void gemm_lds_group_kernel(Group<OA, G> a, Group<OB, G> b,
+                                                                 Group<Epi, G> epi, int M, int N,
+                                                                 int K, int k_split, TileMap map,
+                                                                 unsigned long long* stamps) {
+  __shared__ __attribute__((aligned(1024)))
+  char smem[lds_smem_bytes<BM, BN, BK, NS, OA, OB, NW>()];
   const int g = blockIdx.y;
   stamp_block_start(stamps);
-  gemm_lds_body<BM, BN, BK, NS>(smem, blockIdx.x, blockIdx.z, a.v[g], b.v[g], epi.v[g], M, N, K,
-                                k_split, map);
+  gemm_lds_body<BM, BN, BK, NS, OA, OB, Epi, NW>(smem, blockIdx.x, blockIdx.z, a.v[g], b.v[g],
+                                                 epi.v[g], M, N, K, k_split, map);
   stamp_block_end(stamps);
 }
 
@@ -720,7 +732,8 @@ template <class P>
 struct LdsProblemSmem;
 template <class T, class OA, class OB, class Epi>
 struct LdsProblemSmem<LdsProblem<T, OA, OB, Epi>> {
-  static constexpr int value = lds_smem_bytes<T::bm, T::bn, T::bk, T::ns, OA, OB>();
+  static constexpr int value = lds_smem_bytes<T::bm, T::bn, T::bk, T::ns, OA, OB, T::nw>();
+  static constexpr int nw = T::nw;
 };
 
 template <class T, class OA, class OB, class Epi>
@@ -728,15 +741,26 @@ __device__ __forceinline__ void run_lds_problem(char* smem, const LdsProblem<T, 
                                                 int bid) {
   const int z = p.blocks == p.tiles ? 0 : bid / p.tiles;
   Epi epi = p.epi;
-  gemm_lds_body<T::bm, T::bn, T::bk, T::ns>(smem, bid - z * p.tiles, z, p.a, p.b, epi, p.M, p.N,
-                                            p.K, p.k_split, p.map);
+  gemm_lds_body<T::bm, T::bn, T::bk, T::ns, OA, OB, Epi, T::nw>(smem, bid - z * p.tiles, z, p.a,
+                                                                 p.b, epi, p.M, p.N, p.K,
+                                                                 p.k_split, p.map);
 }
 
 // Independent GEMMs (possibly of different tile configs, operand kinds and
 // epilogues) in one launch: the first ps[0].blocks blocks run ps[0], the next
 // ps[1].blocks run ps[1], ..., so the blocks of all of them share the CUs.
 template <class... Ps>
-__global__ __launch_bounds__(256) void gemm_lds_multi_kernel(unsigned long long* stamps, Ps... ps) {
+constexpr int multi_nw() {
+  constexpr int nw[] = {LdsProblemSmem<Ps>::nw...};
+  for (int w : nw)
+    if (w != nw[0]) return -1;
+  return nw[0];
+}
+
+template <class... Ps>
+__global__ __launch_bounds__(multi_nw<Ps...>() * 64) void gemm_lds_multi_kernel(
+    unsigned long long* stamps, Ps... ps) {
+  static_assert(multi_nw<Ps...>() > 0, "the problems of one launch share the wave count");
   constexpr int S = max_of(LdsProblemSmem<Ps>::value...);
   __shared__ __attribute__((aligned(1024))) char smem[S];
   int bid = blockIdx.x;
@@ -767,22 +791,22 @@ __global__ __launch_bounds__(256) void gemm_lds_multi_kernel(unsigned long long*
 // dW 16.7 -> 13.7 us, head dW 46.7 -> 36.8 us); 128x128 tiles were slower or
 // equal. BK = 64 serves contraction lengths that are not multiples of 128.
 struct LdsMid {
-  static constexpr int bm = 64, bn = 64, bk = 128, ns = 2;
+  static constexpr int bm = 64, bn = 64, bk = 128, ns = 2, nw = 4;
 };
 struct LdsShort {
-  static constexpr int bm = 64, bn = 64, bk = 64, ns = 4;
+  static constexpr int bm = 64, bn = 64, bk = 64, ns = 4, nw = 4;
 };
 struct LdsDeep {
-  static constexpr int bm = 64, bn = 64, bk = 128, ns = 4;
+  static constexpr int bm = 64, bn = 64, bk = 128, ns = 4, nw = 4;
 };
 struct LdsBig {
-  static constexpr int bm = 128, bn = 128, bk = 32, ns = 4;
+  static constexpr int bm = 128, bn = 128, bk = 32, ns = 4, nw = 4;
 };
 struct LdsHuge {
-  static constexpr int bm = 128, bn = 256, bk = 32, ns = 4;
+  static constexpr int bm = 128, bn = 256, bk = 32, ns = 4, nw = 4;
 };
 struct LdsGiant {
-  static constexpr int bm = 256, bn = 256, bk = 32, ns = 4;
+  static constexpr int bm = 256, bn = 256, bk = 32, ns = 4, nw = 4;
 };
 
 constexpr long kBigAutoBlocks = 512;
@@ -866,8 +890,8 @@ hipError_t launch_lds_group(hipStream_t s, const Group<OA, G>& a, const Group<OB
   const long tiles = cdiv(M, T::bm) * cdiv(N, T::bn);
   const int ks = (int)(cdiv(K, T::bk) * T::bk);
   unsigned long long* stamps = take_probe_stamps(tiles * G);
-  launch((gemm_lds_group_kernel<T::bm, T::bn, T::bk, T::ns, OA, OB, Epi, G>),
-         dim3((unsigned)tiles, G, 1), dim3(kThreads), 0, s, a, b, epi, (int)M, (int)N, (int)K, ks,
+  launch((gemm_lds_group_kernel<T::bm, T::bn, T::bk, T::ns, OA, OB, Epi, G, T::nw>),
+         dim3((unsigned)tiles, G, 1), dim3(T::nw * 64), 0, s, a, b, epi, (int)M, (int)N, (int)K, ks,
          tile_map_for<T, OA, OB>(M, N), stamps);
   return hipGetLastError();
 }
@@ -880,8 +904,8 @@ hipError_t launch_lds(hipStream_t s, const OA& a, const OB& b, const Epi& epi, l
   const long tiles = cdiv(M, T::bm) * cdiv(N, T::bn);
   const int ks = (int)(cdiv(cdiv(K, splits), T::bk) * T::bk);
   unsigned long long* stamps = take_probe_stamps(tiles * splits);
-  launch((gemm_lds_kernel<T::bm, T::bn, T::bk, T::ns, OA, OB, Epi>),
-         dim3((unsigned)tiles, 1, splits), dim3(kThreads), 0, s, a, b, epi, (int)M, (int)N, (int)K,
+  launch((gemm_lds_kernel<T::bm, T::bn, T::bk, T::ns, OA, OB, Epi, T::nw>),
+         dim3((unsigned)tiles, 1, splits), dim3(T::nw * 64), 0, s, a, b, epi, (int)M, (int)N, (int)K,
          ks, tile_map_for<T, OA, OB>(M, N), stamps);
   return hipGetLastError();
 }
@@ -899,8 +923,9 @@ LdsProblem<T, OA, OB, Epi> lds_problem(const OA& a, const OB& b, const Epi& epi,
 template <class T, class OA, class OB, class Epi>
 hipError_t launch_lds_problem(hipStream_t s, const LdsProblem<T, OA, OB, Epi>& p) {
   unsigned long long* stamps = take_probe_stamps(p.blocks);
-  launch((gemm_lds_kernel<T::bm, T::bn, T::bk, T::ns, OA, OB, Epi>),
-         dim3((unsigned)p.tiles, 1, (unsigned)(p.blocks / p.tiles)), dim3(kThreads), 0, s, p.a, p.b,
+  launch((gemm_lds_kernel<T::bm, T::bn, T::bk, T::ns, OA, OB, Epi, T::nw>),
+         dim3((unsigned)p.tiles, 1, (unsigned)(p.blocks / p.tiles)), dim3(T::nw * 64), 0, s, p.a,
+         p.b,
          p.epi, p.M, p.N, p.K, p.k_split, p.map, stamps);
   return hipGetLastError();
 }
@@ -909,7 +934,8 @@ hipError_t launch_lds_problem(hipStream_t s, const LdsProblem<T, OA, OB, Epi>& p
 template <class... Ps>
 hipError_t launch_lds_multi(hipStream_t s, const Ps&... ps) {
   unsigned long long* stamps = take_probe_stamps(0L + (0L + ... + ps.blocks));
-  launch((gemm_lds_multi_kernel<Ps...>), dim3((unsigned)(0 + ... + ps.blocks)), dim3(kThreads), 0,
+  launch((gemm_lds_multi_kernel<Ps...>), dim3((unsigned)(0 + ... + ps.blocks)),
+         dim3(multi_nw<Ps...>() * 64), 0,
          s, stamps, ps...);
   return hipGetLastError();
 }
