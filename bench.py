@@ -326,6 +326,59 @@ def stress_profile(rt, steps: int, warmup: int) -> None:
     tr.close()
 
 
+def rosa_live(rt, steps: int, warmup: int) -> None:
+    """One JSON line: config 4's step with the suffix automaton driven live
+    (ullis_hip_heron_step_sam: every layer's Q/K/V planes to the host, the
+    indices back) against the same step with all layers' indices given up
+    front. The host-side automaton here returns the same precomputed indices
+    at once, so the difference is the hand-off itself: the copies, the host
+    synchronisation per layer, and the Q/K/V branch moved onto the residual
+    chain."""
+    import ctypes as C
+    from ullis_amd.runtime import HeronShape, HeronTrainer
+    from ullis_amd.synth import heron_arena, step_inputs
+
+    c = CONFIG
+    shape = HeronShape(**c)
+    tr = HeronTrainer(rt, shape)
+    tr.upload_arena(heron_arena(tr.layout, tr.arena_bytes, shape.dims(), seed=7))
+    x, labels, idx = step_inputs(shape.rows, c["d_model"], c["vocab"], c["n_layers"], c["batch"],
+                                 c["time"], seed=7)
+    nd = shape.rows * c["d_model"]
+    dx, dl, di = rt.put(x), rt.put(labels), rt.put(idx)
+    g = rt.zeros(np.float32, nd)
+    idx_l = [np.ascontiguousarray(idx[l * nd:(l + 1) * nd]) for l in range(c["n_layers"])]
+    lib, ctx = rt.lib, rt.ctx
+
+    def run(live, n):
+        rt.sync()
+        rt._check(lib.ullis_hip_event_record(ctx, 0), "event")
+        t0 = time.perf_counter()
+        for _ in range(n):
+            if live:
+                tr.step_sam(lambda layer, planes: idx_l[layer], dx, dl, NO_IGNORE, LR, g)
+            else:
+                tr.step(dx, dl, NO_IGNORE, LR, di, g)
+        rt._check(lib.ullis_hip_event_record(ctx, 1), "event")
+        rt.sync()
+        wall = time.perf_counter() - t0
+        ms = C.c_float()
+        rt._check(lib.ullis_hip_event_elapsed_ms(ctx, 0, 1, C.byref(ms)), "elapsed")
+        return ms.value / n, wall * 1e3 / n
+
+    for live in (False, True):
+        run(live, warmup)
+    fused_ms, fused_wall = run(False, steps)
+    live_ms, live_wall = run(True, steps)
+    print(json.dumps({
+        "rosa_live": "config 4 (D512 L12 T2048): automaton indices handed over per layer",
+        "fused_ms_per_step": round(fused_ms, 4), "live_ms_per_step": round(live_ms, 4),
+        "live_wall_ms_per_step": round(live_wall, 4),
+        "handoff_us_per_layer": round((live_ms - fused_ms) * 1e3 / c["n_layers"], 2),
+        "steps": steps}), flush=True)
+    tr.close()
+
+
 def copy_calibration(rt, mib: int) -> None:
     """One copy kernel (ullis_hip_copy) that reads `mib` MiB and writes `mib` MiB.
 
@@ -365,6 +418,9 @@ def main() -> int:
     ap.add_argument("--stress", action="store_true",
                     help="instead of the bench line, run config 5 (the MFMA stress profile) "
                          "and print its step time and per-kernel MFMA rates")
+    ap.add_argument("--rosa-live", action="store_true",
+                    help="instead of the bench line, time the step with the suffix automaton "
+                         "driven live, layer by layer, against indices given up front")
     ap.add_argument("--graph", type=int, default=0,
                     help="1: replay each step's launches from a captured HIP graph")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -379,7 +435,8 @@ def main() -> int:
         print("bench.py: this build measures one MI355X only (no multi-GPU path); "
               "run with --gpus 1", file=sys.stderr)
         return 2
-    plain = args.decode_gemv == 0 and not args.stress and args.ln_isolated == 0
+    plain = (args.decode_gemv == 0 and not args.stress and args.ln_isolated == 0 and
+             not args.rosa_live)
     # the CPU baseline's child processes start before this process touches the GPU
     baseline = (cpu_baseline(args.cpu_rows, max(1, args.cpu_runs))
                 if plain and args.cpu_rows > 0 else None)
@@ -398,6 +455,9 @@ def main() -> int:
         return 0
     if args.ln_isolated > 0:
         layer_norm_isolated(rt, args.ln_isolated)
+        return 0
+    if args.rosa_live:
+        rosa_live(rt, args.steps, args.warmup)
         return 0
     trainer = HeronTrainer(rt, shape)
     arena = heron_arena(trainer.layout, trainer.arena_bytes, shape.dims(), seed=7)

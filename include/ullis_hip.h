@@ -312,6 +312,55 @@ int ullis_hip_heron_step_tokens(ullis_hip_heron* h, uint16_t* table, float* tabl
                                 float* x_emb, float* g_emb, float* row_loss, float* stats4,
                                 uint32_t* qkv_bits, uint32_t* invalid);
 /*
+ * The suffix automaton driven live, layer by layer (MetalRuntime::
+ * rosa_block_forward's hand-off, src/metal.rs:1411-1511; the automaton is
+ * rosa_qkv_batch_packed_channel_major, src/rosa.rs:486-513, and stays with the
+ * caller). ullis_hip_heron_step_sam runs the step of ullis_hip_heron_step
+ * (from token ids when table is non-NULL, as ullis_hip_heron_step_tokens,
+ * else from the rows in x_emb), except that no indices are given up front:
+ * for each layer l it computes the Q/K/V sign bit-planes, copies them to
+ * pinned host memory and calls sam(user, l, planes, idx) on the calling
+ * thread. planes holds 3 x ceil(batch*time*d/32) u32 words (Q, K, V; bit
+ * row*d + c = projection > 0, LSB-first); the callback writes the layer's
+ * indices into idx (batch*d*time u8, channel-major [batch][d][time], pinned
+ * host memory) and returns 0, or non-zero to abort the step before any
+ * parameter changes. Both buffers are the library's and are reused for the
+ * next layer once the callback returns. The call blocks the host on each
+ * layer's planes; it never replays a step graph. Other arguments as for
+ * ullis_hip_heron_step / ullis_hip_heron_step_tokens.
+ */
+typedef int (*ullis_hip_sam_fn)(void* user, size_t layer, const uint32_t* planes, uint8_t* idx);
+int ullis_hip_heron_step_sam(ullis_hip_heron* h, uint16_t* table, float* table_residual,
+                             size_t vocab, const uint32_t* tokens, float* x_emb,
+                             const uint32_t* labels, uint32_t ignore_id, float learning_rate,
+                             ullis_hip_sam_fn sam, void* sam_user, float* g_emb, float* row_loss,
+                             float* stats4, uint32_t* qkv_bits, uint32_t* invalid);
+
+/*
+ * T = 1 greedy decode (UllisHeron::generate_step, src/model.rs:2717-2753; the
+ * reference runs it on the CPU): one token for each of `batch` sequences
+ * (1..8) through every block's forward_one (src/model.rs:2243-2262) on the
+ * trainer's parameters. ullis_hip_heron_decode_init(h, batch) sizes the
+ * decode state and starts new sequences (no previous token: the time-shift
+ * mixes see -x, as time_shift_one, src/model.rs:214-228); each
+ * ullis_hip_heron_decode_step then takes tokens (device u32 [batch]; an id
+ * >= vocab gathers a zero row and is counted into *invalid, device u32,
+ * optional), writes logits (device fp32 [batch][vocab]) and, when non-NULL,
+ * next_tokens (device u32 [batch], the argmax, lowest index on ties), and keeps
+ * each layer's LayerNorm outputs as the next token's previous values. The
+ * suffix automaton's indices of this token come either from rosa_idx (device
+ * u8 [n_layers][batch][d]) or from the callback, called per layer with the
+ * Q/K/V sign bits (3 x ceil(batch*d/32) words, bit b*d + c) and writing idx
+ * [batch][d] (sam / sam_user as for ullis_hip_heron_step_sam); exactly one
+ * of the two. The reference's context_len limit is the caller's to keep.
+ */
+int ullis_hip_heron_decode_init(ullis_hip_heron* h, size_t batch);
+int ullis_hip_heron_decode_step(ullis_hip_heron* h, const uint16_t* table, size_t vocab,
+                                const uint32_t* tokens, const uint8_t* rosa_idx,
+                                ullis_hip_sam_fn sam, void* sam_user, float* logits,
+                                uint32_t* next_tokens, uint32_t* invalid);
+
+/*
  * CausalLoss of the last step (src/model.rs:58-80, as train_step_on fills it,
  * src/model.rs:2997-3024), into *out (DEVICE memory, sizeof(ullis_hip_causal_loss)
  * bytes): loss, valid count, sign-bit flips per class (head, CMix key, ROSA

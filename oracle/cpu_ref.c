@@ -1159,3 +1159,152 @@ done:
   free(a.descs);
   return rc;
 }
+
+/* ------------------------------------------------------- T = 1 decode ---- */
+
+/* time_shift_one, src/model.rs:214-228: prev - x, or -x without a previous token */
+static void time_shift_one(const float* x, const float* prev, int has_prev, size_t d, float* xx) {
+  size_t c;
+  for (c = 0; c < d; ++c) xx[c] = has_prev ? prev[c] - x[c] : -x[c];
+}
+
+/*
+ * One token per sequence of UllisHeron::generate_step (src/model.rs:2717-2753):
+ * embedding row, every block's forward_one (src/model.rs:2243-2262; ROSA
+ * forward_one src/model.rs:1320-1353, CMix forward_one src/model.rs:1003-1016),
+ * ln_out, head. The suffix automaton's idx for this token is given
+ * ([n_layers][batch][d] u8) instead of RosaSam::push; the Q/K/V sign bits it
+ * would have been pushed (bit_from_activation = value > 0, src/rosa.rs:372)
+ * go to qkv_bits ([n_layers][3][batch][d] u8) when non-NULL. rosa_prev /
+ * cmix_prev ([n_layers][batch][d]) are the state's x_prev, read when has_prev
+ * and overwritten with this token's values; logits [batch][vocab].
+ */
+int ucr_heron_decode_step(const ullis_heron_dims* dims, uint8_t* arena, const uint16_t* table,
+                          const uint32_t* tokens, size_t batch, const uint8_t* idx,
+                          float* rosa_prev, float* cmix_prev, int has_prev, float* logits,
+                          uint8_t* qkv_bits) {
+  size_t d = dims->d_model, f = dims->dim_ffn, v = dims->vocab, L = dims->n_layers;
+  size_t b, layer, c, i;
+  uint64_t total;
+  arena_view a;
+  ln_view ln_out;
+  packed_view head;
+  float *x = NULL, *h = NULL, *tmp = NULL, *xx = NULL, *qi = NULL, *q = NULL, *k = NULL;
+  float *vv = NULL, *y = NULL, *key = NULL, *relu2 = NULL;
+  int rc = 0;
+  a.n = ullis_heron_layout(dims, NULL, 0, &total);
+  a.descs = (ullis_tensor_desc*)calloc(a.n, sizeof(ullis_tensor_desc));
+  if (!a.descs) return -1;
+  ullis_heron_layout(dims, a.descs, a.n, &total);
+  a.base = arena;
+  XMALLOC(x, d);
+  XMALLOC(h, d);
+  XMALLOC(tmp, d);
+  XMALLOC(xx, d);
+  XMALLOC(qi, d);
+  XMALLOC(q, d);
+  XMALLOC(k, d);
+  XMALLOC(vv, d);
+  XMALLOC(y, d);
+  XMALLOC(key, f);
+  XMALLOC(relu2, f);
+  if (ln_bind(&a, "ln_out", &ln_out) || packed_bind(&a, "head", v, d, 1, &head)) {
+    rc = -3;
+    goto done;
+  }
+  for (b = 0; b < batch; ++b) {
+    if (tokens[b] >= v) { rc = -2; goto done; }
+    for (c = 0; c < d; ++c) x[c] = ucr_f16_to_f32(table[(size_t)tokens[b] * d + c]);
+    for (layer = 0; layer < L; ++layer) {
+      char p[ULLIS_NAME_MAX];
+      ln_view ln2, ln3;
+      packed_view pq, pk, pv, po, kp;
+      uint16_t *x_q, *x_k, *x_v, *e, *cx_k, *value;
+      float* rp = rosa_prev + (layer * batch + b) * d;
+      float* cp = cmix_prev + (layer * batch + b) * d;
+      const uint8_t* id = idx + (layer * batch + b) * d;
+#define DBIND(view, name, out_, in_, bias_)                                  \
+  snprintf(p, sizeof p, "blocks.%zu." name, layer);                          \
+  if (packed_bind(&a, p, out_, in_, bias_, &view)) { rc = -3; goto done; }
+#define DTBIND(var, name)                                \
+  snprintf(p, sizeof p, "blocks.%zu." name, layer);      \
+  var = tensor_ptr(&a, p);                               \
+  if (!var) { rc = -3; goto done; }
+      snprintf(p, sizeof p, "blocks.%zu.ln2", layer);
+      if (ln_bind(&a, p, &ln2)) { rc = -3; goto done; }
+      snprintf(p, sizeof p, "blocks.%zu.ln3", layer);
+      if (ln_bind(&a, p, &ln3)) { rc = -3; goto done; }
+      DBIND(pq, "rosa.q", d, d, 1);
+      DBIND(pk, "rosa.k", d, d, 1);
+      DBIND(pv, "rosa.v", d, d, 1);
+      DBIND(po, "rosa.o", d, d, 1);
+      DBIND(kp, "ffn.key", f, d, 0);
+      DTBIND(x_q, "rosa.x_q");
+      DTBIND(x_k, "rosa.x_k");
+      DTBIND(x_v, "rosa.x_v");
+      DTBIND(e, "rosa.e");
+      DTBIND(cx_k, "ffn.x_k");
+      DTBIND(value, "ffn.value");
+      if (layer == 0) { /* forward_one: h = ln0(x) */
+        ln_view ln0;
+        snprintf(p, sizeof p, "blocks.%zu.ln0", layer);
+        if (ln_bind(&a, p, &ln0)) { rc = -3; goto done; }
+        ucr_layer_norm_forward(x, 1, d, ln0.w, ln0.b, h);
+      } else {
+        memcpy(h, x, d * sizeof(float));
+      }
+      /* ROSA forward_one (src/model.rs:1320-1353) */
+      ucr_layer_norm_forward(h, 1, d, ln3.w, ln3.b, tmp); /* rosa_in */
+      time_shift_one(tmp, rp, has_prev, d, xx);
+      for (c = 0; c < d; ++c) qi[c] = tmp[c] + xx[c] * ucr_f16_to_f32(x_q[c]);
+      ucr_packed_forward(qi, 1, d, d, pq.bits, pq.scale, pq.bias, q);
+      for (c = 0; c < d; ++c) qi[c] = tmp[c] + xx[c] * ucr_f16_to_f32(x_k[c]);
+      ucr_packed_forward(qi, 1, d, d, pk.bits, pk.scale, pk.bias, k);
+      for (c = 0; c < d; ++c) qi[c] = tmp[c] + xx[c] * ucr_f16_to_f32(x_v[c]);
+      ucr_packed_forward(qi, 1, d, d, pv.bits, pv.scale, pv.bias, vv);
+      if (qkv_bits) {
+        uint8_t* qb = qkv_bits + (layer * 3) * batch * d + b * d;
+        for (c = 0; c < d; ++c) {
+          qb[c] = q[c] > 0.0f;
+          qb[batch * d + c] = k[c] > 0.0f;
+          qb[2 * batch * d + c] = vv[c] > 0.0f;
+        }
+      }
+      for (c = 0; c < d; ++c) y[c] = (2.0f * (float)id[c] - 1.0f) * ucr_f16_to_f32(e[c]);
+      memcpy(rp, tmp, d * sizeof(float)); /* layer.rosa_x_prev = Some(rosa_in) */
+      ucr_packed_forward(y, 1, d, d, po.bits, po.scale, po.bias, tmp);
+      for (c = 0; c < d; ++c) h[c] += tmp[c];
+      /* CMix forward_one (src/model.rs:1003-1016) */
+      ucr_layer_norm_forward(h, 1, d, ln2.w, ln2.b, tmp); /* ffn_in */
+      time_shift_one(tmp, cp, has_prev, d, xx);
+      for (c = 0; c < d; ++c) qi[c] = tmp[c] + xx[c] * ucr_f16_to_f32(cx_k[c]);
+      memcpy(cp, tmp, d * sizeof(float)); /* layer.cmix_x_prev = Some(ffn_in) */
+      ucr_packed_forward(qi, 1, d, f, kp.bits, kp.scale, NULL, key);
+      for (i = 0; i < f; ++i) {
+        const float kv = key[i] > 0.0f ? key[i] : 0.0f;
+        relu2[i] = kv * kv;
+      }
+      ucr_fp16_forward(relu2, 1, f, d, value, tmp);
+      for (c = 0; c < d; ++c) h[c] += tmp[c];
+      memcpy(x, h, d * sizeof(float));
+#undef DBIND
+#undef DTBIND
+    }
+    ucr_layer_norm_forward(x, 1, d, ln_out.w, ln_out.b, h);
+    ucr_packed_forward(h, 1, d, v, head.bits, head.scale, head.bias, logits + b * v);
+  }
+done:
+  free(x);
+  free(h);
+  free(tmp);
+  free(xx);
+  free(qi);
+  free(q);
+  free(k);
+  free(vv);
+  free(y);
+  free(key);
+  free(relu2);
+  free(a.descs);
+  return rc;
+}

@@ -135,6 +135,16 @@ int ucr_heron_train_step(const ullis_heron_dims* dims, uint8_t* arena, const flo
                          float learning_rate, const uint8_t* rosa_idx, float* g_emb,
                          float* row_loss, uint32_t* qkv_bits, ucr_step_stats* stats);
 
+/* T = 1 decode of generate_step (src/model.rs:2717-2753) for `batch` sequences,
+ * the automaton's indices of this token given ([n_layers][batch][d]);
+ * rosa_prev / cmix_prev [n_layers][batch][d] are read when has_prev and
+ * overwritten; logits [batch][vocab]; qkv_bits (optional) the Q/K/V sign bits
+ * [n_layers][3][batch][d] u8. */
+int ucr_heron_decode_step(const ullis_heron_dims* dims, uint8_t* arena, const uint16_t* table,
+                          const uint32_t* tokens, size_t batch, const uint8_t* idx,
+                          float* rosa_prev, float* cmix_prev, int has_prev, float* logits,
+                          uint8_t* qkv_bits);
+
 /* Embedding gather and sequential scatter SGD (src/model.rs:2866-2873, 2986-2993). */
 int ucr_embedding_gather(const uint16_t* table, size_t d, const uint32_t* tokens, size_t rows,
                          float* x);

@@ -65,6 +65,7 @@ def lib() -> C.CDLL:
                      "ucr_mean_abs_delta_fp16", "ucr_unigram_cross_entropy"]:
             getattr(_LIB, name).restype = C.c_float
         _LIB.ucr_head_ce_horizon.restype = C.c_int
+        _LIB.ucr_heron_decode_step.restype = C.c_int
         _LIB.ucr_heron_layout.restype = C.c_size_t
         _LIB.ucr_heron_layout.argtypes = [C.POINTER(HeronDims), C.POINTER(TensorDesc), C.c_size_t,
                                           C.POINTER(C.c_uint64)]
@@ -231,6 +232,28 @@ def head_ce(hidden, rows, time, d, vocab, bits, scale, bias, targets, ignore_id,
     return {"mean_loss": mean.value, "n_valid": nv.value, "row_loss": row_loss,
             "hidden_gradient": g_h, "weight_gradient": g_w, "scale_gradient": g_s,
             "bias_gradient": g_b}
+
+
+# ------------------------------------------------------------ T = 1 decode
+def heron_decode_step(dims: HeronDims, arena: np.ndarray, table, tokens, idx, rosa_prev,
+                      cmix_prev, has_prev: bool):
+    """generate_step for len(tokens) sequences with the automaton's indices given
+    ([n_layers][batch][d] u8). rosa_prev / cmix_prev (float32 [n_layers*batch*d])
+    are updated in place. Returns (logits [batch, vocab], qkv_bits u8
+    [n_layers, 3, batch, d])."""
+    t = _u32(tokens)
+    batch = t.size
+    assert rosa_prev.dtype == np.float32 and cmix_prev.dtype == np.float32
+    logits = np.zeros(batch * dims.vocab, np.float32)
+    qkv = np.zeros(dims.n_layers * 3 * batch * dims.d_model, np.uint8)
+    rc = lib().ucr_heron_decode_step(C.byref(dims), _p(arena), _p(_u16(table)), _p(t),
+                                     _sz(batch), _p(np.ascontiguousarray(idx, np.uint8)),
+                                     _p(rosa_prev), _p(cmix_prev), C.c_int(int(has_prev)),
+                                     _p(logits), _p(qkv))
+    if rc != 0:
+        raise RuntimeError(f"ucr_heron_decode_step failed: {rc}")
+    return (logits.reshape(batch, dims.vocab),
+            qkv.reshape(dims.n_layers, 3, batch, dims.d_model))
 
 
 # ---------------------------------------------------- CausalLoss statistics

@@ -375,3 +375,104 @@ def test_block_step_matches_fused_step(rt, d, layers, f, vocab, time):
                                       tensor_view(fa, fused.layout, name), err_msg=name)
     blocks.close()
     fused.close()
+
+
+def stand_in_sam(batch, time, d):
+    """A deterministic stand-in for the suffix automaton: its indices are a
+    function of the sign bit-planes it is handed, as the automaton's are
+    (rosa_qkv_batch_packed_channel_major, src/rosa.rs:486-513):
+    idx[b, c, t] = q[t] xor k[t - 1] xor v[t - 2] of channel c (zero before
+    the sequence's start), returned channel-major [batch][d][time]."""
+    n = batch * time * d
+
+    def sam(qp, kp, vp):
+        q, k, v = (unpack_bits(p, n).reshape(batch, time, d).astype(np.uint8) for p in (qp, kp, vp))
+        idx = q.copy()
+        idx[:, 1:, :] ^= k[:, :-1, :]
+        idx[:, 2:, :] ^= v[:, :-2, :]
+        return np.ascontiguousarray(idx.transpose(0, 2, 1)).ravel()
+
+    return sam
+
+
+@pytest.mark.parametrize("d,layers,f,vocab,batch,time", [(64, 2, 128, 256, 2, 64),
+                                                         (512, 2, 2048, 8192, 1, 512)])
+def test_live_automaton_step_matches_block_path(rt, d, layers, f, vocab, batch, time):
+    """ullis_hip_heron_step_sam (the fused step handing each layer's Q/K/V sign
+    bit-planes to the caller's automaton and taking its indices back,
+    src/metal.rs:1411-1511) against the block path (HeronBlockStep) driving the
+    same stand-in automaton on its own planes: bit-identical arena, row losses,
+    statistics and embedding gradient, and the automaton sees the same planes
+    on both paths."""
+    shape = HeronShape(d_model=d, n_layers=layers, dim_ffn=f, vocab=vocab, batch=batch, time=time)
+    fused = HeronTrainer(rt, shape)
+    blocks = HeronBlockStep(rt, shape)
+    arena = heron_arena(fused.layout, fused.arena_bytes, shape.dims(), seed=6, random_ln=True)
+    x, labels, _ = step_inputs(shape.rows, d, vocab, layers, batch, time, seed=6)
+    nd = shape.rows * d
+    words = (nd + 31) // 32
+    automaton = stand_in_sam(batch, time, d)
+
+    fused.upload_arena(arena)
+    seen_fused = []
+
+    def sam_fused(layer, planes):
+        seen_fused.append((layer, planes.copy()))
+        return automaton(planes[0], planes[1], planes[2])
+
+    dx, dl = rt.put(x), rt.put(labels)
+    g = rt.zeros(np.float32, nd)
+    rl = rt.zeros(np.float32, shape.rows)
+    st = rt.zeros(np.float32, 4)
+    qkv = rt.zeros(np.uint32, layers * 3 * words)
+    fused.step_sam(sam_fused, dx, dl, NO_IGNORE, 0.01, g, rl, st, qkv)
+    rt.sync()
+    fa, fg, frl = fused.download_arena(), g.download(np.float32), rl.download(np.float32)
+    fst, fq = st.download(np.float32), qkv.download(np.uint32).reshape(layers, 3, words)
+
+    blocks.upload_arena(arena)
+    seen_blocks = []
+
+    def sam_blocks(layer, qp, kp, vp):
+        seen_blocks.append(layer)
+        return automaton(qp, kp, vp)
+
+    out = blocks.step(x, labels, NO_IGNORE, 0.01, sam_blocks)
+    ba = blocks.download_arena()
+    assert [l for l, _ in seen_fused] == seen_blocks == list(range(layers))
+    for l, planes in seen_fused:
+        for j in range(3):
+            np.testing.assert_array_equal(planes[j], fq[l, j])
+            np.testing.assert_array_equal(out["qkv_planes"][l][j], fq[l, j], err_msg=f"{l}/{j}")
+    np.testing.assert_array_equal(out["stats"][:3], fst[:3])
+    np.testing.assert_array_equal(out["row_loss"].view(np.uint32), frl.view(np.uint32))
+    np.testing.assert_array_equal(out["g_emb"].view(np.uint32), fg.view(np.uint32))
+    for name, _dt, _count, _off, _derived in fused.layout:
+        np.testing.assert_array_equal(tensor_view(ba, fused.layout, name),
+                                      tensor_view(fa, fused.layout, name), err_msg=name)
+    blocks.close()
+    fused.close()
+
+
+def test_live_automaton_failure_aborts_before_any_update(rt):
+    """An automaton that fails (non-zero from the callback, here at the second
+    layer) ends the step with an error before any parameter changes."""
+    shape = HeronShape(d_model=64, n_layers=3, dim_ffn=128, vocab=256, batch=1, time=32)
+    tr = HeronTrainer(rt, shape)
+    arena = heron_arena(tr.layout, tr.arena_bytes, shape.dims(), seed=8)
+    x, labels, _ = step_inputs(shape.rows, 64, 256, 3, 1, 32, seed=8)
+    tr.upload_arena(arena)
+    before = tr.download_arena()
+    automaton = stand_in_sam(1, 32, 64)
+
+    def sam(layer, planes):
+        if layer == 1:
+            raise RuntimeError("automaton failed")
+        return automaton(planes[0], planes[1], planes[2])
+
+    g = rt.zeros(np.float32, shape.rows * 64)
+    with pytest.raises(RuntimeError, match="automaton failed"):
+        tr.step_sam(sam, rt.put(x), rt.put(labels), NO_IGNORE, 0.01, g)
+    rt.sync()
+    np.testing.assert_array_equal(tr.download_arena(), before)
+    tr.close()

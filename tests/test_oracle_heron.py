@@ -304,3 +304,46 @@ def test_oracle_heron_step_matches_float64_rederivation(d, layers, ffn, vocab, b
         bits = tensor_view(arena, layout, name + ".bits")
         np.testing.assert_array_equal(bits, pack_bits((pk.sign > 0).ravel()), err_msg=name)
 
+
+
+def test_oracle_decode_matches_the_train_forward_row_by_row():
+    """ucr_heron_decode_step (generate_step, src/model.rs:2717-2753) fed the
+    tokens of a sequence one at a time, with the automaton's indices of each
+    position, reproduces the train step's forward: the CE of its logits at
+    position t against label t + 1 equals the train step's row loss (the
+    reference's generate_step_logits_match_one_shot_hidden, src/model.rs:
+    4991-5043, states the same equivalence), and the Q/K/V sign bits it
+    produces are the train step's bit-planes. The train step's forward is
+    pinned by the float64 re-derivation above."""
+    d, layers, ffn, vocab, batch, time = 64, 2, 128, 256, 2, 12
+    dims = o.HeronDims(d, layers, ffn, vocab)
+    layout, total = o.heron_layout(dims)
+    arena = heron_arena(layout, total, dims, seed=21, random_ln=True, mix_range=(0.2, 0.8))
+    rng = np.random.default_rng(21)
+    table = rng.standard_normal(vocab * d).astype(np.float16).view(np.uint16)
+    tokens = rng.integers(0, vocab, batch * time).astype(np.uint32)
+    labels = np.roll(tokens, -1).astype(np.uint32)
+    _, _, idx = step_inputs(batch * time, d, vocab, layers, batch, time, seed=21)
+    x = o.embedding_gather(table, d, tokens)
+    train = o.heron_train_step(dims, arena.copy(), x, labels, NO_IGNORE, batch, time, 1e-3, idx)
+    # idx [L][B][D][T] channel-major -> per token [L][B][D]
+    idx4 = idx.reshape(layers, batch, d, time)
+    planes = unpack_bits(train["qkv_bits"], layers * 3 * ((batch * time * d + 31) // 32) * 32)
+    words = (batch * time * d + 31) // 32
+    planes = planes.reshape(layers, 3, words * 32)[:, :, :batch * time * d].reshape(
+        layers, 3, batch, time, d)
+    rp = np.zeros(layers * batch * d, np.float32)
+    cp = np.zeros(layers * batch * d, np.float32)
+    tok = tokens.reshape(batch, time)
+    for t in range(time):
+        logits, qkv = o.heron_decode_step(dims, arena, table, tok[:, t],
+                                          np.ascontiguousarray(idx4[:, :, :, t]), rp, cp, t > 0)
+        np.testing.assert_array_equal(qkv, planes[:, :, :, t, :], err_msg=f"bits at t={t}")
+        if t + 1 >= time:
+            continue
+        lg = logits.astype(np.float64)
+        for b in range(batch):
+            m = lg[b].max()
+            # the train step scores row r against labels[r + 1] (horizon 1)
+            ce = m + np.log(np.exp(lg[b] - m).sum()) - lg[b, labels[b * time + t + 1]]
+            assert abs(ce - train["row_loss"][b * time + t]) <= 1e-5, (t, b)

@@ -69,6 +69,10 @@ class CausalLoss(C.Structure):
         return {name: getattr(self, name) for name, _ in self._fields_}
 
 
+# ullis_hip_sam_fn: int (*)(void* user, size_t layer, const uint32_t* planes, uint8_t* idx)
+SAM_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_size_t, C.POINTER(C.c_uint32),
+                     C.POINTER(C.c_uint8))
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "ullis_hip_version": (i32, []),
@@ -123,6 +127,10 @@ SIGNATURES = {
     "ullis_hip_heron_refresh_derived": (i32, [vp]),
     "ullis_hip_heron_step": (i32, [vp, vp, vp, u32, f32, vp, vp, vp, vp, vp, vp]),
     "ullis_hip_heron_causal_loss": (i32, [vp, vp, vp, u32, vp, vp, sz, vp]),
+    "ullis_hip_heron_decode_init": (i32, [vp, sz]),
+    "ullis_hip_heron_decode_step": (i32, [vp, vp, sz, vp, vp, SAM_FN, vp, vp, vp, vp]),
+    "ullis_hip_heron_step_sam": (i32, [vp, vp, vp, sz, vp, vp, vp, u32, f32, SAM_FN, vp, vp, vp,
+                                      vp, vp, vp]),
     "ullis_hip_heron_step_tokens": (i32, [vp, vp, vp, sz, vp, vp, u32, f32, vp, vp, vp, vp, vp,
                                          vp, vp]),
     "ullis_hip_heron_set_graph": (i32, [vp, i32]),

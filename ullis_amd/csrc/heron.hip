@@ -148,6 +148,28 @@ struct ullis_hip_heron {
   const uint16_t* const* e_dev = nullptr;
   uint32_t* qkv = nullptr;
   void* head_ws = nullptr;
+  // live suffix automaton (ullis_hip_heron_step_sam), allocated on first use:
+  // pinned host planes of one layer and indices of one layer, the device
+  // indices of every layer, and the event the host waits on
+  uint32_t* sam_planes_host = nullptr;
+  uint8_t* sam_idx_host = nullptr;
+  uint8_t* sam_idx_dev = nullptr;
+  hipEvent_t ev_sam = nullptr;
+  // T = 1 decode state (ullis_hip_heron_decode_*), one allocation
+  struct Decode {
+    long batch = 0;
+    bool has_prev = false;
+    void* mem = nullptr;
+    float *rosa_prev = nullptr, *cmix_prev = nullptr;  // [L][batch][D]
+    float *x = nullptr, *ln = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;  // [batch][D]
+    uint16_t *q16 = nullptr, *k16 = nullptr, *v16 = nullptr, *y16 = nullptr, *sh16 = nullptr;
+    uint16_t *hid16 = nullptr, *r2_16 = nullptr;  // [batch][D], [batch][F]
+    uint8_t *idx = nullptr, *idx_rm = nullptr;    // [batch][D]
+    uint32_t* planes = nullptr;                   // [3][words]
+    uint32_t* invalid = nullptr;
+    uint32_t* planes_host = nullptr;              // pinned
+    uint8_t* idx_host = nullptr;                  // pinned
+  } dec;
   int splits_o = 1, splits_key = 1, splits_value = 1;
   // kernel probe: events around every launch of one launch class
   int probe = 0;
@@ -668,6 +690,13 @@ void ullis_hip_heron_destroy(ullis_hip_heron* h) {
   if (h->act) (void)hipFree(h->act);
   if (h->job_mem) (void)hipFree(h->job_mem);
   if (h->probe_stamps) (void)hipFree(h->probe_stamps);
+  if (h->sam_planes_host) (void)hipHostFree(h->sam_planes_host);
+  if (h->sam_idx_host) (void)hipHostFree(h->sam_idx_host);
+  if (h->sam_idx_dev) (void)hipFree(h->sam_idx_dev);
+  if (h->ev_sam) (void)hipEventDestroy(h->ev_sam);
+  if (h->dec.mem) (void)hipFree(h->dec.mem);
+  if (h->dec.planes_host) (void)hipHostFree(h->dec.planes_host);
+  if (h->dec.idx_host) (void)hipHostFree(h->dec.idx_host);
   if (h->graph_exec) (void)hipGraphExecDestroy(h->graph_exec);
   delete h;
 }
@@ -764,10 +793,17 @@ struct EmbedArgs {
 // stream (arguments checked by ullis_hip_heron_step). With emb, the
 // embedding scatter-SGD of g_emb runs as soon as g_emb is complete, beside
 // the second stream's last updates.
+// The suffix automaton of a step driven live, layer by layer, by the
+// caller's callback (ullis_hip_heron_step_sam).
+struct SamHandoff {
+  ullis_hip_sam_fn fn;
+  void* user;
+};
+
 int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels,
                   uint32_t ignore_id, float lr, const uint8_t* rosa_idx, float* g_emb,
                   float* row_loss, float* stats4, uint32_t* qkv_bits, uint32_t* invalid_out,
-                  const EmbedArgs* emb = nullptr) {
+                  const EmbedArgs* emb = nullptr, const SamHandoff* live = nullptr) {
   ullis_hip_ctx* c = h->ctx;
   hipStream_t s = c->stream;
   const long R = h->rows, D = h->D, F = h->F, L = h->L, T = h->time, B = h->batch;
@@ -784,8 +820,11 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
   if (!emb) STEP(fill_f32(s, reinterpret_cast<float*>(h->invalid), 1, 0.0f), "clear invalid");
   // y = (2 idx - 1) e (e is not updated before the step's end): layer 0's
   // here, the other layers' on the second stream after layer 0's O product
-  STEP(rosa_expand_layers(s, rosa_idx, h->e_host.data(), h->e_dev, 1, B, T, D, h->y16, h->idx_rm),
-       "rosa y");
+  // (with a live automaton, each layer's once its indices are back)
+  if (!live)
+    STEP(rosa_expand_layers(s, rosa_idx, h->e_host.data(), h->e_dev, 1, B, T, D, h->y16,
+                            h->idx_rm),
+         "rosa y");
   // The O products of every layer (src/model.rs:1428) read only y and the O
   // weights, all final here (updates run at the step's end): the second
   // stream computes them ahead of their layers, and each layer's LN2 adds its
@@ -804,11 +843,13 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
   };
   STEP(hipEventRecord(h->ev_start, s), "event");
   STEP(hipStreamWaitEvent(h->side, h->ev_start, 0), "event wait");
-  if (int rc = o_forward(0)) return rc;
-  if (L > 1)
-    STEP(rosa_expand_layers(h->side, rosa_idx + nd, h->e_host.data() + 1, h->e_dev + 1, L - 1, B,
-                            T, D, h->y16 + nd, h->idx_rm + nd),
-         "rosa y");
+  if (!live) {
+    if (int rc = o_forward(0)) return rc;
+    if (L > 1)
+      STEP(rosa_expand_layers(h->side, rosa_idx + nd, h->e_host.data() + 1, h->e_dev + 1, L - 1,
+                              B, T, D, h->y16 + nd, h->idx_rm + nd),
+           "rosa y");
+  }
 
   // ------------------------------------------------------------- forward
   for (long l = 0; l < L; ++l) {
@@ -819,13 +860,19 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
     } else if (l == 0) {
       STEP(copy_device(s, x_l, x_emb, (long)sizeof(float) * nd), "copy x");
     }
-    // ROSA block (src/model.rs:1354-1440). The Q/K/V branch runs on the
-    // second stream once x_l is complete.
-    STEP(hipEventRecord(h->ev_fwd[l], s), "event");
-    STEP(hipStreamWaitEvent(h->side, h->ev_fwd[l], 0), "event wait");
-    if (l + 1 < L)
-      if (int rc = o_forward(l + 1)) return rc;
-    STEP(layer_norm_mix_forward(h->side, x_l, R, T, D, b.ln3.w, b.ln3.b, h->ln3_16, false, b.x_q,
+    // ROSA block (src/model.rs:1354-1440). With the automaton's indices
+    // given, the Q/K/V branch runs on the second stream once x_l is
+    // complete; with a live automaton it is on the residual chain: Q/K/V,
+    // their sign bit-planes to the host, the caller's automaton, the indices
+    // back, y = (2 idx - 1) e and the O product (src/metal.rs:1411-1511).
+    hipStream_t qs = live ? s : h->side;
+    if (!live) {
+      STEP(hipEventRecord(h->ev_fwd[l], s), "event");
+      STEP(hipStreamWaitEvent(h->side, h->ev_fwd[l], 0), "event wait");
+      if (l + 1 < L)
+        if (int rc = o_forward(l + 1)) return rc;
+    }
+    STEP(layer_norm_mix_forward(qs, x_l, R, T, D, b.ln3.w, b.ln3.b, h->ln3_16, false, b.x_q,
                                 h->q16, b.x_k, h->k16, b.x_v, h->v16),
          "ln3 + mix3");
     {
@@ -835,7 +882,31 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
       const uint16_t* const bi[3] = {b.q.bias, b.k.bias, b.v.bias};
       uint32_t* const planes[3] = {qkv + (l * 3 + 0) * words, qkv + (l * 3 + 1) * words,
                                    qkv + (l * 3 + 2) * words};
-      STEP(packed_forward_bits3(h->side, xin, R, D, D, wb, sc, bi, planes), "qkv");
+      STEP(packed_forward_bits3(qs, xin, R, D, D, wb, sc, bi, planes), "qkv");
+    }
+    if (live) {
+      // planes out (pinned host memory), the callback, indices back
+      STEP(hipMemcpyAsync(h->sam_planes_host, qkv + l * 3 * words, sizeof(uint32_t) * 3 * words,
+                          hipMemcpyDeviceToHost, s),
+           "planes to host");
+      STEP(hipEventRecord(h->ev_sam, s), "event");
+      STEP(hipEventSynchronize(h->ev_sam), "planes sync");
+      const int cb = live->fn(live->user, (size_t)l, h->sam_planes_host, h->sam_idx_host);
+      if (cb != 0)
+        return c->fail(ULLIS_HIP_ERR_INVALID, "suffix automaton callback failed at layer " +
+                                                  std::to_string(l) + " (" + std::to_string(cb) +
+                                                  ")");
+      STEP(hipMemcpyAsync(h->sam_idx_dev + l * nd, h->sam_idx_host, (size_t)nd,
+                          hipMemcpyHostToDevice, s),
+           "indices to device");
+      STEP(rosa_expand_layers(s, h->sam_idx_dev + l * nd, h->e_host.data() + l, h->e_dev + l, 1, B,
+                              T, D, h->y16 + l * nd, h->idx_rm + l * nd),
+           "rosa y");
+      const Block& bo = h->blocks[l];
+      PackedFwdOut o;
+      o.y32 = h->o_pre + l * nd;
+      STEP(packed_forward(s, h->y16 + l * nd, kF16, R, D, D, bo.o.bits, bo.o.scale, bo.o.bias, o),
+           "o");
     }
     float* ar = h->after_rosa + l * nd;
     // CMix (src/model.rs:1018-1078) on ar = x_l + o_l (add_inplace,
@@ -844,7 +915,7 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
     uint16_t* sh = h->shifted16 + l * nd;
     uint16_t* key = h->key16 + l * nf;
     uint16_t* r2 = h->relu2_16 + l * nf;
-    STEP(hipStreamWaitEvent(s, h->ev_o[l], 0), "event wait");
+    if (!live) STEP(hipStreamWaitEvent(s, h->ev_o[l], 0), "event wait");
     PROBED(ULLIS_HIP_PROBE_LN_FORWARD,
            layer_norm_mix_forward(s, h->o_pre + l * nd, R, T, D, b.ln2.w, b.ln2.b, ln2, true,
                                   b.cx_k, sh, nullptr, nullptr, nullptr, nullptr, x_l, ar),
@@ -1026,6 +1097,7 @@ struct StepCall {
   uint32_t* invalid;
   bool from_tokens;
   EmbedArgs emb;
+  const SamHandoff* live = nullptr;
   ullis_hip_heron::StepArgs key() const {
     ullis_hip_heron::StepArgs k{};
     const void* p[] = {x_emb,    labels,   rosa_idx,     g_emb,           row_loss,
@@ -1044,7 +1116,7 @@ int step_call_launches(ullis_hip_heron* h, const StepCall& sc) {
   ullis_hip_ctx* c = h->ctx;
   if (!sc.from_tokens)
     return step_launches(h, sc.x_emb, sc.labels, sc.ignore_id, sc.lr, sc.rosa_idx, sc.g_emb,
-                         sc.row_loss, sc.stats4, sc.qkv_bits, sc.invalid);
+                         sc.row_loss, sc.stats4, sc.qkv_bits, sc.invalid, nullptr, sc.live);
   // the refused-step counter starts the step here: the gather adds the token
   // ids >= vocab, the head the labels >= vocab
   STEP(fill_f32(c->stream, reinterpret_cast<float*>(h->invalid), 1, 0.0f), "clear invalid");
@@ -1052,15 +1124,16 @@ int step_call_launches(ullis_hip_heron* h, const StepCall& sc) {
                         const_cast<float*>(sc.x_emb), h->invalid),
        "embedding gather");
   return step_launches(h, sc.x_emb, sc.labels, sc.ignore_id, sc.lr, sc.rosa_idx, sc.g_emb,
-                       sc.row_loss, sc.stats4, sc.qkv_bits, sc.invalid, &sc.emb);
+                       sc.row_loss, sc.stats4, sc.qkv_bits, sc.invalid, &sc.emb, sc.live);
 }
 
 // Eager launches, or (step graph on) the captured graph of them, captured
 // again whenever the step's arguments change.
 int run_step(ullis_hip_heron* h, const StepCall& sc) {
   ullis_hip_ctx* c = h->ctx;
-  // probed steps run eagerly: the probe times individual launches
-  if (!h->graph_on || h->probe != ULLIS_HIP_PROBE_NONE || t_launch_probe)
+  // probed steps run eagerly: the probe times individual launches; so do
+  // steps with a live automaton, which synchronise with the host every layer
+  if (!h->graph_on || h->probe != ULLIS_HIP_PROBE_NONE || t_launch_probe || sc.live)
     return step_call_launches(h, sc);
   const ullis_hip_heron::StepArgs args = sc.key();
   hipStream_t s = c->stream;
@@ -1143,6 +1216,188 @@ int ullis_hip_heron_step(ullis_hip_heron* h, const float* x_emb, const uint32_t*
   const StepCall sc{x_emb,  labels,   ignore_id, lr,    rosa_idx, g_emb,
                     row_loss, stats4, qkv_bits,  invalid, false,  EmbedArgs{}};
   return run_step(h, sc);
+}
+
+int ullis_hip_heron_step_sam(ullis_hip_heron* h, uint16_t* table, float* table_residual,
+                             size_t vocab, const uint32_t* tokens, float* x_emb,
+                             const uint32_t* labels, uint32_t ignore_id, float lr,
+                             ullis_hip_sam_fn sam, void* sam_user, float* g_emb, float* row_loss,
+                             float* stats4, uint32_t* qkv_bits, uint32_t* invalid) {
+  if (!h) return ULLIS_HIP_ERR_INVALID;
+  ullis_hip_ctx* c = h->ctx;
+  if (!x_emb || !labels || !g_emb || !sam)
+    return c->fail(ULLIS_HIP_ERR_INVALID, "heron step with an automaton needs x_emb, labels, "
+                                          "g_emb and the automaton callback");
+  if (table && (!table_residual || !tokens || vocab == 0 || vocab > (size_t)UINT32_MAX))
+    return c->fail(ULLIS_HIP_ERR_INVALID,
+                   "heron step from tokens needs the table carry, tokens and a u32 vocab");
+  if (!(lr > 0.0f) || !__builtin_isfinite(lr))
+    return c->fail(ULLIS_HIP_ERR_INVALID,
+                   "train step requires a positive learning rate and time >= 2");
+  const long nd = h->rows * h->D;
+  if (!h->sam_idx_dev) {
+    // first live step: pinned staging of one layer's planes and indices, and
+    // device indices of every layer
+    const size_t words = (size_t)cdiv(nd, 32);
+    if (hipHostMalloc(reinterpret_cast<void**>(&h->sam_planes_host), 4 * 3 * words,
+                      hipHostMallocDefault) != hipSuccess ||
+        hipHostMalloc(reinterpret_cast<void**>(&h->sam_idx_host), (size_t)nd,
+                      hipHostMallocDefault) != hipSuccess ||
+        hipMalloc(&h->sam_idx_dev, (size_t)nd * h->L) != hipSuccess ||
+        hipEventCreateWithFlags(&h->ev_sam, hipEventDisableTiming) != hipSuccess) {
+      (void)hipGetLastError();
+      return c->fail(ULLIS_HIP_ERR_NOMEM, "suffix automaton staging allocation failed");
+    }
+  }
+  const SamHandoff live{sam, sam_user};
+  StepCall sc{x_emb, labels, ignore_id, lr, h->sam_idx_dev, g_emb, row_loss, stats4, qkv_bits,
+              invalid, table != nullptr,
+              table ? EmbedArgs{table, table_residual, (long)vocab, tokens} : EmbedArgs{}};
+  sc.live = &live;
+  return run_step(h, sc);
+}
+
+int ullis_hip_heron_decode_init(ullis_hip_heron* h, size_t batch) {
+  if (!h) return ULLIS_HIP_ERR_INVALID;
+  ullis_hip_ctx* c = h->ctx;
+  if (batch == 0 || batch > (size_t)kGemvMaxRows)
+    return c->fail(ULLIS_HIP_ERR_INVALID, "decode batch must be in [1, 8]");
+  auto& d = h->dec;
+  const long B = (long)batch, D = h->D, F = h->F, L = h->L;
+  const long words = cdiv(B * D, 32);
+  if (d.batch != B) {
+    STEP(hipStreamSynchronize(c->stream), "decode sync");
+    if (d.mem) (void)hipFree(d.mem);
+    if (d.planes_host) (void)hipHostFree(d.planes_host);
+    if (d.idx_host) (void)hipHostFree(d.idx_host);
+    d = ullis_hip_heron::Decode{};
+    size_t bytes = 0;
+    auto add = [&](size_t b) { bytes += Carver::bytes_for(b); };
+    add(4ul * L * B * D * 2);
+    for (int i = 0; i < 5; ++i) add(4ul * B * D);
+    for (int i = 0; i < 6; ++i) add(2ul * B * D);
+    add(2ul * B * F);
+    add(2ul * B * D);
+    add(4ul * 3 * words);
+    add(4);
+    if (hipMalloc(&d.mem, bytes) != hipSuccess ||
+        hipHostMalloc(reinterpret_cast<void**>(&d.planes_host), 4ul * 3 * words,
+                      hipHostMallocDefault) != hipSuccess ||
+        hipHostMalloc(reinterpret_cast<void**>(&d.idx_host), (size_t)(B * D),
+                      hipHostMallocDefault) != hipSuccess) {
+      (void)hipGetLastError();
+      return c->fail(ULLIS_HIP_ERR_NOMEM, "decode state allocation failed");
+    }
+    Carver cv(d.mem);
+    d.rosa_prev = cv.take<float>(L * B * D);
+    d.cmix_prev = cv.take<float>(L * B * D);
+    d.x = cv.take<float>(B * D);
+    d.ln = cv.take<float>(B * D);
+    d.q = cv.take<float>(B * D);
+    d.k = cv.take<float>(B * D);
+    d.v = cv.take<float>(B * D);
+    d.q16 = cv.take<uint16_t>(B * D);
+    d.k16 = cv.take<uint16_t>(B * D);
+    d.v16 = cv.take<uint16_t>(B * D);
+    d.y16 = cv.take<uint16_t>(B * D);
+    d.sh16 = cv.take<uint16_t>(B * D);
+    d.hid16 = cv.take<uint16_t>(B * D);
+    d.r2_16 = cv.take<uint16_t>(B * F);
+    d.idx = cv.take<uint8_t>(B * D);
+    d.idx_rm = cv.take<uint8_t>(B * D);
+    d.planes = cv.take<uint32_t>(3 * words);
+    d.invalid = cv.take<uint32_t>(1);
+    d.batch = B;
+  }
+  d.has_prev = false;  // a new sequence per row: no previous token
+  return 0;
+}
+
+int ullis_hip_heron_decode_step(ullis_hip_heron* h, const uint16_t* table, size_t vocab,
+                                const uint32_t* tokens, const uint8_t* rosa_idx,
+                                ullis_hip_sam_fn sam, void* sam_user, float* logits,
+                                uint32_t* next_tokens, uint32_t* invalid) {
+  if (!h) return ULLIS_HIP_ERR_INVALID;
+  ullis_hip_ctx* c = h->ctx;
+  auto& d = h->dec;
+  if (!d.mem) return c->fail(ULLIS_HIP_ERR_INVALID, "decode step before ullis_hip_heron_decode_init");
+  if (!table || !tokens || !logits || vocab == 0 || vocab > (size_t)UINT32_MAX)
+    return c->fail(ULLIS_HIP_ERR_INVALID, "decode step needs the table, tokens and logits");
+  if ((rosa_idx == nullptr) == (sam == nullptr))
+    return c->fail(ULLIS_HIP_ERR_INVALID,
+                   "decode step takes either the automaton's indices or its callback");
+  hipStream_t s = c->stream;
+  const long B = d.batch, D = h->D, F = h->F, V = h->V, L = h->L;
+  const long nd = B * D, words = cdiv(nd, 32);
+  // generate_step (src/model.rs:2717-2753): the embedding rows
+  STEP(fill_f32(s, reinterpret_cast<float*>(d.invalid), 1, 0.0f), "clear invalid");
+  STEP(embedding_gather(s, table, (long)vocab, D, tokens, B, d.x, d.invalid), "decode gather");
+  for (long l = 0; l < L; ++l) {
+    const Block& b = h->blocks[l];
+    // forward_one (src/model.rs:2243-2262): h = ln0(x) at the first block
+    if (b.has_ln0) STEP(layer_norm_forward(s, d.x, B, D, b.ln0.w, b.ln0.b, d.x, nullptr), "ln0");
+    // ROSA forward_one (src/model.rs:1320-1353)
+    STEP(layer_norm_forward(s, d.x, B, D, b.ln3.w, b.ln3.b, d.ln, nullptr), "ln3");
+    STEP(decode_mix(s, d.ln, d.rosa_prev + l * nd, d.has_prev, B, D, b.x_q, d.q16, b.x_k, d.k16,
+                    b.x_v, d.v16),
+         "rosa mixes");
+    {
+      PackedFwdOut oq, ok, ov;
+      oq.y32 = d.q;
+      ok.y32 = d.k;
+      ov.y32 = d.v;
+      STEP(packed_forward(s, d.q16, kF16, B, D, D, b.q.bits, b.q.scale, b.q.bias, oq), "q");
+      STEP(packed_forward(s, d.k16, kF16, B, D, D, b.k.bits, b.k.scale, b.k.bias, ok), "k");
+      STEP(packed_forward(s, d.v16, kF16, B, D, D, b.v.bits, b.v.scale, b.v.bias, ov), "v");
+      // bit_from_activation (src/rosa.rs:372), the bits RosaSam::push takes
+      STEP(sign_pack_bits(s, d.q, nd, d.planes), "q bits");
+      STEP(sign_pack_bits(s, d.k, nd, d.planes + words), "k bits");
+      STEP(sign_pack_bits(s, d.v, nd, d.planes + 2 * words), "v bits");
+    }
+    const uint8_t* idx = rosa_idx ? rosa_idx + l * nd : d.idx;
+    if (sam) {
+      STEP(hipMemcpyAsync(d.planes_host, d.planes, 4ul * 3 * words, hipMemcpyDeviceToHost, s),
+           "planes to host");
+      STEP(hipStreamSynchronize(s), "planes sync");
+      const int cb = sam(sam_user, (size_t)l, d.planes_host, d.idx_host);
+      if (cb != 0)
+        return c->fail(ULLIS_HIP_ERR_INVALID, "suffix automaton callback failed at layer " +
+                                                  std::to_string(l) + " (" + std::to_string(cb) +
+                                                  ")");
+      STEP(hipMemcpyAsync(d.idx, d.idx_host, (size_t)nd, hipMemcpyHostToDevice, s),
+           "indices to device");
+    }
+    // y = (2 idx - 1) e; h += O(y)
+    STEP(rosa_expand(s, idx, b.e, B, 1, D, d.y16, d.idx_rm), "rosa y");
+    {
+      PackedFwdOut o;
+      o.y32 = d.x;
+      o.resid = d.x;
+      STEP(packed_forward(s, d.y16, kF16, B, D, D, b.o.bits, b.o.scale, b.o.bias, o), "o");
+    }
+    // CMix forward_one (src/model.rs:1003-1016): h += value(relu2(key(mix(ln2(h)))))
+    STEP(layer_norm_forward(s, d.x, B, D, b.ln2.w, b.ln2.b, d.ln, nullptr), "ln2");
+    STEP(decode_mix(s, d.ln, d.cmix_prev + l * nd, d.has_prev, B, D, b.cx_k, d.sh16, nullptr,
+                    nullptr, nullptr, nullptr),
+         "cmix mix");
+    {
+      PackedFwdOut o;
+      o.relu2_16 = d.r2_16;
+      STEP(packed_forward(s, d.sh16, kF16, B, D, F, b.key.bits, b.key.scale, nullptr, o), "key");
+    }
+    STEP(fp16_forward(s, d.r2_16, kF16, B, F, D, b.value, d.x, d.x, nullptr), "value");
+  }
+  STEP(layer_norm_forward(s, d.x, B, D, h->ln_out.w, h->ln_out.b, nullptr, d.hid16), "ln_out");
+  {
+    PackedFwdOut o;
+    o.y32 = logits;
+    STEP(packed_forward(s, d.hid16, kF16, B, D, V, h->head.bits, h->head.scale, h->head.bias, o),
+         "head");
+  }
+  if (next_tokens) STEP(argmax_rows(s, logits, B, V, next_tokens), "argmax");
+  if (invalid) STEP(copy_device(s, invalid, d.invalid, sizeof(uint32_t)), "invalid");
+  d.has_prev = true;
+  return 0;
 }
 
 int ullis_hip_heron_causal_loss(ullis_hip_heron* h, const float* g_emb, const uint32_t* labels,

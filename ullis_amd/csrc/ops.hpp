@@ -307,6 +307,15 @@ hipError_t rosa_expand_layers(hipStream_t s, const uint8_t* idx_cm, const uint16
                               const uint16_t* const* e_dev, long layers, long batch, long time,
                               long ch, uint16_t* y16, uint8_t* idx_rm);
 
+// ----------------------------------------------------------- T = 1 decode
+// out_j = f16(x + (prev - x) * mix_j) (xx = -x without a previous token) for
+// the given mixes (null: skipped), then prev = x; x / prev fp32 [rows][d].
+hipError_t decode_mix(hipStream_t s, const float* x, float* prev, bool has_prev, long rows,
+                      long d, const uint16_t* mix0, uint16_t* out0, const uint16_t* mix1,
+                      uint16_t* out1, const uint16_t* mix2, uint16_t* out2);
+// next[r] = argmax_v logits[r][v] (lowest index among equal maxima).
+hipError_t argmax_rows(hipStream_t s, const float* logits, long rows, long vocab, uint32_t* next);
+
 // ---------------------------------------------------------------- embedding
 // x = f32 rows of the f16 table at tokens (ids >= vocab: zero rows, counted
 // into *invalid when non-null).

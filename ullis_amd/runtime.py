@@ -595,6 +595,83 @@ class HeronTrainer:
             row_loss.ptr if row_loss else None, stats.ptr if stats else None,
             qkv_bits.ptr if qkv_bits else None, invalid.ptr if invalid else None), "heron_step")
 
+    def step_sam(self, sam, x_emb: DeviceBuffer, labels: DeviceBuffer, ignore_id: int, lr: float,
+                 g_emb: DeviceBuffer, row_loss: DeviceBuffer | None = None,
+                 stats: DeviceBuffer | None = None, qkv_bits: DeviceBuffer | None = None,
+                 invalid: DeviceBuffer | None = None, table: DeviceBuffer | None = None,
+                 table_res: DeviceBuffer | None = None, tokens: DeviceBuffer | None = None):
+        """ullis_hip_heron_step_sam: the step with the suffix automaton driven live.
+        sam(layer, planes) gets the layer's Q/K/V sign bit-planes (uint32 [3, words])
+        and returns its indices (uint8, channel-major [batch, d, time]). With table /
+        table_res / tokens the step runs from token ids (x_emb is then written)."""
+        s = self.shape
+        words = (s.rows * s.d_model + 31) // 32
+        n_idx = s.rows * s.d_model
+        failure = []
+
+        def cb(user, layer, planes_p, idx_p):
+            try:
+                planes = np.ctypeslib.as_array(planes_p, shape=(3 * words,)).reshape(3, words)
+                idx = np.ascontiguousarray(sam(int(layer), planes.copy()), np.uint8).ravel()
+                if idx.size != n_idx:
+                    raise ValueError(f"automaton returned {idx.size} indices, want {n_idx}")
+                C.memmove(idx_p, idx.ctypes.data, n_idx)
+                return 0
+            except Exception as e:  # reported after the call
+                failure.append(e)
+                return 1
+
+        fn = _lib.SAM_FN(cb)
+        rc = self.rt.lib.ullis_hip_heron_step_sam(
+            self.h, table.ptr if table else None, table_res.ptr if table_res else None,
+            s.vocab if table else 0, tokens.ptr if tokens else None, x_emb.ptr, labels.ptr,
+            ignore_id, lr, fn, None, g_emb.ptr, row_loss.ptr if row_loss else None,
+            stats.ptr if stats else None, qkv_bits.ptr if qkv_bits else None,
+            invalid.ptr if invalid else None)
+        if failure:
+            raise failure[0]
+        self.rt._check(rc, "heron_step_sam")
+
+    def decode_init(self, batch: int):
+        """ullis_hip_heron_decode_init: decode state for `batch` (1..8) new sequences."""
+        self.rt._check(self.rt.lib.ullis_hip_heron_decode_init(self.h, batch), "decode_init")
+        self._decode_batch = batch
+
+    def decode_step(self, table: DeviceBuffer, tokens: DeviceBuffer, logits: DeviceBuffer,
+                    next_tokens: DeviceBuffer | None = None, rosa_idx: DeviceBuffer | None = None,
+                    sam=None, invalid: DeviceBuffer | None = None):
+        """ullis_hip_heron_decode_step: one token per sequence (generate_step). The
+        automaton's indices come from rosa_idx (device u8 [n_layers][batch][d]) or
+        from sam(layer, planes) -> idx u8 [batch, d] (planes: uint32 [3, words])."""
+        s = self.shape
+        batch = self._decode_batch
+        words = (batch * s.d_model + 31) // 32
+        failure = []
+        fn = None
+        if sam is not None:
+            n_idx = batch * s.d_model
+
+            def cb(user, layer, planes_p, idx_p):
+                try:
+                    planes = np.ctypeslib.as_array(planes_p, shape=(3 * words,)).reshape(3, words)
+                    idx = np.ascontiguousarray(sam(int(layer), planes.copy()), np.uint8).ravel()
+                    if idx.size != n_idx:
+                        raise ValueError(f"automaton returned {idx.size} indices, want {n_idx}")
+                    C.memmove(idx_p, idx.ctypes.data, n_idx)
+                    return 0
+                except Exception as e:
+                    failure.append(e)
+                    return 1
+
+            fn = _lib.SAM_FN(cb)
+        rc = self.rt.lib.ullis_hip_heron_decode_step(
+            self.h, table.ptr, s.vocab, tokens.ptr, rosa_idx.ptr if rosa_idx else None, fn, None,
+            logits.ptr, next_tokens.ptr if next_tokens else None,
+            invalid.ptr if invalid else None)
+        if failure:
+            raise failure[0]
+        self.rt._check(rc, "decode_step")
+
     def causal_loss(self, g_emb: DeviceBuffer, labels: DeviceBuffer, ignore_id: int,
                     row_loss: DeviceBuffer | None = None, table_res: DeviceBuffer | None = None
                     ) -> dict:
