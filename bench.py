@@ -379,6 +379,81 @@ def rosa_live(rt, steps: int, warmup: int) -> None:
     tr.close()
 
 
+DECODE_CONFIGS = [
+    ("config 4", dict(d_model=512, n_layers=12, dim_ffn=2048, vocab=8192)),
+    ("config 5", dict(d_model=1024, n_layers=24, dim_ffn=4096, vocab=32768)),
+]
+
+
+def decode_weight_bytes(d: int, layers: int, ffn: int, vocab: int) -> int:
+    """Bytes one T = 1 decode step must read at least: every layer's sign bits
+    (Q/K/V/O d x d, key ffn x d), fp16 value weights (d x ffn), fp16 row scales
+    and biases, mixes, e and LayerNorm parameters, then the head's bits, scale
+    and bias. Activations (a few KiB) are left out."""
+    per_layer = (4 * d * d + ffn * d) // 8 + 2 * ffn * d + 2 * (4 * 2 * d + ffn) + 2 * 8 * d
+    return layers * per_layer + vocab * d // 8 + 2 * 2 * vocab + 2 * 2 * d
+
+
+def decode_step_bench(rt, steps: int, warmup: int) -> None:
+    """One JSON line per (config, batch): the T = 1 decode step
+    (ullis_hip_heron_decode_step) with the automaton's indices given, timed by
+    events on the library's stream over `steps` tokens, and the same with the
+    indices handed over per layer through the host callback. The floor is the
+    step's weight bytes at the HBM peak."""
+    import ctypes as C
+    from ullis_amd.runtime import HeronShape, HeronTrainer
+    from ullis_amd.synth import heron_arena
+
+    lib, ctx = rt.lib, rt.ctx
+    for name, dims in DECODE_CONFIGS:
+        shape = HeronShape(**dims, batch=1, time=2)
+        tr = HeronTrainer(rt, shape)
+        tr.upload_arena(heron_arena(tr.layout, tr.arena_bytes, shape.dims(), seed=7))
+        d, L, V = dims["d_model"], dims["n_layers"], dims["vocab"]
+        rng = np.random.default_rng(7)
+        table = rt.put(rng.standard_normal(V * d).astype(np.float16).view(np.uint16))
+        wbytes = decode_weight_bytes(d, L, dims["dim_ffn"], V)
+        for batch in (1, 8):
+            tokens = rt.put(rng.integers(0, V, batch).astype(np.uint32))
+            idx_h = (rng.random(L * batch * d) < 0.5).astype(np.uint8)
+            idx = rt.put(idx_h)
+            idx_l = idx_h.reshape(L, batch, d)
+            logits = rt.zeros(np.float32, batch * V)
+            nxt = rt.zeros(np.uint32, batch)
+            tr.decode_init(batch)
+
+            def run(n, live):
+                rt.sync()
+                rt._check(lib.ullis_hip_event_record(ctx, 0), "event")
+                t0 = time.perf_counter()
+                for _ in range(n):
+                    if live:
+                        tr.decode_step(table, tokens, logits, next_tokens=nxt,
+                                       sam=lambda layer, planes: idx_l[layer])
+                    else:
+                        tr.decode_step(table, tokens, logits, next_tokens=nxt, rosa_idx=idx)
+                rt._check(lib.ullis_hip_event_record(ctx, 1), "event")
+                rt.sync()
+                wall = time.perf_counter() - t0
+                ms = C.c_float()
+                rt._check(lib.ullis_hip_event_elapsed_ms(ctx, 0, 1, C.byref(ms)), "elapsed")
+                return ms.value * 1e3 / n, wall * 1e6 / n
+
+            run(warmup, False)
+            us, wall_us = run(steps, False)
+            run(warmup, True)
+            live_us, _ = run(steps, True)
+            floor_us = wbytes / (HBM_PEAK_GBS * 1e9) * 1e6
+            print(json.dumps({
+                "decode_step": f"{name}: D{d} L{L} F{dims['dim_ffn']} V{V}", "batch": batch,
+                "us_per_step": round(us, 2), "wall_us_per_step": round(wall_us, 2),
+                "tokens_per_s": round(batch / (us * 1e-6), 1),
+                "weight_bytes": wbytes, "hbm_floor_us": round(floor_us, 2),
+                "frac_of_floor": round(floor_us / us, 4),
+                "live_us_per_step": round(live_us, 2), "steps": steps}), flush=True)
+        tr.close()
+
+
 def copy_calibration(rt, mib: int) -> None:
     """One copy kernel (ullis_hip_copy) that reads `mib` MiB and writes `mib` MiB.
 
@@ -421,6 +496,9 @@ def main() -> int:
     ap.add_argument("--rosa-live", action="store_true",
                     help="instead of the bench line, time the step with the suffix automaton "
                          "driven live, layer by layer, against indices given up front")
+    ap.add_argument("--decode-step", action="store_true",
+                    help="instead of the bench line, time the T = 1 decode step at configs 4 "
+                         "and 5, batch 1 and 8, against its weight-streaming floor")
     ap.add_argument("--graph", type=int, default=0,
                     help="1: replay each step's launches from a captured HIP graph")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -436,7 +514,7 @@ def main() -> int:
               "run with --gpus 1", file=sys.stderr)
         return 2
     plain = (args.decode_gemv == 0 and not args.stress and args.ln_isolated == 0 and
-             not args.rosa_live)
+             not args.rosa_live and not args.decode_step)
     # the CPU baseline's child processes start before this process touches the GPU
     baseline = (cpu_baseline(args.cpu_rows, max(1, args.cpu_runs))
                 if plain and args.cpu_rows > 0 else None)
@@ -458,6 +536,9 @@ def main() -> int:
         return 0
     if args.rosa_live:
         rosa_live(rt, args.steps, args.warmup)
+        return 0
+    if args.decode_step:
+        decode_step_bench(rt, args.steps, args.warmup)
         return 0
     trainer = HeronTrainer(rt, shape)
     arena = heron_arena(trainer.layout, trainer.arena_bytes, shape.dims(), seed=7)

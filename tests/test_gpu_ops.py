@@ -478,7 +478,9 @@ GEMV_REL = 1e-5  # same fp16-rounded inputs, fp32 sums in another order
 
 @pytest.mark.parametrize("rows", [1, 3, 8])
 @pytest.mark.parametrize("in_f,out_f,bias", [(512, 2048, True), (1024, 32768, True),
-                                             (96, 1000, False), (4096, 64, True)])
+                                             (96, 1000, False), (4096, 64, True),
+                                             (128, 300, True), (256, 64, False),
+                                             (384, 640, True), (640, 96, True)])
 def test_packed_few_rows_matches_oracle(rt, rows, in_f, out_f, bias):
     # T = 1 decode shapes (batch <= 8): the few-row path of binary_linear
     rng = np.random.default_rng(rows * 7 + in_f + out_f)

@@ -71,6 +71,16 @@ struct Carver {
   static size_t bytes_for(size_t bytes) { return (bytes + 255) / 256 * 256; }
 };
 
+// Counts the bytes a sequence of Carver::take calls needs (returns null pointers).
+struct CarveSizer {
+  size_t used = 0;
+  template <class T>
+  T* take(size_t count) {
+    used += Carver::bytes_for(count * sizeof(T));
+    return nullptr;
+  }
+};
+
 // Split-K factor for a weight-gradient GEMM [out, in] over `rows`: enough
 // 64x64-tile blocks for two per CU (512), at least 256 rows per split, at most 8.
 inline int dw_splits(long out, long in, long rows, long target_blocks = 512) {

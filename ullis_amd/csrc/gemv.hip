@@ -83,9 +83,11 @@ __device__ __forceinline__ void stage_x_rows(uint16_t* xs, const void* x, int x_
 // through a 16-entry table in LDS, as the streamed GEMM does), and x^T is the
 // B operand (rows m of x as columns; columns >= M are zero), so one
 // instruction covers 32 weight rows x 16 inputs for every row of x at once.
-// The four waves split the inputs in quarters (short dependent chains, four
-// times the loads in flight) and their partial tiles are summed in LDS in
-// wave order. LDS: the sign table (128 B), x [M][in] fp16, 4 partial tiles.
+// The four waves split the inputs into four ranges of whole 4-word
+// (128-input) groups, the unit of one 16-byte sign load (short dependent
+// chains, four times the loads in flight; with fewer than four groups some
+// waves own none), and their partial tiles are summed in LDS in wave order.
+// LDS: the sign table (128 B), x [M][in] fp16, 4 partial tiles.
 __global__ __launch_bounds__(kGemvThreads) void gemv_bits_kernel(
     const void* x, int x_dtype, int rows_m, int in, int out, const uint32_t* bits,
     const uint16_t* scale, const uint16_t* bias, GemvOut o) {
@@ -100,15 +102,15 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_bits_kernel(
     lut[threadIdx.x] = ((nb & 1u) << 15) | ((nb & 2u) << 30);
   }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int words = in >> 5, wq = words >> 2;  // words % 4 == 0
+  const int groups = in >> 7;  // in % 128 == 0
+  const int wbeg = 4 * (wave * groups / 4), wend = 4 * ((wave + 1) * groups / 4);
   const int m = lane & 31;         // B column: the row of x this lane feeds
   const bool mok = m < rows_m;
   const int kh = 8 * (lane >> 5);  // this lane's 8 inputs within a 16-input step
   typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
   const long tile = blockIdx.x;
   const long row = tile * 32 + (lane & 31);
-  const uint32_t* br = bits + (row < out ? row : 0) * words;
-  const int wend = (wave + 1) * wq;
+  const uint32_t* br = bits + (row < out ? row : 0) * (long)(in >> 5);
   uint4 bw[4];
   auto load_words = [&](int w0) {
 #pragma unroll
@@ -119,14 +121,14 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_bits_kernel(
     }
   };
   // the first sign words are on their way while x is staged
-  load_words(wave * wq);
+  load_words(wbeg);
   stage_x_rows(xs, x, x_dtype, in, rows_m);
   __syncthreads();
   floatx16 acc;
 #pragma unroll
   for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-  for (int w0 = wave * wq; w0 < wend; w0 += 16) {
-    if (w0 != wave * wq) load_words(w0);
+  for (int w0 = wbeg; w0 < wend; w0 += 16) {
+    if (w0 != wbeg) load_words(w0);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       if (w0 + 4 * u >= wend) break;

@@ -163,7 +163,7 @@ struct ullis_hip_heron {
     float *rosa_prev = nullptr, *cmix_prev = nullptr;  // [L][batch][D]
     float *x = nullptr, *ln = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;  // [batch][D]
     uint16_t *q16 = nullptr, *k16 = nullptr, *v16 = nullptr, *y16 = nullptr, *sh16 = nullptr;
-    uint16_t *hid16 = nullptr, *r2_16 = nullptr;  // [batch][D], [batch][F]
+    uint16_t *hid16 = nullptr, *key16 = nullptr, *r2_16 = nullptr;  // [batch][D], [batch][F] x 2
     uint8_t *idx = nullptr, *idx_rm = nullptr;    // [batch][D]
     uint32_t* planes = nullptr;                   // [3][words]
     uint32_t* invalid = nullptr;
@@ -540,93 +540,61 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
   const long pt_mix = (long)h->nb_mix * D;
   const size_t head_ws = head_ce_workspace_bytes(R, D, V);
 
-  size_t bytes = 0;
-  auto add = [&](size_t b) { bytes += Carver::bytes_for(b); };
-  add(4ul * nd * (L + 1));   // resid
-  add(4ul * nd * L);         // after_rosa
-  add(4ul * nd * L);         // o_pre
-  for (int i = 0; i < 4; ++i) add(2ul * nd);  // ln16 q16 k16 v16
-  add(2ul * nd * L);         // y16
-  add(2ul * nd * L);         // ln2_16
-  add(2ul * nd * L);         // shifted16
-  add(1ul * nd * L);         // idx_rm
-  add(2ul * nf * L);         // key16
-  add(2ul * nf * L);         // relu2_16
-  add(2ul * nf);             // gk16
-  add(2ul * nd * (L + 1));   // gx16_b
-  add(4ul * nd);             // g_side
-  add(2ul * nd);             // ln3_16
-  add(4ul * nd * 3);         // g_x g_a g_b
-  add(4ul * gp_value * L);
-  add(4ul * gp_key * L);
-  add(4ul * gp_o * L);
-  add(4ul * gp_head);
-  add(4ul * pt_mix * L);
-  for (int i = 0; i < 2; ++i) add(4ul * pt_col * L);  // pt_ob pt_e
-  add(4ul * pt_ln * L);      // pt_ln2
-  add(4ul * pt_ln);          // pt_lnout
-  add(4ul * 2 * nb_ln0 * D); // pt_ln0
-  add(4ul * (L + 2));        // slots
-  add(4ul * 4);              // stats
-  add(4ul * R);              // row_loss
-  add(4ul * words * 3 * L);  // qkv bit-planes
-  add(head_ws);
-  add(4);                    // invalid
-  add(4ul * F * L);          // flips_key
-  add(4ul * D * L);          // flips_o
-  add(4ul * V);              // flips_head
-  add(4ul * V);              // step_head
-  add(4ul * V);              // gscale_head
-  add(diag_workspace_bytes(V));
-  if (hipMalloc(&h->act, bytes) != hipSuccess) {
+  // one carving sequence, run once to size the allocation and once to place the buffers
+  auto carve = [&](auto& cv) {
+    h->resid = cv.template take<float>(nd * (L + 1));
+    h->after_rosa = cv.template take<float>(nd * L);
+    h->o_pre = cv.template take<float>(nd * L);
+    h->ln16 = cv.template take<uint16_t>(nd);
+    h->q16 = cv.template take<uint16_t>(nd);
+    h->k16 = cv.template take<uint16_t>(nd);
+    h->v16 = cv.template take<uint16_t>(nd);
+    h->y16 = cv.template take<uint16_t>(nd * L);
+    h->ln2_16 = cv.template take<uint16_t>(nd * L);
+    h->shifted16 = cv.template take<uint16_t>(nd * L);
+    h->idx_rm = cv.template take<uint8_t>(nd * L);
+    h->key16 = cv.template take<uint16_t>(nf * L);
+    h->relu2_16 = cv.template take<uint16_t>(nf * L);
+    h->gk16 = cv.template take<uint16_t>(nf);
+    h->gx16_b = cv.template take<uint16_t>(nd * (L + 1));
+    h->g_side = cv.template take<float>(nd);
+    h->ln3_16 = cv.template take<uint16_t>(nd);
+    h->g_x = cv.template take<float>(nd);
+    h->g_a = cv.template take<float>(nd);
+    h->g_b = cv.template take<float>(nd);
+    h->gp_value = cv.template take<float>(gp_value * L);
+    h->gp_key = cv.template take<float>(gp_key * L);
+    h->gp_o = cv.template take<float>(gp_o * L);
+    h->gp_head = cv.template take<float>(gp_head);
+    h->pt_mix = cv.template take<float>(pt_mix * L);
+    h->pt_ob = cv.template take<float>(pt_col * L);
+    h->pt_e = cv.template take<float>(pt_col * L);
+    h->pt_ln2 = cv.template take<float>(pt_ln * L);
+    h->pt_lnout = cv.template take<float>(pt_ln);
+    h->pt_ln0 = cv.template take<float>(2 * nb_ln0 * D);
+    h->slots = cv.template take<float>(L + 2);
+    h->stats = cv.template take<float>(4);
+    h->row_loss = cv.template take<float>(R);
+    h->qkv = cv.template take<uint32_t>(words * 3 * L);
+    h->head_ws = cv.template take<char>(head_ws);
+    h->invalid = cv.template take<uint32_t>(1);
+    h->flips_key = cv.template take<uint32_t>(F * L);
+    h->flips_o = cv.template take<uint32_t>(D * L);
+    h->flips_head = cv.template take<uint32_t>(V);
+    h->step_head = cv.template take<float>(V);
+    h->gscale_head = cv.template take<float>(V);
+    h->diag_ws = cv.template take<char>(diag_workspace_bytes(V));
+  };
+  CarveSizer sizer;
+  carve(sizer);
+  if (hipMalloc(&h->act, sizer.used) != hipSuccess) {
     (void)hipFree(h->arena);
     delete h;
     return c->fail(ULLIS_HIP_ERR_NOMEM, "heron activation allocation of " +
-                                            std::to_string(bytes) + " bytes failed");
+                                            std::to_string(sizer.used) + " bytes failed");
   }
   Carver cv(h->act);
-  h->resid = cv.take<float>(nd * (L + 1));
-  h->after_rosa = cv.take<float>(nd * L);
-  h->o_pre = cv.take<float>(nd * L);
-  h->ln16 = cv.take<uint16_t>(nd);
-  h->q16 = cv.take<uint16_t>(nd);
-  h->k16 = cv.take<uint16_t>(nd);
-  h->v16 = cv.take<uint16_t>(nd);
-  h->y16 = cv.take<uint16_t>(nd * L);
-  h->ln2_16 = cv.take<uint16_t>(nd * L);
-  h->shifted16 = cv.take<uint16_t>(nd * L);
-  h->idx_rm = cv.take<uint8_t>(nd * L);
-  h->key16 = cv.take<uint16_t>(nf * L);
-  h->relu2_16 = cv.take<uint16_t>(nf * L);
-  h->gk16 = cv.take<uint16_t>(nf);
-  h->gx16_b = cv.take<uint16_t>(nd * (L + 1));
-  h->g_side = cv.take<float>(nd);
-  h->ln3_16 = cv.take<uint16_t>(nd);
-  h->g_x = cv.take<float>(nd);
-  h->g_a = cv.take<float>(nd);
-  h->g_b = cv.take<float>(nd);
-  h->gp_value = cv.take<float>(gp_value * L);
-  h->gp_key = cv.take<float>(gp_key * L);
-  h->gp_o = cv.take<float>(gp_o * L);
-  h->gp_head = cv.take<float>(gp_head);
-  h->pt_mix = cv.take<float>(pt_mix * L);
-  h->pt_ob = cv.take<float>(pt_col * L);
-  h->pt_e = cv.take<float>(pt_col * L);
-  h->pt_ln2 = cv.take<float>(pt_ln * L);
-  h->pt_lnout = cv.take<float>(pt_ln);
-  h->pt_ln0 = cv.take<float>(2 * nb_ln0 * D);
-  h->slots = cv.take<float>(L + 2);
-  h->stats = cv.take<float>(4);
-  h->row_loss = cv.take<float>(R);
-  h->qkv = cv.take<uint32_t>(words * 3 * L);
-  h->head_ws = cv.take<char>(head_ws);
-  h->invalid = cv.take<uint32_t>(1);
-  h->flips_key = cv.take<uint32_t>(F * L);
-  h->flips_o = cv.take<uint32_t>(D * L);
-  h->flips_head = cv.take<uint32_t>(V);
-  h->step_head = cv.take<float>(V);
-  h->gscale_head = cv.take<float>(V);
-  h->diag_ws = cv.take<char>(diag_workspace_bytes(V));
+  carve(cv);
   if (int rc = build_update_jobs(h)) {
     ullis_hip_heron_destroy(h);
     return rc;
@@ -1271,16 +1239,31 @@ int ullis_hip_heron_decode_init(ullis_hip_heron* h, size_t batch) {
     if (d.planes_host) (void)hipHostFree(d.planes_host);
     if (d.idx_host) (void)hipHostFree(d.idx_host);
     d = ullis_hip_heron::Decode{};
-    size_t bytes = 0;
-    auto add = [&](size_t b) { bytes += Carver::bytes_for(b); };
-    add(4ul * L * B * D * 2);
-    for (int i = 0; i < 5; ++i) add(4ul * B * D);
-    for (int i = 0; i < 6; ++i) add(2ul * B * D);
-    add(2ul * B * F);
-    add(2ul * B * D);
-    add(4ul * 3 * words);
-    add(4);
-    if (hipMalloc(&d.mem, bytes) != hipSuccess ||
+    // one carving sequence, run once to size the allocation and once to place the buffers
+    auto carve = [&](auto& cv) {
+      d.rosa_prev = cv.template take<float>(L * B * D);
+      d.cmix_prev = cv.template take<float>(L * B * D);
+      d.x = cv.template take<float>(B * D);
+      d.ln = cv.template take<float>(B * D);
+      d.q = cv.template take<float>(B * D);
+      d.k = cv.template take<float>(B * D);
+      d.v = cv.template take<float>(B * D);
+      d.q16 = cv.template take<uint16_t>(B * D);
+      d.k16 = cv.template take<uint16_t>(B * D);
+      d.v16 = cv.template take<uint16_t>(B * D);
+      d.y16 = cv.template take<uint16_t>(B * D);
+      d.sh16 = cv.template take<uint16_t>(B * D);
+      d.hid16 = cv.template take<uint16_t>(B * D);
+      d.key16 = cv.template take<uint16_t>(B * F);
+      d.r2_16 = cv.template take<uint16_t>(B * F);
+      d.idx = cv.template take<uint8_t>(B * D);
+      d.idx_rm = cv.template take<uint8_t>(B * D);
+      d.planes = cv.template take<uint32_t>(3 * words);
+      d.invalid = cv.template take<uint32_t>(1);
+    };
+    CarveSizer sizer;
+    carve(sizer);
+    if (hipMalloc(&d.mem, sizer.used) != hipSuccess ||
         hipHostMalloc(reinterpret_cast<void**>(&d.planes_host), 4ul * 3 * words,
                       hipHostMallocDefault) != hipSuccess ||
         hipHostMalloc(reinterpret_cast<void**>(&d.idx_host), (size_t)(B * D),
@@ -1289,24 +1272,7 @@ int ullis_hip_heron_decode_init(ullis_hip_heron* h, size_t batch) {
       return c->fail(ULLIS_HIP_ERR_NOMEM, "decode state allocation failed");
     }
     Carver cv(d.mem);
-    d.rosa_prev = cv.take<float>(L * B * D);
-    d.cmix_prev = cv.take<float>(L * B * D);
-    d.x = cv.take<float>(B * D);
-    d.ln = cv.take<float>(B * D);
-    d.q = cv.take<float>(B * D);
-    d.k = cv.take<float>(B * D);
-    d.v = cv.take<float>(B * D);
-    d.q16 = cv.take<uint16_t>(B * D);
-    d.k16 = cv.take<uint16_t>(B * D);
-    d.v16 = cv.take<uint16_t>(B * D);
-    d.y16 = cv.take<uint16_t>(B * D);
-    d.sh16 = cv.take<uint16_t>(B * D);
-    d.hid16 = cv.take<uint16_t>(B * D);
-    d.r2_16 = cv.take<uint16_t>(B * F);
-    d.idx = cv.take<uint8_t>(B * D);
-    d.idx_rm = cv.take<uint8_t>(B * D);
-    d.planes = cv.take<uint32_t>(3 * words);
-    d.invalid = cv.take<uint32_t>(1);
+    carve(cv);
     d.batch = B;
   }
   d.has_prev = false;  // a new sequence per row: no previous token
@@ -1335,7 +1301,10 @@ int ullis_hip_heron_decode_step(ullis_hip_heron* h, const uint16_t* table, size_
   for (long l = 0; l < L; ++l) {
     const Block& b = h->blocks[l];
     // forward_one (src/model.rs:2243-2262): h = ln0(x) at the first block
-    if (b.has_ln0) STEP(layer_norm_forward(s, d.x, B, D, b.ln0.w, b.ln0.b, d.x, nullptr), "ln0");
+    if (b.has_ln0) {
+      STEP(layer_norm_forward(s, d.x, B, D, b.ln0.w, b.ln0.b, d.v, nullptr), "ln0");
+      STEP(copy_device(s, d.x, d.v, 4ul * nd), "ln0 copy");
+    }
     // ROSA forward_one (src/model.rs:1320-1353)
     STEP(layer_norm_forward(s, d.x, B, D, b.ln3.w, b.ln3.b, d.ln, nullptr), "ln3");
     STEP(decode_mix(s, d.ln, d.rosa_prev + l * nd, d.has_prev, B, D, b.x_q, d.q16, b.x_k, d.k16,
@@ -1382,6 +1351,7 @@ int ullis_hip_heron_decode_step(ullis_hip_heron* h, const uint16_t* table, size_
          "cmix mix");
     {
       PackedFwdOut o;
+      o.y16 = d.key16;  // the products write relu2 beside the key itself
       o.relu2_16 = d.r2_16;
       STEP(packed_forward(s, d.sh16, kF16, B, D, F, b.key.bits, b.key.scale, nullptr, o), "key");
     }

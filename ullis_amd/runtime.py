@@ -647,7 +647,7 @@ class HeronTrainer:
         batch = self._decode_batch
         words = (batch * s.d_model + 31) // 32
         failure = []
-        fn = None
+        fn = _lib.SAM_FN()  # NULL unless a callback is given
         if sam is not None:
             n_idx = batch * s.d_model
 
