@@ -394,7 +394,7 @@ def decode_weight_bytes(d: int, layers: int, ffn: int, vocab: int) -> int:
     return layers * per_layer + vocab * d // 8 + 2 * 2 * vocab + 2 * 2 * d
 
 
-def decode_step_bench(rt, steps: int, warmup: int) -> None:
+def decode_step_bench(rt, steps: int, warmup: int, graph: bool = True) -> None:
     """One JSON line per (config, batch): the T = 1 decode step
     (ullis_hip_heron_decode_step) with the automaton's indices given, timed by
     events on the library's stream over `steps` tokens, and the same with the
@@ -420,7 +420,7 @@ def decode_step_bench(rt, steps: int, warmup: int) -> None:
             idx_l = idx_h.reshape(L, batch, d)
             logits = rt.zeros(np.float32, batch * V)
             nxt = rt.zeros(np.uint32, batch)
-            tr.decode_init(batch)
+            tr.decode_init(batch, graph=graph)
 
             def run(n, live):
                 rt.sync()
@@ -450,7 +450,8 @@ def decode_step_bench(rt, steps: int, warmup: int) -> None:
                 "tokens_per_s": round(batch / (us * 1e-6), 1),
                 "weight_bytes": wbytes, "hbm_floor_us": round(floor_us, 2),
                 "frac_of_floor": round(floor_us / us, 4),
-                "live_us_per_step": round(live_us, 2), "steps": steps}), flush=True)
+                "live_us_per_step": round(live_us, 2), "graph": graph, "steps": steps}),
+                  flush=True)
         tr.close()
 
 
@@ -499,8 +500,9 @@ def main() -> int:
     ap.add_argument("--decode-step", action="store_true",
                     help="instead of the bench line, time the T = 1 decode step at configs 4 "
                          "and 5, batch 1 and 8, against its weight-streaming floor")
-    ap.add_argument("--graph", type=int, default=0,
-                    help="1: replay each step's launches from a captured HIP graph")
+    ap.add_argument("--graph", type=int, default=None,
+                    help="1: replay each step's launches from a captured HIP graph (default 0; "
+                         "with --decode-step, default 1)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after the timed region, run one plain device copy kernel of this many "
                          "MiB (read + write) so HBM counters can be scaled against known bytes")
@@ -538,12 +540,13 @@ def main() -> int:
         rosa_live(rt, args.steps, args.warmup)
         return 0
     if args.decode_step:
-        decode_step_bench(rt, args.steps, args.warmup)
+        decode_step_bench(rt, args.steps, args.warmup,
+                          graph=True if args.graph is None else bool(args.graph))
         return 0
     trainer = HeronTrainer(rt, shape)
     arena = heron_arena(trainer.layout, trainer.arena_bytes, shape.dims(), seed=7)
     trainer.upload_arena(arena)
-    trainer.set_graph(bool(args.graph))
+    trainer.set_graph(bool(args.graph or 0))
     x, labels, idx = step_inputs(shape.rows, c["d_model"], c["vocab"], c["n_layers"], c["batch"],
                                  c["time"], seed=7)
     dl, di = rt.put(labels), rt.put(idx)

@@ -354,7 +354,8 @@ int ullis_hip_heron_step_sam(ullis_hip_heron* h, uint16_t* table, float* table_r
  * [batch][d] (sam / sam_user as for ullis_hip_heron_step_sam); exactly one
  * of the two. The reference's context_len limit is the caller's to keep.
  */
-int ullis_hip_heron_decode_init(ullis_hip_heron* h, size_t batch);
+#define ULLIS_HIP_DECODE_EAGER 1
+int ullis_hip_heron_decode_init(ullis_hip_heron* h, size_t batch, int flags);
 int ullis_hip_heron_decode_step(ullis_hip_heron* h, const uint16_t* table, size_t vocab,
                                 const uint32_t* tokens, const uint8_t* rosa_idx,
                                 ullis_hip_sam_fn sam, void* sam_user, float* logits,

@@ -98,6 +98,9 @@ def test_decode_matches_oracle(rt, case):
 
 
 def test_decode_given_indices_equal_the_callback_path_and_init_restarts(rt):
+    """The graph replay of the step with given indices (tokens 0 and 2 replay
+    the parity-0 graph), the eager step, and the step whose indices come from
+    the host callback give identical logits; decode_init restarts."""
     d, layers, ffn, vocab, batch = 128, 3, 256, 512, 4
     trainer, _, table = make(rt, d, layers, ffn, vocab, batch, seed=3)
     rng = np.random.default_rng(9)
@@ -108,8 +111,8 @@ def test_decode_given_indices_equal_the_callback_path_and_init_restarts(rt):
     didx = rt.zeros(np.uint8, layers * batch * d)
     logits = rt.zeros(np.float32, batch * vocab)
 
-    def run(via_callback):
-        trainer.decode_init(batch)
+    def run(via_callback, graph=True):
+        trainer.decode_init(batch, graph=graph)
         out = []
         for t in range(3):
             dtok.upload(tokens[t])
@@ -124,8 +127,10 @@ def test_decode_given_indices_equal_the_callback_path_and_init_restarts(rt):
 
     a = run(True)
     b = run(False)  # decode_init restarts the sequences: no previous token at t = 0
+    c = run(False, graph=False)
     for t in range(3):
         np.testing.assert_array_equal(a[t], b[t], err_msg=f"token {t}")
+        np.testing.assert_array_equal(a[t], c[t], err_msg=f"token {t}, eager")
     assert not np.array_equal(a[0], a[1])
 
 

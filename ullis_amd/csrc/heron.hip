@@ -158,17 +158,33 @@ struct ullis_hip_heron {
   // T = 1 decode state (ullis_hip_heron_decode_*), one allocation
   struct Decode {
     long batch = 0;
-    bool has_prev = false;
+    int parity = 0;  // which half of the previous-token buffers this token reads
+    bool eager = false;  // no graph replay (ULLIS_HIP_DECODE_EAGER)
     void* mem = nullptr;
-    float *rosa_prev = nullptr, *cmix_prev = nullptr;  // [L][batch][D]
-    float *x = nullptr, *ln = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;  // [batch][D]
+    // the previous token's LN3 / LN2 outputs per layer, [2][L][batch][D]:
+    // a token reads half `parity` and writes the other
+    float *rosa_prev = nullptr, *cmix_prev = nullptr;
+    float *x = nullptr, *x2 = nullptr, *ln = nullptr;                            // [batch][D]
+    float *q = nullptr, *k = nullptr, *v = nullptr;                              // [batch][D]
     uint16_t *q16 = nullptr, *k16 = nullptr, *v16 = nullptr, *y16 = nullptr, *sh16 = nullptr;
     uint16_t *hid16 = nullptr, *key16 = nullptr, *r2_16 = nullptr;  // [batch][D], [batch][F] x 2
     uint8_t *idx = nullptr, *idx_rm = nullptr;    // [batch][D]
     uint32_t* planes = nullptr;                   // [3][words]
-    uint32_t* invalid = nullptr;
     uint32_t* planes_host = nullptr;              // pinned
     uint8_t* idx_host = nullptr;                  // pinned
+    // graphs of the step with the automaton's indices given, one per parity,
+    // for the pointers in `key`
+    struct Key {
+      const void* p[6];
+      long vocab;
+      bool operator==(const Key& o) const {
+        for (int i = 0; i < 6; ++i)
+          if (p[i] != o.p[i]) return false;
+        return vocab == o.vocab;
+      }
+    };
+    hipGraphExec_t graph[2] = {nullptr, nullptr};
+    Key graph_key[2] = {};
   } dec;
   int splits_o = 1, splits_key = 1, splits_value = 1;
   // kernel probe: events around every launch of one launch class
@@ -662,6 +678,8 @@ void ullis_hip_heron_destroy(ullis_hip_heron* h) {
   if (h->sam_idx_host) (void)hipHostFree(h->sam_idx_host);
   if (h->sam_idx_dev) (void)hipFree(h->sam_idx_dev);
   if (h->ev_sam) (void)hipEventDestroy(h->ev_sam);
+  for (auto& g : h->dec.graph)
+    if (g) (void)hipGraphExecDestroy(g);
   if (h->dec.mem) (void)hipFree(h->dec.mem);
   if (h->dec.planes_host) (void)hipHostFree(h->dec.planes_host);
   if (h->dec.idx_host) (void)hipHostFree(h->dec.idx_host);
@@ -1225,9 +1243,11 @@ int ullis_hip_heron_step_sam(ullis_hip_heron* h, uint16_t* table, float* table_r
   return run_step(h, sc);
 }
 
-int ullis_hip_heron_decode_init(ullis_hip_heron* h, size_t batch) {
+int ullis_hip_heron_decode_init(ullis_hip_heron* h, size_t batch, int flags) {
   if (!h) return ULLIS_HIP_ERR_INVALID;
   ullis_hip_ctx* c = h->ctx;
+  if ((flags & ~ULLIS_HIP_DECODE_EAGER) != 0)
+    return c->fail(ULLIS_HIP_ERR_INVALID, "unknown decode flags");
   if (batch == 0 || batch > (size_t)kGemvMaxRows)
     return c->fail(ULLIS_HIP_ERR_INVALID, "decode batch must be in [1, 8]");
   auto& d = h->dec;
@@ -1235,15 +1255,18 @@ int ullis_hip_heron_decode_init(ullis_hip_heron* h, size_t batch) {
   const long words = cdiv(B * D, 32);
   if (d.batch != B) {
     STEP(hipStreamSynchronize(c->stream), "decode sync");
+    for (auto& g : d.graph)
+      if (g) (void)hipGraphExecDestroy(g);
     if (d.mem) (void)hipFree(d.mem);
     if (d.planes_host) (void)hipHostFree(d.planes_host);
     if (d.idx_host) (void)hipHostFree(d.idx_host);
     d = ullis_hip_heron::Decode{};
     // one carving sequence, run once to size the allocation and once to place the buffers
     auto carve = [&](auto& cv) {
-      d.rosa_prev = cv.template take<float>(L * B * D);
-      d.cmix_prev = cv.template take<float>(L * B * D);
+      d.rosa_prev = cv.template take<float>(2 * L * B * D);
+      d.cmix_prev = cv.template take<float>(2 * L * B * D);
       d.x = cv.template take<float>(B * D);
+      d.x2 = cv.template take<float>(B * D);
       d.ln = cv.template take<float>(B * D);
       d.q = cv.template take<float>(B * D);
       d.k = cv.template take<float>(B * D);
@@ -1259,7 +1282,6 @@ int ullis_hip_heron_decode_init(ullis_hip_heron* h, size_t batch) {
       d.idx = cv.template take<uint8_t>(B * D);
       d.idx_rm = cv.template take<uint8_t>(B * D);
       d.planes = cv.template take<uint32_t>(3 * words);
-      d.invalid = cv.template take<uint32_t>(1);
     };
     CarveSizer sizer;
     carve(sizer);
@@ -1275,9 +1297,163 @@ int ullis_hip_heron_decode_init(ullis_hip_heron* h, size_t batch) {
     carve(cv);
     d.batch = B;
   }
-  d.has_prev = false;  // a new sequence per row: no previous token
+  // new sequences: no previous token, i.e. previous LayerNorm outputs of 0
+  // (time_shift_one then gives -x)
+  STEP(fill_f32(c->stream, d.rosa_prev, L * B * D, 0.0f), "decode state clear");
+  STEP(fill_f32(c->stream, d.cmix_prev, L * B * D, 0.0f), "decode state clear");
+  d.parity = 0;
+  d.eager = (flags & ULLIS_HIP_DECODE_EAGER) != 0;
   return 0;
 }
+
+}  // extern "C"
+
+namespace {
+
+struct DecodeCall {
+  const uint16_t* table;
+  long vocab;
+  const uint32_t* tokens;
+  const uint8_t* rosa_idx;
+  ullis_hip_sam_fn sam;
+  void* sam_user;
+  float* logits;
+  uint32_t* next;
+  uint32_t* invalid;
+  ullis_hip_heron::Decode::Key key() const {
+    return {{table, tokens, rosa_idx, logits, next, invalid}, vocab};
+  }
+};
+
+// The launches of one decode token, reading the previous-token buffers of
+// `parity`: generate_step (src/model.rs:2717-2753), every block's
+// forward_one (src/model.rs:2243-2262), the head and the argmax.
+int decode_launches(ullis_hip_heron* h, const DecodeCall& a, int parity) {
+  ullis_hip_ctx* c = h->ctx;
+  auto& d = h->dec;
+  hipStream_t s = c->stream;
+  const long B = d.batch, D = h->D, F = h->F, V = h->V, L = h->L;
+  const long nd = B * D, words = cdiv(nd, 32);
+  const bool fused = decode_fused_ok(B, D, F);
+  float* rp_in = d.rosa_prev + parity * L * nd;
+  float* rp_out = d.rosa_prev + (1 - parity) * L * nd;
+  float* cp_in = d.cmix_prev + parity * L * nd;
+  float* cp_out = d.cmix_prev + (1 - parity) * L * nd;
+  const Block& b0 = h->blocks[0];
+  // x = emb(token); h = ln0(x) at the first block
+  const bool ln0_fused = fused;  // the embedding kernel applies LN0 where the fused kernels apply
+  STEP(decode_embed(s, a.table, a.vocab, D, a.tokens, B, d.x, a.invalid,
+                    b0.has_ln0 && ln0_fused ? b0.ln0.w : nullptr,
+                    b0.has_ln0 && ln0_fused ? b0.ln0.b : nullptr),
+       "decode embed");
+  if (b0.has_ln0 && !ln0_fused) {
+    STEP(layer_norm_forward(s, d.x, B, D, b0.ln0.w, b0.ln0.b, d.ln, nullptr), "ln0");
+    STEP(copy_device(s, d.x, d.ln, 4l * nd), "ln0 copy");
+  }
+  for (long l = 0; l < L; ++l) {
+    const Block& b = h->blocks[l];
+    // ROSA forward_one (src/model.rs:1320-1353): the Q/K/V sign planes of
+    // mix(LN3(h)) (bit_from_activation, src/rosa.rs:372)
+    DecodeQkv p;
+    DecodeO po;
+    if (fused) {
+      const Packed* lin[3] = {&b.q, &b.k, &b.v};
+      const uint16_t* mix[3] = {b.x_q, b.x_k, b.x_v};
+      for (int j = 0; j < 3; ++j) {
+        p.mix[j] = mix[j];
+        p.bits[j] = lin[j]->bits;
+        p.scale[j] = lin[j]->scale;
+        p.bias[j] = lin[j]->bias;
+        p.planes[j] = d.planes + j * words;
+      }
+      po.idx = a.rosa_idx ? a.rosa_idx + l * nd : d.idx;
+      po.e = b.e;
+      po.bits = b.o.bits;
+      po.scale = b.o.scale;
+      po.bias = b.o.bias;
+      // with the indices given, Q/K/V and O in one launch; a live automaton
+      // needs this token's Q/K/V planes first
+      STEP(decode_qkvo(s, d.x, d.x2, B, D, a.sam ? 0 : 2, b.ln3.w, b.ln3.b, rp_in + l * nd,
+                       rp_out + l * nd, p, po),
+           "decode qkv");
+    } else {
+      STEP(layer_norm_forward(s, d.x, B, D, b.ln3.w, b.ln3.b, d.ln, nullptr), "ln3");
+      STEP(decode_mix(s, d.ln, rp_in + l * nd, rp_out + l * nd, B, D, b.x_q, d.q16, b.x_k,
+                      d.k16, b.x_v, d.v16),
+           "rosa mixes");
+      PackedFwdOut oq, ok, ov;
+      oq.y32 = d.q;
+      ok.y32 = d.k;
+      ov.y32 = d.v;
+      STEP(packed_forward(s, d.q16, kF16, B, D, D, b.q.bits, b.q.scale, b.q.bias, oq), "q");
+      STEP(packed_forward(s, d.k16, kF16, B, D, D, b.k.bits, b.k.scale, b.k.bias, ok), "k");
+      STEP(packed_forward(s, d.v16, kF16, B, D, D, b.v.bits, b.v.scale, b.v.bias, ov), "v");
+      STEP(sign_pack_bits(s, d.q, nd, d.planes), "q bits");
+      STEP(sign_pack_bits(s, d.k, nd, d.planes + words), "k bits");
+      STEP(sign_pack_bits(s, d.v, nd, d.planes + 2 * words), "v bits");
+    }
+    const uint8_t* idx = a.rosa_idx ? a.rosa_idx + l * nd : d.idx;
+    if (a.sam) {
+      STEP(hipMemcpyAsync(d.planes_host, d.planes, 4ul * 3 * words, hipMemcpyDeviceToHost, s),
+           "planes to host");
+      STEP(hipStreamSynchronize(s), "planes sync");
+      const int cb = a.sam(a.sam_user, (size_t)l, d.planes_host, d.idx_host);
+      if (cb != 0)
+        return c->fail(ULLIS_HIP_ERR_INVALID, "suffix automaton callback failed at layer " +
+                                                  std::to_string(l) + " (" + std::to_string(cb) +
+                                                  ")");
+      STEP(hipMemcpyAsync(d.idx, d.idx_host, (size_t)nd, hipMemcpyHostToDevice, s),
+           "indices to device");
+    }
+    // h += O((2 idx - 1) e); the fused path leaves it in x2
+    if (fused) {
+      if (a.sam)
+        STEP(decode_qkvo(s, d.x, d.x2, B, D, 1, b.ln3.w, b.ln3.b, rp_in + l * nd,
+                         rp_out + l * nd, p, po),
+             "decode o");
+    } else {
+      STEP(rosa_expand(s, idx, b.e, B, 1, D, d.y16, d.idx_rm), "rosa y");
+      PackedFwdOut o;
+      o.y32 = d.x;
+      o.resid = d.x;
+      STEP(packed_forward(s, d.y16, kF16, B, D, D, b.o.bits, b.o.scale, b.o.bias, o), "o");
+    }
+    // CMix forward_one (src/model.rs:1003-1016): h += value(relu2(key(mix(ln2(h)))))
+    if (fused) {
+      STEP(decode_key(s, d.x2, B, D, F, b.ln2.w, b.ln2.b, cp_in + l * nd, cp_out + l * nd,
+                      b.cx_k, b.key.bits, b.key.scale, d.r2_16),
+           "decode key");
+    } else {
+      STEP(layer_norm_forward(s, d.x, B, D, b.ln2.w, b.ln2.b, d.ln, nullptr), "ln2");
+      STEP(decode_mix(s, d.ln, cp_in + l * nd, cp_out + l * nd, B, D, b.cx_k, d.sh16, nullptr,
+                      nullptr, nullptr, nullptr),
+           "cmix mix");
+      PackedFwdOut o;
+      o.y16 = d.key16;  // the products write relu2 beside the key itself
+      o.relu2_16 = d.r2_16;
+      STEP(packed_forward(s, d.sh16, kF16, B, D, F, b.key.bits, b.key.scale, nullptr, o), "key");
+    }
+    STEP(fp16_forward(s, d.r2_16, kF16, B, F, D, b.value, d.x, fused ? d.x2 : d.x, nullptr),
+         "value");
+  }
+  if (fused) {
+    STEP(decode_head(s, d.x, B, D, V, h->ln_out.w, h->ln_out.b, h->head.bits, h->head.scale,
+                     h->head.bias, a.logits),
+         "decode head");
+  } else {
+    STEP(layer_norm_forward(s, d.x, B, D, h->ln_out.w, h->ln_out.b, nullptr, d.hid16), "ln_out");
+    PackedFwdOut o;
+    o.y32 = a.logits;
+    STEP(packed_forward(s, d.hid16, kF16, B, D, V, h->head.bits, h->head.scale, h->head.bias, o),
+         "head");
+  }
+  if (a.next) STEP(argmax_rows(s, a.logits, B, V, a.next), "argmax");
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
 
 int ullis_hip_heron_decode_step(ullis_hip_heron* h, const uint16_t* table, size_t vocab,
                                 const uint32_t* tokens, const uint8_t* rosa_idx,
@@ -1292,81 +1468,41 @@ int ullis_hip_heron_decode_step(ullis_hip_heron* h, const uint16_t* table, size_
   if ((rosa_idx == nullptr) == (sam == nullptr))
     return c->fail(ULLIS_HIP_ERR_INVALID,
                    "decode step takes either the automaton's indices or its callback");
-  hipStream_t s = c->stream;
-  const long B = d.batch, D = h->D, F = h->F, V = h->V, L = h->L;
-  const long nd = B * D, words = cdiv(nd, 32);
-  // generate_step (src/model.rs:2717-2753): the embedding rows
-  STEP(fill_f32(s, reinterpret_cast<float*>(d.invalid), 1, 0.0f), "clear invalid");
-  STEP(embedding_gather(s, table, (long)vocab, D, tokens, B, d.x, d.invalid), "decode gather");
-  for (long l = 0; l < L; ++l) {
-    const Block& b = h->blocks[l];
-    // forward_one (src/model.rs:2243-2262): h = ln0(x) at the first block
-    if (b.has_ln0) {
-      STEP(layer_norm_forward(s, d.x, B, D, b.ln0.w, b.ln0.b, d.v, nullptr), "ln0");
-      STEP(copy_device(s, d.x, d.v, 4ul * nd), "ln0 copy");
+  const DecodeCall a{table, (long)vocab, tokens, rosa_idx, sam, sam_user, logits, next_tokens,
+                     invalid};
+  const int par = d.parity;
+  if (sam || t_launch_probe || d.eager) {
+    // a live automaton synchronises with the host every layer: eager launches
+    if (int rc = decode_launches(h, a, par)) return rc;
+  } else {
+    hipStream_t s = c->stream;
+    const auto key = a.key();
+    if (!d.graph[par] || !(d.graph_key[par] == key)) {
+      if (d.graph[par]) {
+        STEP(hipStreamSynchronize(s), "decode graph sync");
+        STEP(hipGraphExecDestroy(d.graph[par]), "decode graph destroy");
+        d.graph[par] = nullptr;
+      }
+      STEP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "decode graph capture");
+      const int rc = decode_launches(h, a, par);
+      hipGraph_t g = nullptr;
+      const hipError_t end = hipStreamEndCapture(s, &g);
+      if (rc) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+      }
+      if (int rc2 = c->hip(end, "decode graph capture end")) return rc2;
+      const hipError_t inst = hipGraphInstantiate(&d.graph[par], g, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(g);
+      if (int rc2 = c->hip(inst, "decode graph instantiate")) {
+        d.graph[par] = nullptr;
+        return rc2;
+      }
+      d.graph_key[par] = key;
     }
-    // ROSA forward_one (src/model.rs:1320-1353)
-    STEP(layer_norm_forward(s, d.x, B, D, b.ln3.w, b.ln3.b, d.ln, nullptr), "ln3");
-    STEP(decode_mix(s, d.ln, d.rosa_prev + l * nd, d.has_prev, B, D, b.x_q, d.q16, b.x_k, d.k16,
-                    b.x_v, d.v16),
-         "rosa mixes");
-    {
-      PackedFwdOut oq, ok, ov;
-      oq.y32 = d.q;
-      ok.y32 = d.k;
-      ov.y32 = d.v;
-      STEP(packed_forward(s, d.q16, kF16, B, D, D, b.q.bits, b.q.scale, b.q.bias, oq), "q");
-      STEP(packed_forward(s, d.k16, kF16, B, D, D, b.k.bits, b.k.scale, b.k.bias, ok), "k");
-      STEP(packed_forward(s, d.v16, kF16, B, D, D, b.v.bits, b.v.scale, b.v.bias, ov), "v");
-      // bit_from_activation (src/rosa.rs:372), the bits RosaSam::push takes
-      STEP(sign_pack_bits(s, d.q, nd, d.planes), "q bits");
-      STEP(sign_pack_bits(s, d.k, nd, d.planes + words), "k bits");
-      STEP(sign_pack_bits(s, d.v, nd, d.planes + 2 * words), "v bits");
-    }
-    const uint8_t* idx = rosa_idx ? rosa_idx + l * nd : d.idx;
-    if (sam) {
-      STEP(hipMemcpyAsync(d.planes_host, d.planes, 4ul * 3 * words, hipMemcpyDeviceToHost, s),
-           "planes to host");
-      STEP(hipStreamSynchronize(s), "planes sync");
-      const int cb = sam(sam_user, (size_t)l, d.planes_host, d.idx_host);
-      if (cb != 0)
-        return c->fail(ULLIS_HIP_ERR_INVALID, "suffix automaton callback failed at layer " +
-                                                  std::to_string(l) + " (" + std::to_string(cb) +
-                                                  ")");
-      STEP(hipMemcpyAsync(d.idx, d.idx_host, (size_t)nd, hipMemcpyHostToDevice, s),
-           "indices to device");
-    }
-    // y = (2 idx - 1) e; h += O(y)
-    STEP(rosa_expand(s, idx, b.e, B, 1, D, d.y16, d.idx_rm), "rosa y");
-    {
-      PackedFwdOut o;
-      o.y32 = d.x;
-      o.resid = d.x;
-      STEP(packed_forward(s, d.y16, kF16, B, D, D, b.o.bits, b.o.scale, b.o.bias, o), "o");
-    }
-    // CMix forward_one (src/model.rs:1003-1016): h += value(relu2(key(mix(ln2(h)))))
-    STEP(layer_norm_forward(s, d.x, B, D, b.ln2.w, b.ln2.b, d.ln, nullptr), "ln2");
-    STEP(decode_mix(s, d.ln, d.cmix_prev + l * nd, d.has_prev, B, D, b.cx_k, d.sh16, nullptr,
-                    nullptr, nullptr, nullptr),
-         "cmix mix");
-    {
-      PackedFwdOut o;
-      o.y16 = d.key16;  // the products write relu2 beside the key itself
-      o.relu2_16 = d.r2_16;
-      STEP(packed_forward(s, d.sh16, kF16, B, D, F, b.key.bits, b.key.scale, nullptr, o), "key");
-    }
-    STEP(fp16_forward(s, d.r2_16, kF16, B, F, D, b.value, d.x, d.x, nullptr), "value");
+    STEP(hipGraphLaunch(d.graph[par], s), "decode graph launch");
   }
-  STEP(layer_norm_forward(s, d.x, B, D, h->ln_out.w, h->ln_out.b, nullptr, d.hid16), "ln_out");
-  {
-    PackedFwdOut o;
-    o.y32 = logits;
-    STEP(packed_forward(s, d.hid16, kF16, B, D, V, h->head.bits, h->head.scale, h->head.bias, o),
-         "head");
-  }
-  if (next_tokens) STEP(argmax_rows(s, logits, B, V, next_tokens), "argmax");
-  if (invalid) STEP(copy_device(s, invalid, d.invalid, sizeof(uint32_t)), "invalid");
-  d.has_prev = true;
+  d.parity = 1 - par;
   return 0;
 }
 

@@ -308,11 +308,50 @@ hipError_t rosa_expand_layers(hipStream_t s, const uint8_t* idx_cm, const uint16
                               long ch, uint16_t* y16, uint8_t* idx_rm);
 
 // ----------------------------------------------------------- T = 1 decode
-// out_j = f16(x + (prev - x) * mix_j) (xx = -x without a previous token) for
-// the given mixes (null: skipped), then prev = x; x / prev fp32 [rows][d].
-hipError_t decode_mix(hipStream_t s, const float* x, float* prev, bool has_prev, long rows,
-                      long d, const uint16_t* mix0, uint16_t* out0, const uint16_t* mix1,
-                      uint16_t* out1, const uint16_t* mix2, uint16_t* out2);
+// Fused decode kernels (decode.hip) for rows <= 8, d % 128 == 0, d <= 1024,
+// f % 32 == 0 and the rows' fp16 inputs within 64 KiB of LDS.
+bool decode_fused_ok(long rows, long d, long f);
+struct DecodeQkv {
+  const uint16_t* mix[3];
+  const uint32_t* bits[3];
+  const uint16_t* scale[3];
+  const uint16_t* bias[3];
+  uint32_t* planes[3];  // sign bits, bit b*d + c
+};
+struct DecodeO {
+  const uint8_t* idx;  // u8 [rows][d], 4-byte aligned
+  const uint16_t* e;
+  const uint32_t* bits;
+  const uint16_t* scale;
+  const uint16_t* bias;
+};
+// x = f32 table rows of tokens (ids >= vocab: zero rows; *invalid = their
+// count, when set), then LN0 in place when ln0_w is set (d <= 1024). rows <= 8.
+hipError_t decode_embed(hipStream_t s, const uint16_t* table, long vocab, long d,
+                        const uint32_t* tokens, long rows, float* x, uint32_t* invalid,
+                        const uint16_t* ln0_w, const uint16_t* ln0_b);
+// part 0: planes_j = sign(bias_j + scale_j * (mix_j(LN(x), prev_in) . S_j^T)),
+// prev_out = LN(x); part 1: x2 = x + bias + scale * (((2 idx - 1) e) . S^T);
+// part 2: both in one launch.
+hipError_t decode_qkvo(hipStream_t s, const float* x, float* x2, long rows, long d, int part,
+                       const uint16_t* ln_w, const uint16_t* ln_b, const float* prev_in,
+                       float* prev_out, const DecodeQkv& p, const DecodeO& po);
+// r2 = f16(max(k, 0)^2), k = scale * (mix(LN(x), prev_in) . S^T) [rows][f];
+// prev_out = LN(x).
+hipError_t decode_key(hipStream_t s, const float* x, long rows, long d, long f,
+                      const uint16_t* ln_w, const uint16_t* ln_b, const float* prev_in,
+                      float* prev_out, const uint16_t* mix, const uint32_t* bits,
+                      const uint16_t* scale, uint16_t* r2);
+// logits = bias + scale * (LN(x) . S^T) [rows][vocab].
+hipError_t decode_head(hipStream_t s, const float* x, long rows, long d, long vocab,
+                       const uint16_t* ln_w, const uint16_t* ln_b, const uint32_t* bits,
+                       const uint16_t* scale, const uint16_t* bias, float* logits);
+// General shapes: out_j = f16(x + (prev_in - x) * mix_j) for the given mixes
+// (null: skipped), prev_out = x; x / prev fp32 [rows][d].
+hipError_t decode_mix(hipStream_t s, const float* x, const float* prev_in, float* prev_out,
+                      long rows, long d, const uint16_t* mix0, uint16_t* out0,
+                      const uint16_t* mix1, uint16_t* out1, const uint16_t* mix2,
+                      uint16_t* out2);
 // next[r] = argmax_v logits[r][v] (lowest index among equal maxima).
 hipError_t argmax_rows(hipStream_t s, const float* logits, long rows, long vocab, uint32_t* next);
 

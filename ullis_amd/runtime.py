@@ -632,9 +632,11 @@ class HeronTrainer:
             raise failure[0]
         self.rt._check(rc, "heron_step_sam")
 
-    def decode_init(self, batch: int):
-        """ullis_hip_heron_decode_init: decode state for `batch` (1..8) new sequences."""
-        self.rt._check(self.rt.lib.ullis_hip_heron_decode_init(self.h, batch), "decode_init")
+    def decode_init(self, batch: int, graph: bool = True):
+        """ullis_hip_heron_decode_init: decode state for `batch` (1..8) new
+        sequences; graph=False launches every token eagerly (no graph replay)."""
+        self.rt._check(self.rt.lib.ullis_hip_heron_decode_init(self.h, batch, 0 if graph else 1),
+                       "decode_init")
         self._decode_batch = batch
 
     def decode_step(self, table: DeviceBuffer, tokens: DeviceBuffer, logits: DeviceBuffer,
