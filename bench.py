@@ -455,6 +455,53 @@ def decode_step_bench(rt, steps: int, warmup: int, graph: bool = True) -> None:
         tr.close()
 
 
+VENDOR_SHAPES = [
+    (2048, 2048, 512, "key fwd / value dX"), (2048, 512, 2048, "value fwd / key dX"),
+    (512, 2048, 2048, "value dW / key dW"), (2048, 512, 512, "O fwd / dX"),
+    (2048, 8192, 512, "head logits"), (2048, 512, 8192, "head dX"), (8192, 512, 2048, "head dW"),
+    (32768, 4096, 1024, "config-5 key fwd"), (32768, 1024, 4096, "config-5 value fwd"),
+]
+
+
+def vendor_gemm() -> None:
+    """One JSON line per heron GEMM shape: the vendor fp16 GEMM (torch.matmul,
+    hipBLASLt) on dense fp16 operands, 20 (4 at config 5) launches captured in a
+    graph and replayed 20 times between events, so host launch cost is out of
+    the figure. A yardstick for the products here, which read sign bits and
+    run epilogues; nothing in the library uses it."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    for m, n, k, name in VENDOR_SHAPES:
+        a = torch.randn(m, k, device=dev, dtype=torch.float16)
+        b = torch.randn(k, n, device=dev, dtype=torch.float16)
+        c = torch.empty(m, n, device=dev, dtype=torch.float16)
+        reps = 20 if m * n * k < 1e10 else 4
+        st = torch.cuda.Stream()
+        with torch.cuda.stream(st):
+            for _ in range(3):
+                torch.matmul(a, b, out=c)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=st):
+            for _ in range(reps):
+                torch.matmul(a, b, out=c)
+        for _ in range(3):
+            g.replay()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(20):
+            g.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1e3 / (20 * reps)
+        tf = 2.0 * m * n * k / (us * 1e-6) / 1e12
+        print(json.dumps({"vendor_gemm": name, "shape_MNK": [m, n, k], "us": round(us, 2),
+                          "tflops": round(tf, 1), "frac": round(tf / FP16_PEAK_TFLOPS, 4)}),
+              flush=True)
+
+
 def copy_calibration(rt, mib: int) -> None:
     """One copy kernel (ullis_hip_copy) that reads `mib` MiB and writes `mib` MiB.
 
@@ -500,6 +547,9 @@ def main() -> int:
     ap.add_argument("--decode-step", action="store_true",
                     help="instead of the bench line, time the T = 1 decode step at configs 4 "
                          "and 5, batch 1 and 8, against its weight-streaming floor")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="instead of the bench line, time the vendor fp16 GEMM (torch.matmul) at "
+                         "the heron GEMM shapes, as a yardstick")
     ap.add_argument("--graph", type=int, default=None,
                     help="1: replay each step's launches from a captured HIP graph (default 0; "
                          "with --decode-step, default 1)")
@@ -509,6 +559,9 @@ def main() -> int:
     args = ap.parse_args()
     if args.cpu_sample > 0:
         cpu_sample(args.cpu_sample)
+        return 0
+    if args.vendor_gemm:
+        vendor_gemm()
         return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
