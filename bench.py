@@ -524,7 +524,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--cpu-rows", type=int, default=256,
+    ap.add_argument("--cpu-rows", type=int, default=128,
                     help="tokens of each CPU-baseline window (0 disables it)")
     ap.add_argument("--cpu-runs", type=int, default=3,
                     help="CPU-baseline windows, run side by side; the median is reported")
