@@ -681,6 +681,14 @@ def main() -> int:
                              if prof_us else None),
             "probe_pass_ms_per_step": round(st_ms / args.steps, 4),
         }
+    # the reference's TrainStepProfile phases (main-stream segments), over a
+    # few more steps run eagerly, outside the reported ones
+    phases = None
+    if args.probe != "none":
+        trainer.phases_begin()
+        timed(5)
+        ph = trainer.phases_end()
+        phases = {k: round(v, 4) for k, v in ph["phases_ms"].items()}
     if args.copy_mib > 0:
         copy_calibration(rt, args.copy_mib)
 
@@ -706,6 +714,7 @@ def main() -> int:
         "roofline": rooflines.get("roofline"),
         "roofline_packed": rooflines.get("roofline_packed"),
         "cpu_baseline": baseline,
+        "phases_ms": phases,
     }
     print(json.dumps(line), flush=True)
     trainer.close()

@@ -441,6 +441,33 @@ int ullis_hip_heron_set_graph(ullis_hip_heron* h, int enable);
 int ullis_hip_heron_probe(ullis_hip_heron* h, int probe_id);
 int ullis_hip_heron_probe_read(ullis_hip_heron* h, float* total_ms, int* launches);
 
+/*
+ * Step phases: the reference's TrainStepProfile (src/model.rs:101-124,
+ * 2864-2994) names its wall-clock phases embed, fwd_ln, fwd_rosa, fwd_cmix,
+ * head, bwd_ln, bwd_cmix, bwd_rosa, embed_sgd (ULLIS_HIP_PHASE_* order below).
+ * ullis_hip_heron_phases(h, 1) times the steps that follow (run eagerly, not
+ * from a graph) with events on the main stream at those phase boundaries;
+ * ullis_hip_heron_phases_read waits for the device and writes, per phase, the
+ * milliseconds of the main stream's segments summed over those steps (*steps
+ * = their number). The main stream carries the step's dependent chain; work
+ * the second stream runs beside it (the Q/K/V branch, the O products and
+ * backward, the deferred updates) is inside those segments, and the wait for
+ * its tail at the step's end counts as bwd_rosa. At most about 2000 phase
+ * boundaries (about 25 config-4 steps) between enabling and reading.
+ */
+#define ULLIS_HIP_PHASE_EMBED 0
+#define ULLIS_HIP_PHASE_FWD_LN 1
+#define ULLIS_HIP_PHASE_FWD_ROSA 2
+#define ULLIS_HIP_PHASE_FWD_CMIX 3
+#define ULLIS_HIP_PHASE_HEAD 4
+#define ULLIS_HIP_PHASE_BWD_LN 5
+#define ULLIS_HIP_PHASE_BWD_CMIX 6
+#define ULLIS_HIP_PHASE_BWD_ROSA 7
+#define ULLIS_HIP_PHASE_EMBED_SGD 8
+#define ULLIS_HIP_PHASE_COUNT 9
+int ullis_hip_heron_phases(ullis_hip_heron* h, int enable);
+int ullis_hip_heron_phases_read(ullis_hip_heron* h, float* ms, int* steps);
+
 #ifdef __cplusplus
 }
 #endif

@@ -16,6 +16,7 @@ sign-bit fractions. Sign bits are compared as mismatch fractions: a latent
 within rounding of 0, or a projection output within rounding of 0, may land
 on either side.
 """
+import ctypes as C
 import json
 import pathlib
 
@@ -545,3 +546,51 @@ def test_graph_replay_of_steps_from_tokens(rt):
     for i, (e, r) in enumerate(zip(eager, graph)):
         for a, b in zip(e, r):
             np.testing.assert_array_equal(a, b, err_msg=f"step {i}")
+
+
+def test_step_phases_cover_the_step_and_change_nothing(rt):
+    """ullis_hip_heron_phases (the reference's TrainStepProfile phases,
+    src/model.rs:2864-2994): every phase of a step from token ids gets time,
+    the phases add up to the step as events around it read it, and a phased
+    step's results are bit-identical to an unphased one's."""
+    shape = HeronShape(d_model=128, n_layers=2, dim_ffn=512, vocab=1024, batch=2, time=128)
+    trainer = HeronTrainer(rt, shape)
+    arena = heron_arena(trainer.layout, trainer.arena_bytes, shape.dims(), seed=13)
+    _, labels, idx = step_inputs(shape.rows, 128, 1024, 2, 2, 128, seed=13)
+    rng = np.random.default_rng(13)
+    table = rng.standard_normal(1024 * 128).astype(np.float16).view(np.uint16)
+    tokens = rt.put(rng.integers(0, 1024, shape.rows).astype(np.uint32))
+    dl, di = rt.put(labels), rt.put(idx)
+    nd = shape.rows * 128
+    xe, g = rt.zeros(np.float32, nd), rt.zeros(np.float32, nd)
+    rl = rt.zeros(np.float32, shape.rows)
+    lib, ctx = rt.lib, rt.ctx
+
+    def run(phased, steps=3):
+        trainer.upload_arena(arena)
+        dt, dtr = rt.put(table), rt.zeros(np.float32, table.size)
+        if phased:
+            trainer.phases_begin()
+        rt.sync()
+        rt._check(lib.ullis_hip_event_record(ctx, 0), "event")
+        for _ in range(steps):
+            trainer.step_tokens(dt, dtr, tokens, dl, NO_IGNORE, 0.01, di, xe, g, rl)
+        rt._check(lib.ullis_hip_event_record(ctx, 1), "event")
+        rt.sync()
+        ms = C.c_float()
+        rt._check(lib.ullis_hip_event_elapsed_ms(ctx, 0, 1, C.byref(ms)), "elapsed")
+        ph = trainer.phases_end() if phased else None
+        return (trainer.download_arena(), dt.download(np.uint16),
+                rl.download(np.float32).view(np.uint32)), ms.value / steps, ph
+
+    plain, _, _ = run(False)
+    phased, step_ms, ph = run(True)
+    for a, b in zip(plain, phased):
+        np.testing.assert_array_equal(a, b)
+    assert ph["steps"] == 3
+    assert set(ph["phases_ms"]) == set(HeronTrainer.PHASES)
+    assert all(v > 0.0 for v in ph["phases_ms"].values()), ph
+    total = sum(ph["phases_ms"].values())
+    # the phases run from the gather to the step's last launch; the events
+    # around the steps also hold the launches between steps
+    assert 0.8 * step_ms <= total <= 1.001 * step_ms, (total, step_ms)

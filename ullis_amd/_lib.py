@@ -127,6 +127,8 @@ SIGNATURES = {
     "ullis_hip_heron_refresh_derived": (i32, [vp]),
     "ullis_hip_heron_step": (i32, [vp, vp, vp, u32, f32, vp, vp, vp, vp, vp, vp]),
     "ullis_hip_heron_causal_loss": (i32, [vp, vp, vp, u32, vp, vp, sz, vp]),
+    "ullis_hip_heron_phases": (i32, [vp, i32]),
+    "ullis_hip_heron_phases_read": (i32, [vp, vp, vp]),
     "ullis_hip_heron_decode_init": (i32, [vp, sz, i32]),
     "ullis_hip_heron_decode_step": (i32, [vp, vp, sz, vp, vp, SAM_FN, vp, vp, vp, vp]),
     "ullis_hip_heron_step_sam": (i32, [vp, vp, vp, sz, vp, vp, vp, u32, f32, SAM_FN, vp, vp, vp,

@@ -192,6 +192,13 @@ struct ullis_hip_heron {
   bool probe_events_only = false;  // ULLIS_HIP_PROBE_EVENTS: GEMMs timed by events too
   int probe_used = 0;
   std::vector<hipEvent_t> probe_events;
+  // phase timing (ullis_hip_heron_phases): events on the main stream at the
+  // boundaries of the reference's TrainStepProfile phases; phase_id[i] is the
+  // phase of the segment that starts at event i (-1: a step's end)
+  bool phase_on = false;
+  int phase_n = 0;
+  std::vector<hipEvent_t> phase_ev;
+  std::vector<int> phase_id;
   unsigned long long* probe_stamps = nullptr;  // device [kStampTotal][2], lazily
   std::vector<long> probe_blocks;              // per probed launch: stamped blocks, 0 = events
   std::vector<long> probe_offset;              // per probed launch: first stamp slot
@@ -256,6 +263,21 @@ bool bind_packed(ullis_hip_heron* h, const std::string& p, long out, long in, bo
   } while (0)
 
 constexpr int kProbeMax = 512;
+constexpr int kPhaseMax = 2048;
+// The reference's phase names (TrainStepProfile, src/model.rs:2864-2994).
+enum Phase : int {
+  kPhEmbed = 0, kPhFwdLn, kPhFwdRosa, kPhFwdCmix, kPhHead, kPhBwdLn, kPhBwdCmix, kPhBwdRosa,
+  kPhEmbedSgd, kPhEnd = -1
+};
+static_assert(kPhEmbedSgd + 1 == ULLIS_HIP_PHASE_COUNT, "phase names");
+// Marks the start of phase k on stream `st` when phase timing is on.
+#define PHASE_AT(st, k)                                                          \
+  do {                                                                           \
+    if (h->phase_on && h->phase_n < kPhaseMax) {                                 \
+      STEP(hipEventRecord(h->phase_ev[h->phase_n], (st)), "phase event");       \
+      h->phase_id[h->phase_n++] = (k);                                           \
+    }                                                                            \
+  } while (0)
 // (start, end) slots for every workgroup of the stamped launches of one probe
 // pass; a launch that no longer fits is timed by events instead
 constexpr long kStampTotal = 1L << 22;
@@ -662,6 +684,7 @@ void ullis_hip_heron_destroy(ullis_hip_heron* h) {
   if (!h) return;
   if (h->ctx) (void)hipStreamSynchronize(h->ctx->stream);
   for (auto& e : h->probe_events) (void)hipEventDestroy(e);
+  for (auto& e : h->phase_ev) (void)hipEventDestroy(e);
   if (h->side) (void)hipStreamSynchronize(h->side);
   for (auto* v : {&h->ev_fwd, &h->ev_bwd, &h->ev_o})
     for (auto& e : *v)
@@ -712,6 +735,44 @@ int ullis_hip_heron_probe(ullis_hip_heron* h, int probe_id) {
            h->probe_stamps, n);
     STEP(hipGetLastError(), "probe stamps clear");
   }
+  return 0;
+}
+
+int ullis_hip_heron_phases(ullis_hip_heron* h, int enable) {
+  if (!h) return ULLIS_HIP_ERR_INVALID;
+  ullis_hip_ctx* c = h->ctx;
+  if (enable && h->phase_ev.empty()) {
+    h->phase_ev.assign(kPhaseMax, nullptr);
+    h->phase_id.assign(kPhaseMax, kPhEnd);
+    for (auto& e : h->phase_ev)
+      if (hipEventCreate(&e) != hipSuccess) {
+        (void)hipGetLastError();
+        return c->fail(ULLIS_HIP_ERR_RUNTIME, "phase event creation failed");
+      }
+  }
+  h->phase_on = enable != 0;
+  h->phase_n = 0;
+  return 0;
+}
+
+int ullis_hip_heron_phases_read(ullis_hip_heron* h, float* ms, int* steps) {
+  if (!h || !ms || !steps) return ULLIS_HIP_ERR_INVALID;
+  ullis_hip_ctx* c = h->ctx;
+  STEP(hipStreamSynchronize(c->stream), "phases sync");
+  STEP(hipStreamSynchronize(h->side), "phases sync");
+  if (h->phase_n >= kPhaseMax)
+    return c->fail(ULLIS_HIP_ERR_INVALID, "phase event capacity exceeded: read after fewer steps");
+  double sum[ULLIS_HIP_PHASE_COUNT] = {};
+  int n = 0;
+  for (int i = 0; i + 1 < h->phase_n; ++i) {
+    if (h->phase_id[i] == kPhEnd) continue;
+    float t = 0.0f;
+    STEP(hipEventElapsedTime(&t, h->phase_ev[i], h->phase_ev[i + 1]), "phase elapsed");
+    sum[h->phase_id[i]] += t;
+  }
+  for (int i = 0; i < h->phase_n; ++i) n += h->phase_id[i] == kPhEnd ? 1 : 0;
+  for (int k = 0; k < ULLIS_HIP_PHASE_COUNT; ++k) ms[k] = (float)sum[k];
+  *steps = n;
   return 0;
 }
 
@@ -801,6 +862,7 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
   int nb = 0;
   bool ln0_now = false;
 
+  PHASE_AT(s, kPhFwdRosa);
   STEP(fill_f32(s, h->slots, L + 2, 0.0f), "clear amax slots");
   // a step from token ids has cleared the counter before its gather
   if (!emb) STEP(fill_f32(s, reinterpret_cast<float*>(h->invalid), 1, 0.0f), "clear invalid");
@@ -842,6 +904,7 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
     Block& b = h->blocks[l];
     float* x_l = h->resid + l * nd;
     if (b.has_ln0) {
+      PHASE_AT(s, kPhFwdLn);
       STEP(layer_norm_forward(s, x_emb, R, D, b.ln0.w, b.ln0.b, x_l, nullptr), "ln0");
     } else if (l == 0) {
       STEP(copy_device(s, x_l, x_emb, (long)sizeof(float) * nd), "copy x");
@@ -852,6 +915,7 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
     // their sign bit-planes to the host, the caller's automaton, the indices
     // back, y = (2 idx - 1) e and the O product (src/metal.rs:1411-1511).
     hipStream_t qs = live ? s : h->side;
+    PHASE_AT(s, kPhFwdRosa);
     if (!live) {
       STEP(hipEventRecord(h->ev_fwd[l], s), "event");
       STEP(hipStreamWaitEvent(h->side, h->ev_fwd[l], 0), "event wait");
@@ -902,10 +966,12 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
     uint16_t* key = h->key16 + l * nf;
     uint16_t* r2 = h->relu2_16 + l * nf;
     if (!live) STEP(hipStreamWaitEvent(s, h->ev_o[l], 0), "event wait");
+    PHASE_AT(s, kPhFwdLn);
     PROBED(ULLIS_HIP_PROBE_LN_FORWARD,
            layer_norm_mix_forward(s, h->o_pre + l * nd, R, T, D, b.ln2.w, b.ln2.b, ln2, true,
                                   b.cx_k, sh, nullptr, nullptr, nullptr, nullptr, x_l, ar),
            "ln2 + mix");
+    PHASE_AT(s, kPhFwdCmix);
     {
       PackedFwdOut o;
       o.y16 = key;
@@ -918,7 +984,9 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
            "value");
   }
   float* x_last = h->resid + L * nd;
+  PHASE_AT(s, kPhFwdLn);
   STEP(layer_norm_forward(s, x_last, R, D, h->ln_out.w, h->ln_out.b, nullptr, h->ln16), "ln_out");
+  PHASE_AT(s, kPhHead);
 
   // ------------------------------------------------------------ head + CE
   {
@@ -946,6 +1014,7 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
     PROBED_SPAN(ULLIS_HIP_PROBE_HEAD_CE, head_ce(s, hc, h->head_ws), "head ce");
   }
   // LN_out backward (src/model.rs:2932-2937)
+  PHASE_AT(s, kPhBwdLn);
   STEP(layer_norm_backward_rows(s, x_last, h->g_a, R, D, h->ln_out.w, h->g_x, 0, h->slots + L,
                                 h->pt_lnout, &nb),
        "ln_out bwd");
@@ -969,6 +1038,7 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
     const float* ar = h->after_rosa + l * nd;
     const long pc = (long)h->nb_col * D;
 
+    PHASE_AT(s, kPhBwdCmix);
     // CMix backward (src/model.rs:1145-1177): value input gradient (+ ReLU^2
     // backward into gk16) with the value weight gradient, then the key input
     // gradient with the key weight gradient
@@ -993,6 +1063,7 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
     }
     // CMix time-shift mix backward (x_k gradient) fused with the LN2
     // backward, += into g_x (src/model.rs:2958-2963)
+    PHASE_AT(s, kPhBwdLn);
     {
       int nb_mix = 0;
       PROBED(ULLIS_HIP_PROBE_LN_BACKWARD,
@@ -1006,6 +1077,7 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
     // O bias gradient (column sums of g_x) and the fp16 copy of g_x for the
     // O GEMMs here and the CMix GEMMs of the block below.
     uint16_t* gx16_l = h->gx16_b + l * nd;
+    PHASE_AT(s, kPhBwdRosa);
     STEP(column_sum_partials(s, h->g_x, nullptr, R, D, h->pt_ob + l * pc, &nb, gx16_l, slot_mid),
          "o g_bias + g_x fp16");
     if (nb != h->nb_col) return c->fail(ULLIS_HIP_ERR_RUNTIME, "o bias partial count");
@@ -1034,6 +1106,7 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
     if (int rc = run_update_seg(h, h->side, (int)l, lr)) return rc;
 
     if (b.has_ln0) {  // (src/model.rs:2978-2982)
+      PHASE_AT(s, kPhBwdLn);
       STEP(layer_norm_backward_rows(s, x_emb, h->g_x, R, D, b.ln0.w, g_emb, 0, nullptr, h->pt_ln0,
                                     &nb),
            "ln0 bwd");
@@ -1050,11 +1123,14 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
     }
   }
 
+  if (emb) PHASE_AT(s, kPhEmbedSgd);
   if (emb)
     STEP(embedding_scatter_sgd(s, emb->table, emb->residual, emb->vocab, D, emb->tokens, R, g_emb,
                                lr, h->invalid),
          "embedding scatter sgd");
   // the second stream's work is done before the updates and the step's end
+  // (its tail is the O backward and the updates: timed as bwd_rosa)
+  PHASE_AT(s, kPhBwdRosa);
   STEP(hipEventRecord(h->ev_join, h->side), "event");
   STEP(hipStreamWaitEvent(s, h->ev_join, 0), "event wait");
 
@@ -1065,6 +1141,7 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
   for (const Packed* k : h->trans_generic)
     STEP(transpose_bits(s, k->bits, k->out, k->in, k->bits_t), "bits_t");
   if (invalid_out) STEP(copy_device(s, invalid_out, h->invalid, sizeof(uint32_t)), "invalid");
+  PHASE_AT(s, kPhEnd);
   return 0;
 }
 
@@ -1105,6 +1182,7 @@ int step_call_launches(ullis_hip_heron* h, const StepCall& sc) {
                          sc.row_loss, sc.stats4, sc.qkv_bits, sc.invalid, nullptr, sc.live);
   // the refused-step counter starts the step here: the gather adds the token
   // ids >= vocab, the head the labels >= vocab
+  PHASE_AT(c->stream, kPhEmbed);
   STEP(fill_f32(c->stream, reinterpret_cast<float*>(h->invalid), 1, 0.0f), "clear invalid");
   STEP(embedding_gather(c->stream, sc.emb.table, sc.emb.vocab, h->D, sc.emb.tokens, h->rows,
                         const_cast<float*>(sc.x_emb), h->invalid),
@@ -1119,7 +1197,8 @@ int run_step(ullis_hip_heron* h, const StepCall& sc) {
   ullis_hip_ctx* c = h->ctx;
   // probed steps run eagerly: the probe times individual launches; so do
   // steps with a live automaton, which synchronise with the host every layer
-  if (!h->graph_on || h->probe != ULLIS_HIP_PROBE_NONE || t_launch_probe || sc.live)
+  if (!h->graph_on || h->probe != ULLIS_HIP_PROBE_NONE || t_launch_probe || sc.live ||
+      h->phase_on)
     return step_call_launches(h, sc);
   const ullis_hip_heron::StepArgs args = sc.key();
   hipStream_t s = c->stream;

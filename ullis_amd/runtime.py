@@ -632,6 +632,26 @@ class HeronTrainer:
             raise failure[0]
         self.rt._check(rc, "heron_step_sam")
 
+    PHASES = ("embed", "fwd_ln", "fwd_rosa", "fwd_cmix", "head", "bwd_ln", "bwd_cmix",
+              "bwd_rosa", "embed_sgd")
+
+    def phases_begin(self):
+        """ullis_hip_heron_phases(h, 1): time the following steps by the
+        reference's TrainStepProfile phases (main-stream segments)."""
+        self.rt._check(self.rt.lib.ullis_hip_heron_phases(self.h, 1), "phases")
+
+    def phases_end(self) -> dict:
+        """The phases' milliseconds per step since phases_begin (averaged over
+        the steps), as TrainStepProfile.phases_ms; stops the timing."""
+        ms = (C.c_float * len(self.PHASES))()
+        steps = C.c_int()
+        self.rt._check(self.rt.lib.ullis_hip_heron_phases_read(self.h, ms, C.byref(steps)),
+                       "phases read")
+        self.rt._check(self.rt.lib.ullis_hip_heron_phases(self.h, 0), "phases")
+        n = max(steps.value, 1)
+        return {"steps": steps.value,
+                "phases_ms": {k: ms[i] / n for i, k in enumerate(self.PHASES)}}
+
     def decode_init(self, batch: int, graph: bool = True):
         """ullis_hip_heron_decode_init: decode state for `batch` (1..8) new
         sequences; graph=False launches every token eagerly (no graph replay)."""
