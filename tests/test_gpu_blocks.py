@@ -328,13 +328,16 @@ def test_block_methods_reject_bad_arguments(rt):
 
 @pytest.mark.parametrize("d,layers,f,vocab,time",
                          [(64, 2, 128, 256, 64), (128, 3, 256, 512, 128),
-                          (512, 2, 2048, 8192, 2048)])
+                          (512, 2, 2048, 8192, 2048), (512, 1, 4096, 512, 8192)])
 def test_block_step_matches_fused_step(rt, d, layers, f, vocab, time):
     """HeronBlockStep (block methods, host residual adds, the automaton
     handed the Q/K/V planes between the projections and O) against the fused
     step on the same arena and inputs: bit-identical, since both run the same
     kernels with the same reductions and the same update arithmetic (the
-    last case has config 4's widths at two layers)."""
+    third case has config 4's widths at two layers). In the last case the
+    fused step's value input gradient reads its value^T cache (both operands
+    k-contiguous) and the block path the value weight itself (a transposed
+    operand): every output still sums the same products in the same order."""
     shape = HeronShape(d_model=d, n_layers=layers, dim_ffn=f, vocab=vocab, batch=1, time=time)
     fused = HeronTrainer(rt, shape)
     blocks = HeronBlockStep(rt, shape)

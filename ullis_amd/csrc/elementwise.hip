@@ -375,6 +375,39 @@ hipError_t fill_f32(hipStream_t s, float* p, long n, float v) {
   return hipGetLastError();
 }
 
+namespace {
+
+// dst[c][r] = src[r][c] for one 64 x 64 tile of 16-bit values through LDS
+// (a padded row keeps the column reads free of bank conflicts).
+__global__ __launch_bounds__(256) void transpose_u16_kernel(const uint16_t* __restrict__ src,
+                                                            long rows, long cols,
+                                                            uint16_t* __restrict__ dst) {
+  __shared__ uint16_t t[64][66];
+  const long r0 = (long)blockIdx.y * 64, c0 = (long)blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int r = ty + 4 * k;
+    if (r0 + r < rows && c0 + tx < cols) t[r][tx] = src[(r0 + r) * cols + c0 + tx];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int c = ty + 4 * k;
+    if (c0 + c < cols && r0 + tx < rows) dst[(c0 + c) * rows + r0 + tx] = t[tx][c];
+  }
+}
+
+}  // namespace
+
+hipError_t transpose_u16(hipStream_t s, const uint16_t* src, long rows, long cols, uint16_t* dst) {
+  if (rows <= 0 || cols <= 0) return hipSuccess;
+  if (cdiv(rows, 64) > 65535 || cdiv(cols, 64) > INT32_MAX) return hipErrorInvalidValue;
+  launch(transpose_u16_kernel, dim3((unsigned)cdiv(cols, 64), (unsigned)cdiv(rows, 64)),
+         dim3(256), 0, s, src, rows, cols, dst);
+  return hipGetLastError();
+}
+
 hipError_t copy_device(hipStream_t s, void* dst, const void* src, long bytes) {
   if (bytes <= 0) return hipSuccess;
   const uintptr_t a = reinterpret_cast<uintptr_t>(dst), b = reinterpret_cast<uintptr_t>(src);

@@ -39,6 +39,7 @@
 // in-bounds row; their results are never stored.
 #pragma once
 
+#include <type_traits>
 #include <utility>
 
 #include "common.hpp"
@@ -395,10 +396,61 @@ constexpr int kBufFloats = 32 * kBufPitch;
 
 __device__ __forceinline__ void lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// Epilogues that read global memory per 16-value row segment (a residual, a
+// tape) may define `Pre` with `pre16(row, col, M, N)`, which issues those
+// loads, and `row16p(..., const Pre&, ...)`, which consumes them: the driver
+// then issues the loads of up to kEpiAhead segments ahead of the one it
+// stores, so their latency overlaps instead of adding up segment by segment.
+template <class E, class = void>
+inline constexpr bool kHasPre16 = false;
+template <class E>
+inline constexpr bool kHasPre16<E, std::void_t<typename E::Pre>> = true;
+constexpr int kEpiAhead = 4;
+
 template <class Epi, int TM, int TN>
 __device__ __forceinline__ void epilogue_rows(Epi& epi, floatx16 (&acc)[TM][TN], float* buf,
                                               int row0, int col0, int lane, int M, int N) {
   const int rr = lane >> 1, cc = (lane & 1) * 16;
+  if constexpr (kHasPre16<Epi>) {
+    constexpr int S = TM * TN;
+    constexpr int P = S < kEpiAhead ? S : kEpiAhead;
+    typename Epi::Pre ring[P];
+    auto at = [&](int sidx, int& r, int& c) {
+      r = row0 + (sidx / TN) * 32 + rr;
+      c = col0 + (sidx % TN) * 32 + cc;
+    };
+#pragma unroll
+    for (int t = 0; t < P; ++t) {
+      int r, c;
+      at(t, r, c);
+      ring[t] = epi.pre16(r, c, M, N);
+    }
+#pragma unroll
+    for (int sidx = 0; sidx < S; ++sidx) {
+      const int i = sidx / TN, j = sidx % TN;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) buf[mfma32_row(r, lane) * kBufPitch + (lane & 31)] = acc[i][j][r];
+      lds_fence();
+      float v[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const floatx4 t = *reinterpret_cast<const floatx4*>(buf + rr * kBufPitch + cc + 4 * q);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[4 * q + e] = t[e];
+      }
+      lds_fence();
+      const int brow = row0 + i * 32, bcol = col0 + j * 32;
+      const typename Epi::Pre cur = ring[sidx % P];
+      if (sidx + P < S) {
+        int r, c;
+        at(sidx + P, r, c);
+        ring[sidx % P] = epi.pre16(r, c, M, N);
+      }
+      epi.row16p(brow + rr, bcol + cc, v, cur, lane, M, N, buf, brow, bcol);
+      lds_fence();
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll

@@ -69,6 +69,9 @@ struct Block {
   float* cx_k_res = nullptr;
   uint16_t* value = nullptr;
   float* value_res = nullptr;
+  // value^T [F][D], kept for the value input gradient of large products
+  // (fp16_dx_wants_w_t; else null), rebuilt after every update
+  uint16_t* value_t = nullptr;
 };
 
 }  // namespace
@@ -93,6 +96,7 @@ struct ullis_hip_heron {
   uint16_t *y16 = nullptr, *ln2_16 = nullptr, *shifted16 = nullptr;
   uint8_t* idx_rm = nullptr;
   uint16_t *key16 = nullptr, *relu2_16 = nullptr, *gk16 = nullptr;
+  uint16_t* value_t_all = nullptr;  // the blocks' value^T caches (Block::value_t)
   // fp16 copy of the (scaled) gradient at each layer boundary x_l, l = 0..L:
   // read by layer l's O backward and layer l-1's CMix backward
   uint16_t* gx16_b = nullptr;
@@ -490,6 +494,10 @@ int run_update_seg(ullis_hip_heron* h, hipStream_t s, int l, float lr) {
        "latent / scale steps");
   STEP(run_trans_jobs(s, h->trans_jobs + g.trans.j0, g.trans.n, g.trans.blocks, h->invalid),
        "bits_t");
+  // the value weight's transpose for the next step's input gradient (a
+  // refused step changed nothing, so transposing again is harmless)
+  if (l < (int)h->L && h->blocks[l].value_t)
+    STEP(transpose_u16(s, h->blocks[l].value, h->D, h->F, h->blocks[l].value_t), "value^T");
   return 0;
 }
 
@@ -577,6 +585,7 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
   const long pt_col = (long)h->nb_col * D, pt_ln = 2L * h->nb_ln * D;
   const long pt_mix = (long)h->nb_mix * D;
   const size_t head_ws = head_ce_workspace_bytes(R, D, V);
+  const long value_t_elems = fp16_dx_wants_w_t(R, F, D) ? F * D * L : 0;
 
   // one carving sequence, run once to size the allocation and once to place the buffers
   auto carve = [&](auto& cv) {
@@ -594,6 +603,8 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
     h->key16 = cv.template take<uint16_t>(nf * L);
     h->relu2_16 = cv.template take<uint16_t>(nf * L);
     h->gk16 = cv.template take<uint16_t>(nf);
+    // (a zero-length take would still return a pointer into the next buffer)
+    h->value_t_all = value_t_elems ? cv.template take<uint16_t>(value_t_elems) : nullptr;
     h->gx16_b = cv.template take<uint16_t>(nd * (L + 1));
     h->g_side = cv.template take<float>(nd);
     h->ln3_16 = cv.template take<uint16_t>(nd);
@@ -633,6 +644,8 @@ int ullis_hip_heron_create(ullis_hip_ctx* c, const ullis_heron_dims* dims, size_
   }
   Carver cv(h->act);
   carve(cv);
+  if (h->value_t_all)
+    for (long l = 0; l < L; ++l) h->blocks[l].value_t = h->value_t_all + l * F * D;
   if (int rc = build_update_jobs(h)) {
     ullis_hip_heron_destroy(h);
     return rc;
@@ -820,6 +833,7 @@ int ullis_hip_heron_refresh_derived(ullis_hip_heron* h) {
   for (auto& b : h->blocks) {
     STEP(transpose_bits(s, b.o.bits, b.o.out, b.o.in, b.o.bits_t), "o bits_t");
     STEP(transpose_bits(s, b.key.bits, b.key.out, b.key.in, b.key.bits_t), "key bits_t");
+    if (b.value_t) STEP(transpose_u16(s, b.value, h->D, h->F, b.value_t), "value^T");
   }
   return 0;
 }
@@ -1051,9 +1065,9 @@ int step_launches(ullis_hip_heron* h, const float* x_emb, const uint32_t* labels
                                h->gp_value + l * h->splits_value * D * F};
       const WeightGradArgs kdw{g16_only, gk16, sh, R, D, F, h->splits_key,
                                h->gp_key + l * h->splits_key * F * D};
-      PROBED(ULLIS_HIP_PROBE_VALUE_BACKWARD,
-             fp16_backward_pair(s, Fp16DxArgs{gx, R, F, D, b.value, nullptr, key, gk16}, vdw),
-             "value backward");
+      Fp16DxArgs vdx{gx, R, F, D, b.value, nullptr, key, gk16};
+      vdx.w_t = b.value_t;
+      PROBED(ULLIS_HIP_PROBE_VALUE_BACKWARD, fp16_backward_pair(s, vdx, vdw), "value backward");
       PROBED(ULLIS_HIP_PROBE_KEY_BACKWARD,
              packed_backward_pair(s,
                                   PackedDxArgs{g16_only, gk16, R, D, F, b.key.bits_t, b.key.scale,

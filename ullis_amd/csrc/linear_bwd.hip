@@ -90,6 +90,8 @@ hipError_t fp16_backward_input(hipStream_t s, GradIn gy32, long rows, long in, l
   });
 }
 
+bool fp16_dx_wants_w_t(long rows, long in, long out) { return lds::giant_ok(rows, in, out); }
+
 hipError_t fp16_weight_grad_partials(hipStream_t s, GradIn gy32, const uint16_t* x16, long rows,
                                      long in, long out, int splits, float* part) {
   return packed_weight_grad_partials(s, gy32, nullptr, x16, rows, in, out, splits, part);

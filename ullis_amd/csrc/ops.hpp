@@ -129,7 +129,13 @@ struct Fp16DxArgs {
   float* gx;
   const uint16_t* key16;
   uint16_t* gk16;
+  // Optional W^T [in][out]: both operands then stream k-contiguous (same
+  // results as with w: every output sums the same products in the same order).
+  const uint16_t* w_t = nullptr;
 };
+// Whether an input gradient of this shape is worth a W^T cache: large
+// products (at least 512 256x256 output tiles), where it measured faster.
+bool fp16_dx_wants_w_t(long rows, long in, long out);
 // Input and weight gradient of one layer in a single launch when both GEMMs
 // take the streamed-LDS kernels (the blocks of both share the CUs), else the
 // two launches of the functions above; same results either way.
@@ -239,6 +245,8 @@ hipError_t layer_norm_param_finish(hipStream_t s, const float* part, int nblk, l
 // ---------------------------------------------------------------- elementwise
 
 hipError_t fill_f32(hipStream_t s, float* p, long n, float v);
+// dst [cols][rows] = src [rows][cols]^T, 16-bit elements.
+hipError_t transpose_u16(hipStream_t s, const uint16_t* src, long rows, long cols, uint16_t* dst);
 // Device-to-device byte copy as a kernel on stream s.
 hipError_t copy_device(hipStream_t s, void* dst, const void* src, long bytes);
 hipError_t clipped_sgd(hipStream_t s, uint16_t* values, float* residual, const float* grad, long n,
