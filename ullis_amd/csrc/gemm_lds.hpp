@@ -616,6 +616,10 @@ __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const
                                               const OB& b, Epi& epi, int M, int N, int K,
                                               int k_split, const TileMap& map) {
   constexpr int NS = ring_ns<NS_CFG, OA, OB>();
+  // Eight-wave tiles (a 2 x 4 wave grid) gave non-finite outputs for a packed
+  // forward at 64x128 tiles in an in-step trial; until that is found, every
+  // product runs four waves.
+  static_assert(NW == 4, "only four-wave tiles are validated");
   constexpr int WGN = NW / 2;  // waves along N
   constexpr int WM = BM / 2, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
