@@ -80,6 +80,8 @@ struct OpMK {
   static_assert(kBytes % (NW * 1024) == 0, "a stage must be whole wave-loads for NW waves");
   static constexpr int kInst = kBytes / (NW * 1024);  // loads per wave per stage
   static constexpr int kExtra = 0;
+  static constexpr bool kPlain = true;  // fragments are plain LDS reads
+  static constexpr int kFragReads = 1;  // LDS read instructions per fragment
   static_assert(CPR == 4 || CPR == 8 || CPR == 16 || CPR == 32, "BK 32, 64, 128 or 256");
   // LDS serves 16 lanes of a ds_read_b128 per cycle from a 256-byte bank
   // window: 16 consecutive rows must land in 16 distinct 16-byte slots.
@@ -137,6 +139,8 @@ struct OpKM {
   static_assert(kBytes % (NW * 1024) == 0, "a stage must be whole wave-loads for NW waves");
   static constexpr int kInst = kBytes / (NW * 1024);
   static constexpr int kExtra = 0;
+  static constexpr bool kPlain = true;
+  static constexpr int kFragReads = 2;
   __device__ static int swz(int k) { return 2 * (k & 3); }
   __device__ void prepare(char*, int, int) const {}
   __device__ __forceinline__ void issue(char* stage, int row0, int k0, int wave, int lane) const {
@@ -313,6 +317,8 @@ struct OpBitsX {
   static constexpr int kBytes = kWordBytes + ROWS * BK * 2;
   static constexpr int kExtra = 0;
   static constexpr bool kExpand = true;
+  static constexpr bool kPlain = true;
+  static constexpr int kFragReads = 1;
   static_assert(CPR == 4 || CPR == 8 || CPR == 16 || CPR == 32, "BK 32, 64, 128 or 256");
   __device__ static int swz(int row) { return OpMK<ROWS, BK, NW>::swz(row); }
   __device__ void prepare(char*, int, int) const {}
@@ -326,12 +332,14 @@ struct OpBitsX {
     }
   }
   // Word id (row id / WPR, k 32 (id % WPR) .. +31) -> four 16-byte chunks of
-  // the tile; bit j (LSB first) is +1 when set, -1 when clear.
-  __device__ __forceinline__ void expand(char* stage) const {
+  // the tile; bit j (LSB first) is +1 when set, -1 when clear. Each thread
+  // expands the words its own loads brought in (issue()'s ids), so once its
+  // own loads have landed it needs no barrier before expanding.
+  __device__ __forceinline__ void expand(char* stage, int wave, int lane) const {
     char* tile = stage + kWordBytes;
 #pragma unroll
-    for (int t = 0; t < kWords / (NW * 64); ++t) {
-      const int id = t * NW * 64 + (int)threadIdx.x;
+    for (int t = 0; t < kInst; ++t) {
+      const int id = (wave * kInst + t) * 64 + lane;
       const uint32_t word = reinterpret_cast<const uint32_t*>(stage)[id];
       const int row = id / WPR, w = id % WPR;
 #pragma unroll
@@ -369,6 +377,26 @@ template <class O, class = void>
 inline constexpr bool kExpands = false;
 template <class O>
 inline constexpr bool kExpands<O, std::enable_if_t<O::kExpand>> = true;
+
+// Operands whose fragments are plain LDS reads (no sign table, no per-k
+// scales): the interleaved K loop takes these.
+template <class O, class = void>
+inline constexpr bool kPlainFrag = false;
+template <class O>
+inline constexpr bool kPlainFrag<O, std::enable_if_t<O::kPlain>> = true;
+
+// s_waitcnt vmcnt(IPS * later), no barrier, for a runtime `later` in [0, S].
+template <int IPS, int S>
+__device__ __forceinline__ void wait_vm_stages(int later) {
+  if constexpr (S == 0) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  } else {
+    if (later >= S)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(IPS * S) : "memory");
+    else
+      wait_vm_stages<IPS, S - 1>(later);
+  }
+}
 
 // wait_barrier<IPS * later>() for a runtime `later` in [0, S] (the K-loop tail).
 template <int IPS, int S>
@@ -609,6 +637,139 @@ constexpr int lds_smem_bytes() {
   return lds_ring_bytes<BM, BN, BK, NS, OA, OB, NW>() + OA::kExtra + OB::kExtra;
 }
 
+// Tiles with at least this many MFMAs per wave per 16-deep step and plain
+// fragment operands take the interleaved K loop.
+constexpr int kInterleaveMfmas = 8;
+template <int BM, int BN, int BK, class OA, class OB, int NW>
+inline constexpr bool kInterleaved = kPlainFrag<OA> && kPlainFrag<OB> && BK >= 32 &&
+                                     (BM / 64) * (BN / (NW * 16)) >= kInterleaveMfmas;
+
+// The interleaved K loop for large tiles. A wave's MFMAs of one 16-deep step
+// are issued with the LDS fragment reads of the next step between them, so the
+// reads complete while the MFMA pipe is busy instead of before it starts. Each
+// stage has one barrier, before its last step: by then every wave has read the
+// whole stage (its buffer is refilled with stage kt + NS right after) and has
+// waited for stage kt + 1 to land (and expanded it, for sign-bit operands), so
+// the last step's MFMAs overlap the first reads of the next stage. Every
+// output sums the same products in the same k order as gemm_lds_body's loop.
+template <int BM, int BN, int BK, int NS_CFG, class OA, class OB, class Epi, int NW>
+__device__ __forceinline__ void gemm_lds_body_il(char* smem, int bid, int kz, const OA& a,
+                                                 const OB& b, Epi& epi, int M, int N, int K,
+                                                 int k_split, const TileMap& map) {
+  constexpr int NS = ring_ns<NS_CFG, OA, OB>();
+  constexpr int WGN = NW / 2;
+  constexpr int WM = BM / 2, WN = BN / WGN;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int STAGE = OA::kBytes + OB::kBytes;
+  constexpr int IPS = OA::kInst + OB::kInst;
+  constexpr int S = BK / 16;
+  static_assert(S >= 2 && S % 2 == 0, "an even number of 16-deep steps per stage");
+  static_assert(NS >= 2 && IPS * (NS - 1) < 64, "pipeline depth");
+  constexpr int RING = lds_ring_bytes<BM, BN, BK, NS_CFG, OA, OB, NW>();
+  char* extra_a = smem + RING;
+  char* extra_b = extra_a + OA::kExtra;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int tiles_n = (N + BN - 1) / BN;
+  int tm, tn;
+  tile_of_block_map(bid, tiles_n, map, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int kbeg = kz * k_split;
+  const int kend = min(K, kbeg + k_split);
+  const int nk = kend > kbeg ? (kend - kbeg) / BK : 0;
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = (floatx16){};
+
+  a.prepare(extra_a, kbeg, kend);
+  b.prepare(extra_b, kbeg, kend);
+  auto stage_at = [&](int kt) { return smem + (kt % NS) * STAGE; };
+  // Loads of stage `kt` into its ring buffer; stages past the last reload the
+  // last one (in bounds, never read), so every wave issues the same loads in
+  // every iteration and each wait below is one fixed vmcnt, with no branch
+  // to split the interleaved instruction stream.
+  auto issue = [&](int kt) {
+    char* st = stage_at(kt);
+    const int k0 = kbeg + min(kt, nk - 1) * BK;
+    a.issue(st, m0, k0, wave, lane);
+    b.issue(st + OA::kBytes, n0, k0, wave, lane);
+  };
+  auto expand = [&](int kt) {
+    if constexpr (kExpands<OA>) a.expand(stage_at(kt), wave, lane);
+    if constexpr (kExpands<OB>) b.expand(stage_at(kt) + OA::kBytes, wave, lane);
+  };
+  half8 fa[2][TM], fb[2][TN];
+  auto read = [&](int kt, int s, half8(&af)[TM], half8(&bf)[TN]) {
+    const char* st = stage_at(kt);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) af[i] = a.frag(st, extra_a, wm * WM + i * 32, 16 * s, lane, 0);
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      bf[j] = b.frag(st + OA::kBytes, extra_b, wn * WN + j * 32, 16 * s, lane, 0);
+  };
+  auto mma = [&](const half8(&af)[TM], const half8(&bf)[TN]) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+  };
+  // Issue order inside a step: MFMAs in pairs, one fragment read (and, in
+  // the last step of a stage, one operand load) after each pair.
+  constexpr int kReads = TM * OA::kFragReads + TN * OB::kFragReads;
+  auto interleave = [&](bool loads) {
+    constexpr int P = TM * TN / 2;
+    constexpr int Q = P > kReads ? (P > IPS ? P : IPS) : (kReads > IPS ? kReads : IPS);
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      if (q < P) __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);            // MFMA
+      if (q < kReads) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);       // LDS read
+      if (loads && q < IPS) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+    }
+  };
+
+  if (nk > 0) {
+    // prologue: fill the whole ring, wait for stage 0, read its first step
+#pragma unroll
+    for (int s = 0; s < NS; ++s) issue(s);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(IPS * (NS - 1)) : "memory");
+    expand(0);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    read(0, 0, fa[0], fb[0]);
+  }
+  for (int kt = 0; kt < nk; ++kt) {
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s) {
+      __builtin_amdgcn_sched_barrier(0);
+      mma(fa[s & 1], fb[s & 1]);
+      read(kt, s + 1, fa[(s + 1) & 1], fb[(s + 1) & 1]);
+      interleave(false);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // this wave's reads of stage kt are complete (lgkmcnt); stage kt + 1 has
+    // landed (vmcnt): expand it, then the barrier frees buffer kt for stage
+    // kt + NS
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(IPS * (NS - 2)) : "memory");
+    expand(kt + 1);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    issue(kt + NS);
+    mma(fa[(S - 1) & 1], fb[(S - 1) & 1]);
+    read(kt + 1, 0, fa[0], fb[0]);  // past the last stage: a stale buffer, never used
+    interleave(true);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  wait_barrier<0>();  // every wave is done reading the ring
+  if constexpr (kHasSplit<Epi>) epi.set_split(kz);
+  epilogue_rows(epi, acc, reinterpret_cast<float*>(smem) + wave * kBufFloats, m0 + wm * WM,
+                n0 + wn * WN, lane, M, N);
+}
+
 // One output tile (bid: tile index, kz: K split) of C = A . B^T in the block's
 // LDS (smem: lds_smem_bytes, 1024-byte aligned).
 template <int BM, int BN, int BK, int NS_CFG, class OA, class OB, class Epi, int NW = 4>
@@ -620,6 +781,11 @@ __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const
   // forward at 64x128 tiles in an in-step trial; until that is found, every
   // product runs four waves.
   static_assert(NW == 4, "only four-wave tiles are validated");
+  if constexpr (kInterleaved<BM, BN, BK, OA, OB, NW>) {
+    gemm_lds_body_il<BM, BN, BK, NS_CFG, OA, OB, Epi, NW>(smem, bid, kz, a, b, epi, M, N, K,
+                                                          k_split, map);
+    return;
+  }
   constexpr int WGN = NW / 2;  // waves along N
   constexpr int WM = BM / 2, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
@@ -667,8 +833,8 @@ __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const
     if constexpr (kExpands<OA> || kExpands<OB>) {
       // the stage's words have landed for every wave: expand them, then
       // barrier again (LDS writes only; the loads in flight stay in flight)
-      if constexpr (kExpands<OA>) a.expand(smem + (kt % NS) * STAGE);
-      if constexpr (kExpands<OB>) b.expand(smem + (kt % NS) * STAGE + OA::kBytes);
+      if constexpr (kExpands<OA>) a.expand(smem + (kt % NS) * STAGE, wave, lane);
+      if constexpr (kExpands<OB>) b.expand(smem + (kt % NS) * STAGE + OA::kBytes, wave, lane);
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
     const char* st = smem + (kt % NS) * STAGE;
@@ -863,6 +1029,13 @@ struct LdsHuge {
 };
 struct LdsGiant {
   static constexpr int bm = 256, bn = 256, bk = 32, ns = 4, nw = 4;
+};
+// 256x256 tiles over sign bits expanded in LDS: BK 64 halves the expansion
+// barriers and makes every row's stage segment a whole 128-byte line (config-5
+// key forward 400 -> 377 us; the fp16 forward measured 310 -> 318-328 us
+// with it, so it keeps LdsGiant).
+struct LdsGiantBits {
+  static constexpr int bm = 256, bn = 256, bk = 64, ns = 2, nw = 4;
 };
 
 constexpr long kBigAutoBlocks = 512;

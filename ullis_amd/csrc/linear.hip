@@ -104,10 +104,14 @@ hipError_t packed_forward(hipStream_t s, const void* x, int x_dtype, long rows, 
     // very large products: 256x256 tiles over sign bits expanded once per
     // stage in LDS
     if (x_dtype == kF16 && lds::mk_ok(x, in) && lds::giant_ok(rows, out, in)) {
-      lds::OpMK<lds::LdsGiant::bm, lds::LdsGiant::bk> a{static_cast<const half_t*>(x), in,
-                                                        (int)rows};
-      lds::OpBitsX<lds::LdsGiant::bn, lds::LdsGiant::bk> b{bits, in / 32, (int)out};
-      return lds::launch_lds<lds::LdsGiant>(s, a, b, epi, rows, out, in, 1);
+      auto giant = [&](auto t) {
+        using T = decltype(t);
+        lds::OpMK<T::bm, T::bk> a{static_cast<const half_t*>(x), in, (int)rows};
+        lds::OpBitsX<T::bn, T::bk> b{bits, in / 32, (int)out};
+        return lds::launch_lds<T>(s, a, b, epi, rows, out, in, 1);
+      };
+      if (in % lds::LdsGiantBits::bk == 0) return giant(lds::LdsGiantBits{});
+      return giant(lds::LdsGiant{});
     }
     if (x_dtype == kF16 && lds::mk_ok(x, in) &&
         lds::with_lds(rows, out, in, 1, &err, [&](auto t) {
