@@ -116,6 +116,34 @@ def test_binary_linear_backward_parity(rt, rows, in_f, out_f):
         assert rel(g[k], w[k]) <= REL, k
 
 
+# Weight gradients over >= 16384 rows whose [out, in] tiles by 256 run on
+# 256x256 tiles split over the rows (context.hpp dw_giant). The scalar oracle
+# is too slow at these sizes, so the reference is the closed form in float64 on
+# the same inputs, G = gy^T . x: the fp16 weight gradient is G
+# (src/metal.rs:2829-2908); the packed one is scale[o] * G, with g_scale[o] =
+# sum_i sign(o, i) G(o, i), g_bias = column sums of gy and gx = gy . (scale *
+# sign) (the oracle's ucr_packed_backward_ste, src/model.rs:745-796).
+@pytest.mark.parametrize("rows,in_f,out_f", [(16384, 1024, 1024), (16384, 256, 4096)])
+def test_weight_gradients_over_many_rows(rt, rows, in_f, out_f):
+    rng = np.random.default_rng(rows + in_f + 3 * out_f)
+    x16, bits, scale, _ = rand_case(rng, rows, in_f, out_f)
+    gy = rng.normal(0, 1e-2, rows * out_f).astype(np.float32)
+    x64 = h2f32(x16).reshape(rows, in_f).astype(np.float64)
+    gy64 = gy.reshape(rows, out_f).astype(np.float64)
+    G = gy64.T @ x64
+    w = f16(rng.normal(0, 0.02, out_f * in_f))
+    _, gw = rt.fp16_linear_backward(x16, gy, w, rows, in_f, out_f)
+    assert rel(gw, G.ravel()) <= REL
+    sc = h2f32(scale).astype(np.float64)
+    lat = np.unpackbits(np.asarray(bits, np.uint32).view(np.uint8), bitorder="little")
+    sign = np.where(lat[: out_f * in_f].reshape(out_f, in_f) != 0, 1.0, -1.0)
+    g = rt.binary_linear_backward(x16, gy, bits, scale, True, rows, in_f, out_f)
+    assert rel(g["weight_gradient"], (sc[:, None] * G).ravel()) <= REL
+    assert rel(g["scale_gradient"], (sign * G).sum(axis=1)) <= REL
+    assert rel(g["bias_gradient"], gy64.sum(axis=0)) <= REL
+    assert rel(g["input_gradient"], (gy64 @ (sc[:, None] * sign)).ravel()) <= REL
+
+
 def finite_rel_and_masks(a, r, name):
     """Non-finite entries must sit where the oracle's are (NaN where NaN, +-Inf
     where +-Inf); the finite ones within REL of the finite reference."""
