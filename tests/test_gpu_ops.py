@@ -117,13 +117,16 @@ def test_binary_linear_backward_parity(rt, rows, in_f, out_f):
 
 
 # Weight gradients over >= 16384 rows whose [out, in] tiles by 256 run on
-# 256x256 tiles split over the rows (context.hpp dw_giant). The scalar oracle
+# 256x256 tiles split over the rows (context.hpp dw_giant), and packed input
+# gradients with 512 or more 256x256 output tiles on 256x256 tiles over the
+# scaled sign bits expanded in LDS (32768 rows here). The scalar oracle
 # is too slow at these sizes, so the reference is the closed form in float64 on
 # the same inputs, G = gy^T . x: the fp16 weight gradient is G
 # (src/metal.rs:2829-2908); the packed one is scale[o] * G, with g_scale[o] =
 # sum_i sign(o, i) G(o, i), g_bias = column sums of gy and gx = gy . (scale *
 # sign) (the oracle's ucr_packed_backward_ste, src/model.rs:745-796).
-@pytest.mark.parametrize("rows,in_f,out_f", [(16384, 1024, 1024), (16384, 256, 4096)])
+@pytest.mark.parametrize("rows,in_f,out_f",
+                         [(16384, 1024, 1024), (16384, 256, 4096), (32768, 1024, 1024)])
 def test_weight_gradients_over_many_rows(rt, rows, in_f, out_f):
     rng = np.random.default_rng(rows + in_f + 3 * out_f)
     x16, bits, scale, _ = rand_case(rng, rows, in_f, out_f)

@@ -295,17 +295,21 @@ struct OpBits {
   }
 };
 
-// Packed sign bits [row][k/32] expanded once per stage into an fp16 +-1 tile
-// in LDS (unscaled only). The raw words stream in as for OpBits; after the
-// stage has landed, the block's threads each expand whole words into the
-// stage's fp16 tile (laid out and swizzled as OpMK's), and the fragments are
-// then plain ds_read_b128 reads. One expansion serves every wave that reads
-// the tile, which pays for 256-row tiles (four waves share each column).
-template <int ROWS, int BK, int NW = 4>
+// Packed sign bits [row][k/32] expanded once per stage into an fp16 tile in
+// LDS: +-1, or with SCALED +-scale[kofs + k] (the input gradient's operand;
+// the block's scale range is staged in LDS by prepare(), as for OpBits). The
+// raw words stream in as for OpBits; after the stage has landed, each thread
+// expands the words its own loads brought in into the stage's fp16 tile (laid
+// out and swizzled as OpMK's), and the fragments are then plain ds_read_b128
+// reads. One expansion serves every wave that reads the tile, which pays for
+// 256-row tiles (four waves share each column).
+template <int ROWS, int BK, int NW = 4, bool SCALED = false>
 struct OpBitsX {
   const uint32_t* p;
   long ldw;  // words between rows
   int rows;
+  const uint16_t* scale = nullptr;  // SCALED only, indexed by kofs + k
+  int kofs = 0;                     // k offset into the rows (multiple of 32)
   static constexpr int WPR = BK / 32;  // words per row per stage
   static constexpr int kWords = ROWS * WPR;
   // one word per lane per load
@@ -315,27 +319,35 @@ struct OpBitsX {
   static constexpr int kWordBytes = ((kWords * 4 + 1023) / 1024) * 1024;
   static constexpr int CPR = BK / 8;  // 16-byte chunks per tile row
   static constexpr int kBytes = kWordBytes + ROWS * BK * 2;
-  static constexpr int kExtra = 0;
+  static constexpr int kMaxScaleK = 8192;
+  static constexpr int kExtra = SCALED ? kMaxScaleK * 2 : 0;
   static constexpr bool kExpand = true;
   static constexpr bool kPlain = true;
   static constexpr int kFragReads = 1;
   static_assert(CPR == 4 || CPR == 8 || CPR == 16 || CPR == 32, "BK 32, 64, 128 or 256");
   __device__ static int swz(int row) { return OpMK<ROWS, BK, NW>::swz(row); }
-  __device__ void prepare(char*, int, int) const {}
+  __device__ void prepare(char* extra, int kbeg, int kend) const {
+    if constexpr (SCALED) {
+      uint16_t* sc = reinterpret_cast<uint16_t*>(extra);
+      for (int k = kbeg + (int)threadIdx.x; k < kend; k += NW * 64) sc[k - kbeg] = scale[kofs + k];
+    }
+  }
   __device__ __forceinline__ void issue(char* stage, int row0, int k0, int wave, int lane) const {
 #pragma unroll
     for (int t = 0; t < kInst; ++t) {
       const int id = (wave * kInst + t) * 64 + lane;
       const int row = id / WPR, w = id % WPR;
       const int r = min(row0 + row, rows - 1);
-      dma4(p + (long)r * ldw + (k0 >> 5) + w, stage + (wave * kInst + t) * 256);
+      dma4(p + (long)r * ldw + ((kofs + k0) >> 5) + w, stage + (wave * kInst + t) * 256);
     }
   }
   // Word id (row id / WPR, k 32 (id % WPR) .. +31) -> four 16-byte chunks of
-  // the tile; bit j (LSB first) is +1 when set, -1 when clear. Each thread
-  // expands the words its own loads brought in (issue()'s ids), so once its
-  // own loads have landed it needs no barrier before expanding.
-  __device__ __forceinline__ void expand(char* stage, int wave, int lane) const {
+  // the tile; bit j (LSB first) is +1 (+scale) when set, -1 (-scale) when
+  // clear. Each thread expands the words its own loads brought in (issue()'s
+  // ids), so once its own loads have landed it needs no barrier before
+  // expanding. k0rel: the stage's first k relative to the block's first.
+  __device__ __forceinline__ void expand(char* stage, const char* extra, int k0rel, int wave,
+                                         int lane) const {
     char* tile = stage + kWordBytes;
 #pragma unroll
     for (int t = 0; t < kInst; ++t) {
@@ -346,10 +358,20 @@ struct OpBitsX {
       for (int q = 0; q < 4; ++q) {
         const uint32_t byte = word >> (8 * q);
         u32x4 o;
+        if constexpr (SCALED) {
+          // the sign bit of each half flips where the weight bit is clear
+          const u32x4 sc =
+              *reinterpret_cast<const u32x4*>(extra + 2 * (k0rel + 32 * w + 8 * q));
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
-          o[m] = 0xBC00BC00u ^ (((byte >> (2 * m)) & 1u) << 15) ^
-                 (((byte >> (2 * m + 1)) & 1u) << 31);
+          for (int m = 0; m < 4; ++m)
+            o[m] = sc[m] ^ ((((~byte) >> (2 * m)) & 1u) << 15) ^
+                   ((((~byte) >> (2 * m + 1)) & 1u) << 31);
+        } else {
+#pragma unroll
+          for (int m = 0; m < 4; ++m)
+            o[m] = 0xBC00BC00u ^ (((byte >> (2 * m)) & 1u) << 15) ^
+                   (((byte >> (2 * m + 1)) & 1u) << 31);
+        }
         const int c = 4 * w + q;
         *reinterpret_cast<u32x4*>(tile + row * (BK * 2) + 16 * (c ^ swz(row))) = o;
       }
@@ -688,6 +710,9 @@ __device__ __forceinline__ void gemm_lds_body_il(char* smem, int bid, int kz, co
 
   a.prepare(extra_a, kbeg, kend);
   b.prepare(extra_b, kbeg, kend);
+  // staged tables (scales) are read by other threads' expansions
+  if constexpr (OA::kExtra > 0 || OB::kExtra > 0)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   auto stage_at = [&](int kt) { return smem + (kt % NS) * STAGE; };
   // Loads of stage `kt` into its ring buffer; stages past the last reload the
   // last one (in bounds, never read), so every wave issues the same loads in
@@ -700,8 +725,9 @@ __device__ __forceinline__ void gemm_lds_body_il(char* smem, int bid, int kz, co
     b.issue(st + OA::kBytes, n0, k0, wave, lane);
   };
   auto expand = [&](int kt) {
-    if constexpr (kExpands<OA>) a.expand(stage_at(kt), wave, lane);
-    if constexpr (kExpands<OB>) b.expand(stage_at(kt) + OA::kBytes, wave, lane);
+    const int k0rel = min(kt, nk - 1) * BK;  // the stage issue() loaded
+    if constexpr (kExpands<OA>) a.expand(stage_at(kt), extra_a, k0rel, wave, lane);
+    if constexpr (kExpands<OB>) b.expand(stage_at(kt) + OA::kBytes, extra_b, k0rel, wave, lane);
   };
   half8 fa[2][TM], fb[2][TN];
   auto read = [&](int kt, int s, half8(&af)[TM], half8(&bf)[TN]) {
@@ -833,8 +859,9 @@ __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const
     if constexpr (kExpands<OA> || kExpands<OB>) {
       // the stage's words have landed for every wave: expand them, then
       // barrier again (LDS writes only; the loads in flight stay in flight)
-      if constexpr (kExpands<OA>) a.expand(smem + (kt % NS) * STAGE, wave, lane);
-      if constexpr (kExpands<OB>) b.expand(smem + (kt % NS) * STAGE + OA::kBytes, wave, lane);
+      if constexpr (kExpands<OA>) a.expand(smem + (kt % NS) * STAGE, extra_a, kt * BK, wave, lane);
+      if constexpr (kExpands<OB>)
+        b.expand(smem + (kt % NS) * STAGE + OA::kBytes, extra_b, kt * BK, wave, lane);
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
     const char* st = smem + (kt % NS) * STAGE;

@@ -413,6 +413,20 @@ bool packed_dx_lds(const PackedDxArgs& d, hipError_t* err, F&& f) {
   // the scaled-bits operand keeps the scales of the block's k range in LDS
   if (!lds::mk_ok(g16, ldgy) || d.out > 8192 || ldb % 32 != 0 || d.kofs % 32 != 0) return false;
   EpiStoreF32 epi{d.gx, d.gy32.amax, d.out_mul, d.accumulate};
+  // very large products: 256x256 tiles over the scaled sign bits expanded in
+  // LDS, on the interleaved K loop
+  if (lds::giant_ok(d.rows, d.in, d.out) && d.out % lds::LdsGiantBits::bk == 0) {
+    using T = lds::LdsGiantBits;
+    lds::OpMK<T::bm, T::bk> a{reinterpret_cast<const half_t*>(g16), ldgy, (int)d.rows};
+    lds::OpBitsX<T::bn, T::bk, T::nw, true> b{d.bits_t, ldb / 32, (int)d.in, d.scale,
+                                              (int)d.kofs};
+    if (d.col_part)
+      *err = f(lds::lds_problem<T>(a, b, EpiSignedColSum{d.gy32.amax, d.sign_idx, d.col_part},
+                                   d.rows, d.in, d.out, 1));
+    else
+      *err = f(lds::lds_problem<T>(a, b, epi, d.rows, d.in, d.out, 1));
+    return true;
+  }
   return lds::with_lds(d.rows, d.in, d.out, 1, err, [&](auto t) {
     using T = decltype(t);
     lds::OpMK<T::bm, T::bk> a{reinterpret_cast<const half_t*>(g16), ldgy, (int)d.rows};
