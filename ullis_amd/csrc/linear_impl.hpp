@@ -465,8 +465,7 @@ bool fp16_dx_lds(const Fp16DxArgs& d, hipError_t* err, F&& f) {
   // or W^T[i*out + o] k-contiguous when given. With W^T, 128x256 tiles of two
   // k-contiguous operands on the interleaved K loop: at config 5 the value
   // backward pair took 1046 us against 1136 us on 128x128 tiles and 1389 us
-  // with the transposed operand (256x256 tiles, whose ReLU^2 epilogue idles
-  // the MFMAs twice as long per tile: 1752 us).
+  // with the transposed operand (256x256 tiles: 1752 us).
   if (d.w_t && lds::mk_ok(d.gy32.p16, d.out) && lds::mk_ok(d.w_t, d.out) &&
       d.out % lds::LdsHuge::bk == 0 && d.rows % lds::LdsHuge::bm == 0 &&
       d.in % lds::LdsHuge::bn == 0) {
