@@ -463,7 +463,7 @@ VENDOR_SHAPES = [
 ]
 
 
-def vendor_gemm() -> None:
+def vendor_gemm(shapes=None) -> None:
     """One JSON line per heron GEMM shape: the vendor fp16 GEMM (torch.matmul,
     hipBLASLt) on dense fp16 operands, 20 (4 at config 5) launches captured in a
     graph and replayed 20 times between events, so host launch cost is out of
@@ -472,7 +472,7 @@ def vendor_gemm() -> None:
     import torch
 
     dev = torch.device("cuda:0")
-    for m, n, k, name in VENDOR_SHAPES:
+    for m, n, k, name in shapes or VENDOR_SHAPES:
         a = torch.randn(m, k, device=dev, dtype=torch.float16)
         b = torch.randn(k, n, device=dev, dtype=torch.float16)
         c = torch.empty(m, n, device=dev, dtype=torch.float16)
@@ -500,6 +500,60 @@ def vendor_gemm() -> None:
         print(json.dumps({"vendor_gemm": name, "shape_MNK": [m, n, k], "us": round(us, 2),
                           "tflops": round(tf, 1), "frac": round(tf / FP16_PEAK_TFLOPS, 4)}),
               flush=True)
+
+
+# The library's large forward products, alone, at the shapes the vendor line
+# above times for config 5 (rows, in, out, kind).
+PRODUCT_SHAPES = [(32768, 1024, 4096, "packed", "config-5 key fwd"),
+                  (32768, 4096, 1024, "fp16", "config-5 value fwd")]
+
+
+def product_gemm(rt, reps: int = 10, with_vendor: bool = True) -> None:
+    """One JSON line per config-5 forward product of the library alone
+    (ullis_hip_binary_linear / ullis_hip_fp16_linear, fp16 output, no epilogue
+    beyond the row scale), `reps` calls between events on the library's stream;
+    then (with_vendor) the vendor fp16 GEMM at the same shapes, so that one
+    process holds both for `rocprofv3 --pmc` passes."""
+    import ctypes as C
+
+    from ullis_amd.synth import f16, pack_bits
+
+    lib, ctx = rt.lib, rt.ctx
+    rng = np.random.default_rng(0)
+    for rows, k, n, kind, name in PRODUCT_SHAPES:
+        x = rt.put(f16(rng.standard_normal(rows * k)))
+        y = rt.buffer(2 * rows * n)
+        if kind == "packed":
+            bits = rt.put(pack_bits(rng.integers(0, 2, n * k).astype(bool)))
+            sc = rt.put(f16(np.full(n, 0.01)))
+
+            def call():
+                rt._check(lib.ullis_hip_binary_linear(ctx, x.ptr, 1, bits.ptr, sc.ptr, None, rows,
+                                                      k, n, None, y.ptr), "binary_linear")
+        else:
+            w = rt.put(f16(rng.standard_normal(n * k) * 0.02))
+
+            def call():
+                rt._check(lib.ullis_hip_fp16_linear(ctx, x.ptr, 1, w.ptr, rows, k, n, None, y.ptr),
+                          "fp16_linear")
+        for _ in range(3):
+            call()
+        rt.sync()
+        rt._check(lib.ullis_hip_event_record(ctx, 0), "event")
+        for _ in range(reps):
+            call()
+        rt._check(lib.ullis_hip_event_record(ctx, 1), "event")
+        rt.sync()
+        ms = C.c_float()
+        rt._check(lib.ullis_hip_event_elapsed_ms(ctx, 0, 1, C.byref(ms)), "elapsed")
+        us = ms.value * 1e3 / reps
+        tf = 2.0 * rows * k * n / (us * 1e-6) / 1e12
+        print(json.dumps({"product_gemm": name, "kind": kind, "shape_MNK": [rows, n, k],
+                          "us": round(us, 2), "tflops": round(tf, 1),
+                          "frac": round(tf / FP16_PEAK_TFLOPS, 4)}), flush=True)
+        del x, y
+    if with_vendor:
+        vendor_gemm([s for s in VENDOR_SHAPES if s[0] >= 32768])
 
 
 def copy_calibration(rt, mib: int) -> None:
@@ -550,6 +604,9 @@ def main() -> int:
     ap.add_argument("--vendor-gemm", action="store_true",
                     help="instead of the bench line, time the vendor fp16 GEMM (torch.matmul) at "
                          "the heron GEMM shapes, as a yardstick")
+    ap.add_argument("--product-gemm", type=int, default=0, metavar="REPS",
+                    help="instead of the bench line, time the library's config-5 forward products "
+                         "alone (REPS calls each), then the vendor GEMM at the same shapes")
     ap.add_argument("--graph", type=int, default=None,
                     help="1: replay each step's launches from a captured HIP graph (default 0; "
                          "with --decode-step, default 1)")
@@ -569,7 +626,7 @@ def main() -> int:
               "run with --gpus 1", file=sys.stderr)
         return 2
     plain = (args.decode_gemv == 0 and not args.stress and args.ln_isolated == 0 and
-             not args.rosa_live and not args.decode_step)
+             not args.rosa_live and not args.decode_step and args.product_gemm == 0)
     # the CPU baseline's child processes start before this process touches the GPU
     baseline = (cpu_baseline(args.cpu_rows, max(1, args.cpu_runs))
                 if plain and args.cpu_rows > 0 else None)
@@ -579,9 +636,17 @@ def main() -> int:
 
     c = CONFIG
     shape = HeronShape(**c)
+    if args.product_gemm > 0:
+        # the vendor line needs torch's HIP runtime up before the library's
+        import torch
+
+        torch.cuda.init()
     rt = HipRuntime(0)
     if args.decode_gemv > 0:
         decode_gemv(rt, args.decode_gemv)
+        return 0
+    if args.product_gemm > 0:
+        product_gemm(rt, args.product_gemm)
         return 0
     if args.stress:
         stress_profile(rt, args.steps, args.warmup)
