@@ -82,6 +82,7 @@ struct OpMK {
   static constexpr int kExtra = 0;
   static constexpr bool kPlain = true;  // fragments are plain LDS reads
   static constexpr int kFragReads = 1;  // LDS read instructions per fragment
+  static constexpr int kNW = NW;        // the block's wave count issue() assumes
   static_assert(CPR == 4 || CPR == 8 || CPR == 16 || CPR == 32, "BK 32, 64, 128 or 256");
   // LDS serves 16 lanes of a ds_read_b128 per cycle from a 256-byte bank
   // window: 16 consecutive rows must land in 16 distinct 16-byte slots.
@@ -141,6 +142,7 @@ struct OpKM {
   static constexpr int kExtra = 0;
   static constexpr bool kPlain = true;
   static constexpr int kFragReads = 2;
+  static constexpr int kNW = NW;
   __device__ static int swz(int k) { return 2 * (k & 3); }
   __device__ void prepare(char*, int, int) const {}
   __device__ __forceinline__ void issue(char* stage, int row0, int k0, int wave, int lane) const {
@@ -200,6 +202,7 @@ struct OpBits {
   static constexpr int kWordsPerWave = kWords / NW;
   static constexpr int kBytes = ((kWords * 4 + 255) / 256) * 256;
   static constexpr int kMaxScaleK = 8192;
+  static constexpr int kNW = NW;
   // extra: 16-entry sign table (128 B), then the scale range when SCALED.
   static constexpr int kLut = 128;
   static constexpr int kExtra = kLut + (SCALED ? kMaxScaleK * 2 : 0);
@@ -324,6 +327,7 @@ struct OpBitsX {
   static constexpr bool kExpand = true;
   static constexpr bool kPlain = true;
   static constexpr int kFragReads = 1;
+  static constexpr int kNW = NW;
   static_assert(CPR == 4 || CPR == 8 || CPR == 16 || CPR == 32, "BK 32, 64, 128 or 256");
   __device__ static int swz(int row) { return OpMK<ROWS, BK, NW>::swz(row); }
   __device__ void prepare(char* extra, int kbeg, int kend) const {
@@ -679,6 +683,7 @@ __device__ __forceinline__ void gemm_lds_body_il(char* smem, int bid, int kz, co
                                                  const OB& b, Epi& epi, int M, int N, int K,
                                                  int k_split, const TileMap& map) {
   constexpr int NS = ring_ns<NS_CFG, OA, OB>();
+  static_assert(OA::kNW == NW && OB::kNW == NW, "operands built for another wave count");
   constexpr int WGN = NW / 2;
   constexpr int WM = BM / 2, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
@@ -807,6 +812,7 @@ __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const
   // forward at 64x128 tiles in an in-step trial; until that is found, every
   // product runs four waves.
   static_assert(NW == 4, "only four-wave tiles are validated");
+  static_assert(OA::kNW == NW && OB::kNW == NW, "operands built for another wave count");
   if constexpr (kInterleaved<BM, BN, BK, OA, OB, NW>) {
     gemm_lds_body_il<BM, BN, BK, NS_CFG, OA, OB, Epi, NW>(smem, bid, kz, a, b, epi, M, N, K,
                                                           k_split, map);

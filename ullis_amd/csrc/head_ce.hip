@@ -354,8 +354,8 @@ hipError_t logits_gemm(hipStream_t s, const uint16_t* hidden16, long rows, long 
   if (lds::mk_ok(hidden16, d) &&
       lds::with_lds(rows, ncols, d, 1, &err, [&](auto t) {
         using T = decltype(t);
-        lds::OpMK<T::bm, T::bk> a{reinterpret_cast<const half_t*>(hidden16), d, (int)rows};
-        lds::OpBits<T::bn, T::bk, false> b{bits_rows, d / 32, (int)ncols, nullptr, 0};
+        lds::OpMK<T::bm, T::bk, T::nw> a{reinterpret_cast<const half_t*>(hidden16), d, (int)rows};
+        lds::OpBits<T::bn, T::bk, false, T::nw> b{bits_rows, d / 32, (int)ncols, nullptr, 0};
         return lds::launch_lds<T>(s, a, b, epi, rows, ncols, d, 1);
       }, lds::LdsPolicy::kNoBig))
     return err;

@@ -106,8 +106,8 @@ hipError_t packed_forward(hipStream_t s, const void* x, int x_dtype, long rows, 
     if (x_dtype == kF16 && lds::mk_ok(x, in) && lds::giant_ok(rows, out, in)) {
       auto giant = [&](auto t) {
         using T = decltype(t);
-        lds::OpMK<T::bm, T::bk> a{static_cast<const half_t*>(x), in, (int)rows};
-        lds::OpBitsX<T::bn, T::bk> b{bits, in / 32, (int)out};
+        lds::OpMK<T::bm, T::bk, T::nw> a{static_cast<const half_t*>(x), in, (int)rows};
+        lds::OpBitsX<T::bn, T::bk, T::nw> b{bits, in / 32, (int)out};
         return lds::launch_lds<T>(s, a, b, epi, rows, out, in, 1);
       };
       if (in % lds::LdsGiantBits::bk == 0) return giant(lds::LdsGiantBits{});
@@ -116,8 +116,8 @@ hipError_t packed_forward(hipStream_t s, const void* x, int x_dtype, long rows, 
     if (x_dtype == kF16 && lds::mk_ok(x, in) &&
         lds::with_lds(rows, out, in, 1, &err, [&](auto t) {
           using T = decltype(t);
-          lds::OpMK<T::bm, T::bk> a{static_cast<const half_t*>(x), in, (int)rows};
-          lds::OpBits<T::bn, T::bk, false> b{bits, in / 32, (int)out, nullptr, 0};
+          lds::OpMK<T::bm, T::bk, T::nw> a{static_cast<const half_t*>(x), in, (int)rows};
+          lds::OpBits<T::bn, T::bk, false, T::nw> b{bits, in / 32, (int)out, nullptr, 0};
           return lds::launch_lds<T>(s, a, b, epi, rows, out, in, 1);
         }))
       return err;
@@ -154,8 +154,8 @@ hipError_t packed_forward_bits3(hipStream_t s, const uint16_t* const x[3], long 
   hipError_t err = hipSuccess;
   if (lds_ok && lds::with_lds(rows, out, in, 1, &err, [&](auto t) {
         using T = decltype(t);
-        lds::Group<lds::OpMK<T::bm, T::bk>, 3> a;
-        lds::Group<lds::OpBits<T::bn, T::bk, false>, 3> b;
+        lds::Group<lds::OpMK<T::bm, T::bk, T::nw>, 3> a;
+        lds::Group<lds::OpBits<T::bn, T::bk, false, T::nw>, 3> b;
         lds::Group<EpiPackedFwd<kOutBits>, 3> e;
         for (int j = 0; j < 3; ++j) {
           a.v[j] = {reinterpret_cast<const half_t*>(x[j]), in, (int)rows};
@@ -241,8 +241,8 @@ hipError_t fp16_forward(hipStream_t s, const void* x, int x_dtype, long rows, lo
   if (x_dtype == kF16 && lds::mk_ok(x, in) && lds::mk_ok(w, in) &&
       lds::with_lds(rows, out, in, 1, &err, [&](auto t) {
         using T = decltype(t);
-        lds::OpMK<T::bm, T::bk> a{static_cast<const half_t*>(x), in, (int)rows};
-        lds::OpMK<T::bn, T::bk> b{reinterpret_cast<const half_t*>(w), in, (int)out};
+        lds::OpMK<T::bm, T::bk, T::nw> a{static_cast<const half_t*>(x), in, (int)rows};
+        lds::OpMK<T::bn, T::bk, T::nw> b{reinterpret_cast<const half_t*>(w), in, (int)out};
         return lds::launch_lds<T>(s, a, b, epi, rows, out, in, 1);
         // one block per CU at heron sizes, reading an operand fresh from HBM:
         // the four-stage ring (measured 18.9 -> 15.2 us in the step)

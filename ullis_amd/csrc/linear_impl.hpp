@@ -417,7 +417,7 @@ bool packed_dx_lds(const PackedDxArgs& d, hipError_t* err, F&& f) {
   // LDS, on the interleaved K loop
   if (lds::giant_ok(d.rows, d.in, d.out) && d.out % lds::LdsGiantBits::bk == 0) {
     using T = lds::LdsGiantBits;
-    lds::OpMK<T::bm, T::bk> a{reinterpret_cast<const half_t*>(g16), ldgy, (int)d.rows};
+    lds::OpMK<T::bm, T::bk, T::nw> a{reinterpret_cast<const half_t*>(g16), ldgy, (int)d.rows};
     lds::OpBitsX<T::bn, T::bk, T::nw, true> b{d.bits_t, ldb / 32, (int)d.in, d.scale,
                                               (int)d.kofs};
     if (d.col_part)
@@ -429,8 +429,8 @@ bool packed_dx_lds(const PackedDxArgs& d, hipError_t* err, F&& f) {
   }
   return lds::with_lds(d.rows, d.in, d.out, 1, err, [&](auto t) {
     using T = decltype(t);
-    lds::OpMK<T::bm, T::bk> a{reinterpret_cast<const half_t*>(g16), ldgy, (int)d.rows};
-    lds::OpBits<T::bn, T::bk, true> b{d.bits_t, ldb / 32, (int)d.in, d.scale, (int)d.kofs};
+    lds::OpMK<T::bm, T::bk, T::nw> a{reinterpret_cast<const half_t*>(g16), ldgy, (int)d.rows};
+    lds::OpBits<T::bn, T::bk, true, T::nw> b{d.bits_t, ldb / 32, (int)d.in, d.scale, (int)d.kofs};
     if (d.col_part)
       return f(lds::lds_problem<T>(a, b, EpiSignedColSum{d.gy32.amax, d.sign_idx, d.col_part},
                                    d.rows, d.in, d.out, 1));
@@ -446,15 +446,15 @@ bool weight_grad_lds(const WeightGradArgs& d, hipError_t* err, F&& f) {
   EpiPartial epi{d.part};
   if (dw_giant(d.out, d.in, d.rows) && d.rows % (lds::LdsGiant::bk * d.splits) == 0) {
     using T = lds::LdsGiant;
-    lds::OpKM<T::bm, T::bk> a{reinterpret_cast<const half_t*>(g16), d.out, (int)d.out};
-    lds::OpKM<T::bn, T::bk> b{reinterpret_cast<const half_t*>(d.x16), d.in, (int)d.in};
+    lds::OpKM<T::bm, T::bk, T::nw> a{reinterpret_cast<const half_t*>(g16), d.out, (int)d.out};
+    lds::OpKM<T::bn, T::bk, T::nw> b{reinterpret_cast<const half_t*>(d.x16), d.in, (int)d.in};
     *err = f(lds::lds_problem<T>(a, b, epi, d.out, d.in, d.rows, d.splits));
     return true;
   }
   return lds::with_lds(d.out, d.in, d.rows, d.splits, err, [&](auto t) {
     using T = decltype(t);
-    lds::OpKM<T::bm, T::bk> a{reinterpret_cast<const half_t*>(g16), d.out, (int)d.out};
-    lds::OpKM<T::bn, T::bk> b{reinterpret_cast<const half_t*>(d.x16), d.in, (int)d.in};
+    lds::OpKM<T::bm, T::bk, T::nw> a{reinterpret_cast<const half_t*>(g16), d.out, (int)d.out};
+    lds::OpKM<T::bn, T::bk, T::nw> b{reinterpret_cast<const half_t*>(d.x16), d.in, (int)d.in};
     return f(lds::lds_problem<T>(a, b, epi, d.out, d.in, d.rows, d.splits));
   });
 }
@@ -470,8 +470,8 @@ bool fp16_dx_lds(const Fp16DxArgs& d, hipError_t* err, F&& f) {
       d.out % lds::LdsHuge::bk == 0 && d.rows % lds::LdsHuge::bm == 0 &&
       d.in % lds::LdsHuge::bn == 0) {
     using T = lds::LdsHuge;
-    lds::OpMK<T::bm, T::bk> a{reinterpret_cast<const half_t*>(d.gy32.p16), d.out, (int)d.rows};
-    lds::OpMK<T::bn, T::bk> b{reinterpret_cast<const half_t*>(d.w_t), d.out, (int)d.in};
+    lds::OpMK<T::bm, T::bk, T::nw> a{reinterpret_cast<const half_t*>(d.gy32.p16), d.out, (int)d.rows};
+    lds::OpMK<T::bn, T::bk, T::nw> b{reinterpret_cast<const half_t*>(d.w_t), d.out, (int)d.in};
     if (d.gk16)
       *err = f(lds::lds_problem<T>(a, b, EpiRelu2Bwd{d.key16, d.gk16}, d.rows, d.in, d.out, 1));
     else
@@ -482,8 +482,8 @@ bool fp16_dx_lds(const Fp16DxArgs& d, hipError_t* err, F&& f) {
   if (!lds::mk_ok(d.gy32.p16, d.out) || !lds::km_ok(d.w, d.in, d.in)) return false;
   return lds::with_lds(d.rows, d.in, d.out, 1, err, [&](auto t) {
     using T = decltype(t);
-    lds::OpMK<T::bm, T::bk> a{reinterpret_cast<const half_t*>(d.gy32.p16), d.out, (int)d.rows};
-    lds::OpKM<T::bn, T::bk> b{reinterpret_cast<const half_t*>(d.w), d.in, (int)d.in};
+    lds::OpMK<T::bm, T::bk, T::nw> a{reinterpret_cast<const half_t*>(d.gy32.p16), d.out, (int)d.rows};
+    lds::OpKM<T::bn, T::bk, T::nw> b{reinterpret_cast<const half_t*>(d.w), d.in, (int)d.in};
     if (d.gk16)
       return f(lds::lds_problem<T>(a, b, EpiRelu2Bwd{d.key16, d.gk16}, d.rows, d.in, d.out, 1));
     return f(lds::lds_problem<T>(a, b, EpiStoreF32{d.gx, d.gy32.amax, nullptr, 0}, d.rows, d.in,
