@@ -808,10 +808,11 @@ __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const
                                               const OB& b, Epi& epi, int M, int N, int K,
                                               int k_split, const TileMap& map) {
   constexpr int NS = ring_ns<NS_CFG, OA, OB>();
-  // Eight-wave tiles (a 2 x 4 wave grid) gave non-finite outputs for a packed
-  // forward at 64x128 tiles in an in-step trial; until that is found, every
-  // product runs four waves.
-  static_assert(NW == 4, "only four-wave tiles are validated");
+  // Eight waves (a 2 x 4 grid) run only on the interleaved loop. (An early
+  // eight-wave trial returned non-finite products because its operands were
+  // built for four waves: waves 4-7 loaded past the stage. The kNW check
+  // below rules that out.)
+  static_assert(NW == 4 || kInterleaved<BM, BN, BK, OA, OB, NW>, "wave count");
   static_assert(OA::kNW == NW && OB::kNW == NW, "operands built for another wave count");
   if constexpr (kInterleaved<BM, BN, BK, OA, OB, NW>) {
     gemm_lds_body_il<BM, BN, BK, NS_CFG, OA, OB, Epi, NW>(smem, bid, kz, a, b, epi, M, N, K,
@@ -1004,18 +1005,17 @@ __device__ __forceinline__ void run_lds_problem(char* smem, const LdsProblem<T, 
 // Independent GEMMs (possibly of different tile configs, operand kinds and
 // epilogues) in one launch: the first ps[0].blocks blocks run ps[0], the next
 // ps[1].blocks run ps[1], ..., so the blocks of all of them share the CUs.
+// The block has the most waves any problem needs; a block of a problem with
+// fewer leaves the rest idle, and they end at once (a barrier waits only for
+// the waves still running).
 template <class... Ps>
 constexpr int multi_nw() {
-  constexpr int nw[] = {LdsProblemSmem<Ps>::nw...};
-  for (int w : nw)
-    if (w != nw[0]) return -1;
-  return nw[0];
+  return max_of(LdsProblemSmem<Ps>::nw...);
 }
 
 template <class... Ps>
 __global__ __launch_bounds__(multi_nw<Ps...>() * 64) void gemm_lds_multi_kernel(
     unsigned long long* stamps, Ps... ps) {
-  static_assert(multi_nw<Ps...>() > 0, "the problems of one launch share the wave count");
   constexpr int S = max_of(LdsProblemSmem<Ps>::value...);
   __shared__ __attribute__((aligned(1024))) char smem[S];
   int bid = blockIdx.x;
@@ -1024,7 +1024,8 @@ __global__ __launch_bounds__(multi_nw<Ps...>() * 64) void gemm_lds_multi_kernel(
   auto one = [&](const auto& p) {
     if (done) return;
     if (bid < p.blocks) {
-      run_lds_problem(smem, p, bid);
+      if ((int)threadIdx.x < LdsProblemSmem<std::decay_t<decltype(p)>>::nw * 64)
+        run_lds_problem(smem, p, bid);
       done = true;
     } else {
       bid -= p.blocks;
@@ -1066,9 +1067,15 @@ struct LdsGiant {
 // 256x256 tiles over sign bits expanded in LDS: BK 64 halves the expansion
 // barriers and makes every row's stage segment a whole 128-byte line (config-5
 // key forward 400 -> 377 us; the fp16 forward measured 310 -> 318-328 us
-// with it, so it keeps LdsGiant).
+// with it, so it keeps LdsGiant), and eight waves, two per SIMD (the packed
+// forward alone 396 -> 362 us; the fp16 forward 343 -> 351 us with them).
 struct LdsGiantBits {
-  static constexpr int bm = 256, bn = 256, bk = 64, ns = 2, nw = 4;
+  static constexpr int bm = 256, bn = 256, bk = 64, ns = 2, nw = 8;
+};
+// 256x256 tiles of eight waves for the weight gradients over many rows
+// (paired in one launch with the input gradients' eight-wave tiles).
+struct LdsGiant8 {
+  static constexpr int bm = 256, bn = 256, bk = 32, ns = 4, nw = 8;
 };
 
 constexpr long kBigAutoBlocks = 512;
@@ -1077,12 +1084,12 @@ constexpr long kGiantAutoBlocks = 512;
 // Per-call-site choice (with_lds): kAuto = LdsBig for large products, else
 // LdsMid / LdsShort by K; kDeep =
 // the four-stage BK 128 ring for launches of one block per CU whose operands
-// come from HBM; kBig = 128x128 tiles; kDeepGiant = kDeep, with 256x256
-// tiles for very large products (two k-contiguous fp16 operands only: with
-// a sign-bit or transposed operand those tiles measured slower than 128x256);
-// kNoBig = kAuto without the 128x128 rule (config 4's head logits, 1024 such
-// tiles: 64x64 tiles measured faster, the head op 170 -> 156 us).
-enum class LdsPolicy { kAuto, kDeep, kBig, kDeepGiant, kNoBig };
+// come from HBM; kBig = 128x128 tiles; kNoBig = kAuto without the 128x128
+// rule (config 4's head logits, 1024 such tiles: 64x64 tiles measured faster,
+// the head op 170 -> 156 us). 256x256 tiles are not chosen here: the call
+// sites that want them (giant_ok) name them, so that no pair launch carries
+// an unused four-wave 256x256 problem.
+enum class LdsPolicy { kAuto, kDeep, kBig, kNoBig };
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool mk_ok(const void* p, long ld) { return p && aligned16(p) && ld % 8 == 0; }
@@ -1109,11 +1116,6 @@ bool with_lds(long M, long N, long K, int splits, hipError_t* err, F&& f,
   // rings for the 128x256 tiles measured slower: fewer blocks fit per CU.
   // 256x256 tiles: 16 MFMAs per fragment step per wave (config-5 value
   // forward 418 -> 335 us).
-  if (policy == LdsPolicy::kDeepGiant && K % LdsGiant::bk == 0 && M % 256 == 0 &&
-      N % 256 == 0 && (M / 256) * (N / 256) * splits >= kGiantAutoBlocks) {
-    *err = f(LdsGiant{});
-    return true;
-  }
   if (K % LdsHuge::bk == 0 && M % 128 == 0 && N % 256 == 0 &&
       (M / 128) * (N / 256) * splits >= kHugeAutoBlocks) {
     *err = f(LdsHuge{});
@@ -1124,7 +1126,7 @@ bool with_lds(long M, long N, long K, int splits, hipError_t* err, F&& f,
     *err = f(LdsBig{});
     return true;
   }
-  if ((policy == LdsPolicy::kDeep || policy == LdsPolicy::kDeepGiant) && K % LdsDeep::bk == 0) {
+  if (policy == LdsPolicy::kDeep && K % LdsDeep::bk == 0) {
     *err = f(LdsDeep{});
     return true;
   }

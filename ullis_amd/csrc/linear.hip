@@ -238,6 +238,14 @@ hipError_t fp16_forward(hipStream_t s, const void* x, int x_dtype, long rows, lo
     return fp16_gemv(s, x, x_dtype, rows, in, out, w, y32, resid, y16);
   EpiF16Fwd epi{y32, resid, y16};
   hipError_t err = hipSuccess;
+  // very large products: 256x256 tiles (four waves; eight measured 343 -> 351
+  // us at config 5's value forward)
+  if (x_dtype == kF16 && lds::mk_ok(x, in) && lds::mk_ok(w, in) && lds::giant_ok(rows, out, in)) {
+    using T = lds::LdsGiant;
+    lds::OpMK<T::bm, T::bk, T::nw> a{static_cast<const half_t*>(x), in, (int)rows};
+    lds::OpMK<T::bn, T::bk, T::nw> b{reinterpret_cast<const half_t*>(w), in, (int)out};
+    return lds::launch_lds<T>(s, a, b, epi, rows, out, in, 1);
+  }
   if (x_dtype == kF16 && lds::mk_ok(x, in) && lds::mk_ok(w, in) &&
       lds::with_lds(rows, out, in, 1, &err, [&](auto t) {
         using T = decltype(t);
@@ -246,7 +254,7 @@ hipError_t fp16_forward(hipStream_t s, const void* x, int x_dtype, long rows, lo
         return lds::launch_lds<T>(s, a, b, epi, rows, out, in, 1);
         // one block per CU at heron sizes, reading an operand fresh from HBM:
         // the four-stage ring (measured 18.9 -> 15.2 us in the step)
-      }, lds::LdsPolicy::kDeepGiant))
+      }, lds::LdsPolicy::kDeep))
     return err;
   return with_tile(rows, out, [&](auto t) {
     using T = decltype(t);

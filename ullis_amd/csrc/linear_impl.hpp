@@ -444,8 +444,8 @@ bool weight_grad_lds(const WeightGradArgs& d, hipError_t* err, F&& f) {
   const uint16_t* g16 = d.gy16 ? d.gy16 : d.gy32.p16;
   if (!lds::km_ok(g16, d.out, d.out) || !lds::km_ok(d.x16, d.in, d.in)) return false;
   EpiPartial epi{d.part};
-  if (dw_giant(d.out, d.in, d.rows) && d.rows % (lds::LdsGiant::bk * d.splits) == 0) {
-    using T = lds::LdsGiant;
+  if (dw_giant(d.out, d.in, d.rows) && d.rows % (lds::LdsGiant8::bk * d.splits) == 0) {
+    using T = lds::LdsGiant8;
     lds::OpKM<T::bm, T::bk, T::nw> a{reinterpret_cast<const half_t*>(g16), d.out, (int)d.out};
     lds::OpKM<T::bn, T::bk, T::nw> b{reinterpret_cast<const half_t*>(d.x16), d.in, (int)d.in};
     *err = f(lds::lds_problem<T>(a, b, epi, d.out, d.in, d.rows, d.splits));
