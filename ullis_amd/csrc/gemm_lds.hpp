@@ -664,8 +664,9 @@ constexpr int lds_smem_bytes() {
 }
 
 // Tiles with at least this many MFMAs per wave per 16-deep step and plain
-// fragment operands take the interleaved K loop.
-constexpr int kInterleaveMfmas = 8;
+// fragment operands take the interleaved K loop (128x128 four-wave tiles
+// included: config 4's value backward pair 22.2 -> 22.0 us).
+constexpr int kInterleaveMfmas = 4;
 template <int BM, int BN, int BK, class OA, class OB, int NW>
 inline constexpr bool kInterleaved = kPlainFrag<OA> && kPlainFrag<OB> && BK >= 32 &&
                                      (BM / 64) * (BN / (NW * 16)) >= kInterleaveMfmas;
@@ -1071,6 +1072,11 @@ struct LdsGiant {
 // forward alone 396 -> 362 us; the fp16 forward 343 -> 351 us with them).
 struct LdsGiantBits {
   static constexpr int bm = 256, bn = 256, bk = 64, ns = 2, nw = 8;
+};
+// 128x256 tiles of eight waves (64x64 per wave, two waves per SIMD): config
+// 5's value dX from the value^T cache (its pair 995 -> 969 us).
+struct LdsHuge8 {
+  static constexpr int bm = 128, bn = 256, bk = 32, ns = 4, nw = 8;
 };
 // 256x256 tiles of eight waves for the weight gradients over many rows
 // (paired in one launch with the input gradients' eight-wave tiles).

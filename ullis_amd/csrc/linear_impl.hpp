@@ -462,14 +462,15 @@ bool weight_grad_lds(const WeightGradArgs& d, hipError_t* err, F&& f) {
 template <class F>
 bool fp16_dx_lds(const Fp16DxArgs& d, hipError_t* err, F&& f) {
   // gX[rows][in] = gY[rows][out] . W[out][in]: B(n = i, k = o) = W[o*in + i],
-  // or W^T[i*out + o] k-contiguous when given. With W^T, 128x256 tiles of two
-  // k-contiguous operands on the interleaved K loop: at config 5 the value
-  // backward pair took 1046 us against 1136 us on 128x128 tiles and 1389 us
-  // with the transposed operand (256x256 tiles: 1752 us).
+  // or W^T[i*out + o] k-contiguous when given. With W^T, 128x256 eight-wave
+  // tiles of two k-contiguous operands on the interleaved K loop: at config 5
+  // the value backward pair took 969 us, against 995 us with four waves, 1136
+  // us on 128x128 tiles and 1389 us with the transposed operand (256x256
+  // tiles: 1752 us).
   if (d.w_t && lds::mk_ok(d.gy32.p16, d.out) && lds::mk_ok(d.w_t, d.out) &&
       d.out % lds::LdsHuge::bk == 0 && d.rows % lds::LdsHuge::bm == 0 &&
-      d.in % lds::LdsHuge::bn == 0) {
-    using T = lds::LdsHuge;
+      d.in % lds::LdsHuge8::bn == 0) {
+    using T = lds::LdsHuge8;
     lds::OpMK<T::bm, T::bk, T::nw> a{reinterpret_cast<const half_t*>(d.gy32.p16), d.out, (int)d.rows};
     lds::OpMK<T::bn, T::bk, T::nw> b{reinterpret_cast<const half_t*>(d.w_t), d.out, (int)d.in};
     if (d.gk16)
