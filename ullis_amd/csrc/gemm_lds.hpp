@@ -1006,17 +1006,20 @@ __device__ __forceinline__ void run_lds_problem(char* smem, const LdsProblem<T, 
 // Independent GEMMs (possibly of different tile configs, operand kinds and
 // epilogues) in one launch: the first ps[0].blocks blocks run ps[0], the next
 // ps[1].blocks run ps[1], ..., so the blocks of all of them share the CUs.
-// The block has the most waves any problem needs; a block of a problem with
-// fewer leaves the rest idle, and they end at once (a barrier waits only for
-// the waves still running).
+// The problems of one launch share the wave count (launch_lds_multi launches
+// problems of different wave counts one after another instead).
 template <class... Ps>
 constexpr int multi_nw() {
-  return max_of(LdsProblemSmem<Ps>::nw...);
+  constexpr int nw[] = {LdsProblemSmem<Ps>::nw...};
+  for (int w : nw)
+    if (w != nw[0]) return -1;
+  return nw[0];
 }
 
 template <class... Ps>
 __global__ __launch_bounds__(multi_nw<Ps...>() * 64) void gemm_lds_multi_kernel(
     unsigned long long* stamps, Ps... ps) {
+  static_assert(multi_nw<Ps...>() > 0, "the problems of one launch share the wave count");
   constexpr int S = max_of(LdsProblemSmem<Ps>::value...);
   __shared__ __attribute__((aligned(1024))) char smem[S];
   int bid = blockIdx.x;
@@ -1025,8 +1028,7 @@ __global__ __launch_bounds__(multi_nw<Ps...>() * 64) void gemm_lds_multi_kernel(
   auto one = [&](const auto& p) {
     if (done) return;
     if (bid < p.blocks) {
-      if ((int)threadIdx.x < LdsProblemSmem<std::decay_t<decltype(p)>>::nw * 64)
-        run_lds_problem(smem, p, bid);
+      run_lds_problem(smem, p, bid);
       done = true;
     } else {
       bid -= p.blocks;
@@ -1201,13 +1203,22 @@ hipError_t launch_lds_problem(hipStream_t s, const LdsProblem<T, OA, OB, Epi>& p
 }
 
 // Shapes must fit int32 (lds_problem's callers check M, N, K).
+// Problems of different wave counts (an eight-wave 256x256 product beside a
+// four-wave one, a shape pair config 4 and 5 never form) run as separate
+// launches, in order, on the stream.
 template <class... Ps>
 hipError_t launch_lds_multi(hipStream_t s, const Ps&... ps) {
-  unsigned long long* stamps = take_probe_stamps(0L + (0L + ... + ps.blocks));
-  launch((gemm_lds_multi_kernel<Ps...>), dim3((unsigned)(0 + ... + ps.blocks)),
-         dim3(multi_nw<Ps...>() * 64), 0,
-         s, stamps, ps...);
-  return hipGetLastError();
+  if constexpr (multi_nw<Ps...>() > 0) {
+    unsigned long long* stamps = take_probe_stamps(0L + (0L + ... + ps.blocks));
+    launch((gemm_lds_multi_kernel<Ps...>), dim3((unsigned)(0 + ... + ps.blocks)),
+           dim3(multi_nw<Ps...>() * 64), 0,
+           s, stamps, ps...);
+    return hipGetLastError();
+  } else {
+    hipError_t e = hipSuccess;
+    ((e = e == hipSuccess ? launch_lds_problem(s, ps) : e), ...);
+    return e;
+  }
 }
 
 template <class P1, class P2>

@@ -20,17 +20,20 @@ constexpr int kLutWords = 32;
 constexpr int kRedFloats = 4 * 16 * 64;
 
 // x rows 0 .. rows_m -> LDS fp16 [rows_m][in] with 16-byte loads (in % 8 ==
-// 0; x 16-byte aligned), a thread's loads issued before its stores: 8 loads
-// in flight per thread for fp16 x, 8 pairs for fp32 x (16 for fp16 measured
-// slower in the value product at 8 rows: 15.9 against 10.7 us).
+// 0, n8 >= 1; x 16-byte aligned), a thread's loads issued before its stores:
+// 8 loads in flight per thread for fp16 x, 8 pairs for fp32 x (16 for fp16
+// measured slower in the value product at 8 rows: 15.9 against 10.7 us).
+// Every load is issued (indices past the end reload the last chunk, whose
+// store is skipped): with the loads under a condition the compiler kept the
+// chunks in scratch memory and waited for each load before the next.
 template <int DEPTH, bool F32>
 __device__ __forceinline__ void stage_x_rows_n(uint16_t* xs, const void* x, int n8) {
   for (int base = 0; base < n8; base += DEPTH * kThreads) {
     uint4 v[DEPTH];
 #pragma unroll
     for (int t = 0; t < DEPTH; ++t) {
-      const int i = base + threadIdx.x + t * kThreads;
-      if (i < n8) {
+      const int i = min(base + (int)threadIdx.x + t * kThreads, n8 - 1);
+      {
         const long e = 8L * i;
         if (!F32) {
           v[t] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + e);
