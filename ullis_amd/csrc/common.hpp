@@ -103,36 +103,71 @@ __device__ __forceinline__ bool latent_is_plus(uint16_t latent_bits) {
   return f16_bits_to_f32(latent_bits) >= 0.0f;
 }
 
-// Wave64 reductions (no LDS).
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+// Cross-lane moves of a xor butterfly with no LDS round trip: v_permlane32_swap
+// and v_permlane16_swap give lane ^ 32 and lane ^ 16, DPP row_ror:8 lane ^ 8,
+// DPP row_ror:4 lane ^ 4 or ^ 12 (the same value once the ^ 8 step has run),
+// and quad permutations lane ^ 2 and ^ 1. (A __shfl_xor is a ds_bpermute,
+// one LDS round trip per step, each waited for before the next.) The lane
+// layouts were checked on gfx950, and the butterflies below are bit-identical
+// to the __shfl_xor ones with the same offsets.
+namespace xlane {
+__device__ __forceinline__ uint32_t swap32(uint32_t v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return (threadIdx.x & 32) ? (uint32_t)r[0] : (uint32_t)r[1];
+}
+__device__ __forceinline__ uint32_t swap16(uint32_t v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return (threadIdx.x & 16) ? (uint32_t)r[0] : (uint32_t)r[1];
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+// The partner value of butterfly step OFF (steps run from large to small).
+template <int OFF>
+__device__ __forceinline__ uint32_t step(uint32_t v) {
+  if constexpr (OFF == 32) return swap32(v);
+  else if constexpr (OFF == 16) return swap16(v);
+  else if constexpr (OFF == 8) return dpp<0x128>(v);  // row_ror:8
+  else if constexpr (OFF == 4) return dpp<0x124>(v);  // row_ror:4
+  else if constexpr (OFF == 2) return dpp<0x4E>(v);   // quad_perm 2,3,0,1
+  else return dpp<0xB1>(v);                           // quad_perm 1,0,3,2
+}
+// v = op(v, partner) for OFF = FROM, FROM / 2, ..., 1 (FROM 8 or more, so
+// that the ^ 4 step follows the ^ 8 one).
+template <int FROM, class T, class Op>
+__device__ __forceinline__ T butterfly(T v, Op op) {
+  static_assert(FROM >= 8 && (FROM & (FROM - 1)) == 0 && FROM <= 32, "butterfly width");
+  if constexpr (FROM >= 32) v = op(v, __builtin_bit_cast(T, step<32>(__builtin_bit_cast(uint32_t, v))));
+  if constexpr (FROM >= 16) v = op(v, __builtin_bit_cast(T, step<16>(__builtin_bit_cast(uint32_t, v))));
+  v = op(v, __builtin_bit_cast(T, step<8>(__builtin_bit_cast(uint32_t, v))));
+  v = op(v, __builtin_bit_cast(T, step<4>(__builtin_bit_cast(uint32_t, v))));
+  v = op(v, __builtin_bit_cast(T, step<2>(__builtin_bit_cast(uint32_t, v))));
+  v = op(v, __builtin_bit_cast(T, step<1>(__builtin_bit_cast(uint32_t, v))));
   return v;
+}
+}  // namespace xlane
+
+// Wave64 reductions; every lane receives the result.
+__device__ __forceinline__ float wave_sum(float v) {
+  return xlane::butterfly<32>(v, [](float a, float b) { return a + b; });
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+  return xlane::butterfly<32>(v, [](float a, float b) { return __builtin_fmaxf(a, b); });
 }
 
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += (uint32_t)__shfl_xor((int)v, off, 64);
-  return v;
+  return xlane::butterfly<32>(v, [](uint32_t a, uint32_t b) { return a + b; });
 }
 
-// Max over the 32 lanes of each half-wave (lanes 0-31 and 32-63 separately).
+// Max / sum over the 32 lanes of each half-wave (lanes 0-31 and 32-63 separately).
 __device__ __forceinline__ float halfwave_max(float v) {
-#pragma unroll
-  for (int off = 16; off > 0; off >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+  return xlane::butterfly<16>(v, [](float a, float b) { return __builtin_fmaxf(a, b); });
 }
 
 __device__ __forceinline__ float halfwave_sum(float v) {
-#pragma unroll
-  for (int off = 16; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  return xlane::butterfly<16>(v, [](float a, float b) { return a + b; });
 }
 
 // Non-negative floats order like their bit patterns, so a u32 atomicMax on the

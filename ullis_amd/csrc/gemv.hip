@@ -28,6 +28,7 @@ using gemv::stage_x_rows;
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float wave_sum(float v, int width) {
+  if (width == 64) return ullis::wave_sum(v);
   for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
   return v;
 }
