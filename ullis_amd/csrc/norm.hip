@@ -97,11 +97,46 @@ __global__ __launch_bounds__(256) void ln_fwd_vec_kernel(const float* __restrict
   }
 }
 
-// mix one 4-channel chunk: out = f16(x + (prev - x) * mix), prev = 0 at t = 0
-// (time_shift_mix on the fp16 LayerNorm output).
-__device__ __forceinline__ void mix4_store(const half4& x, const half4& p, const uint16_t* mix,
-                                           uint16_t* out, int c, long idx) {
-  const half4 m = *reinterpret_cast<const half4*>(mix + c);
+// The arithmetic of ln_row_vec on a row whose chunks (x, or resid + x; zero
+// past ch) and LayerNorm weights are already in registers.
+template <int NV>
+__device__ __forceinline__ void ln_row_regs(const floatx4 (&v)[NV], int ch, int lane,
+                                            const half4 (&wv)[NV], const half4 (&bv)[NV],
+                                            floatx4 (&out)[NV]) {
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) s += (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]);
+  const float mean = wave_sum(s) / (float)ch;
+  float q = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 4;
+    if (c < ch) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float d = v[j][e] - mean;
+        q += d * d;
+      }
+    }
+  }
+  const float var = wave_sum(q) / (float)ch;
+  const float inv = 1.0f / __builtin_sqrtf(var + kLayerNormEps);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 4;
+    if (c < ch) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        out[j][e] = (v[j][e] - mean) * inv * (float)wv[j][e] + (float)bv[j][e];
+    }
+  }
+}
+
+// mix one 4-channel chunk with its mix vector in registers: out = f16(x +
+// (prev - x) * mix), prev = 0 at t = 0 (time_shift_mix on the fp16 LayerNorm
+// output).
+__device__ __forceinline__ void mix4_store(const half4& x, const half4& p, const half4& m,
+                                             uint16_t* out, long idx) {
   half4 o;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -118,6 +153,9 @@ __device__ __forceinline__ void mix4_store(const half4& x, const half4& p, const
 // fp16 rows without the LayerNorm output making a round trip through HBM.
 // y16 (optional) also receives the fp16 LayerNorm output. With resid, the
 // LayerNorm input is resid + x (a residual add), which sum_out receives.
+// Every load of both rows, the LayerNorm weights and the mix vectors is
+// issued before the first is used, so their round trips overlap (loaded
+// row by row, each row waited for its chunks, then its weights, in turn).
 template <int NV>
 __global__ __launch_bounds__(256) void ln_mix_kernel(const float* __restrict__ x, long rows,
                                                      int time, int ch,
@@ -132,13 +170,48 @@ __global__ __launch_bounds__(256) void ln_mix_kernel(const float* __restrict__ x
   const int lane = threadIdx.x & 63;
   const long row = (long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
-  floatx4 cur[NV], prev[NV];
-  ln_row_vec<NV>(x + row * ch, ch, lane, w, b, cur, resid ? resid + row * ch : nullptr,
-                 resid ? sum_out + row * ch : nullptr);
   const bool has_prev = row % time != 0;  // uniform over the wave
-  if (has_prev)
-    ln_row_vec<NV>(x + (row - 1) * ch, ch, lane, w, b, prev,
-                   resid ? resid + (row - 1) * ch : nullptr);
+  const long prow = has_prev ? row - 1 : row;
+  floatx4 vc[NV], vp[NV];
+  half4 wv[NV], bv[NV], m0[NV], m1[NV], m2[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 4;
+    const int cc = c < ch ? c : 0;  // in bounds; chunks past ch are zeroed below
+    vc[j] = *reinterpret_cast<const floatx4*>(x + row * ch + cc);
+    vp[j] = *reinterpret_cast<const floatx4*>(x + prow * ch + cc);
+    wv[j] = *reinterpret_cast<const half4*>(w + cc);
+    bv[j] = *reinterpret_cast<const half4*>(b + cc);
+    if (out0) m0[j] = *reinterpret_cast<const half4*>(mix0 + cc);
+    if (out1) m1[j] = *reinterpret_cast<const half4*>(mix1 + cc);
+    if (out2) m2[j] = *reinterpret_cast<const half4*>(mix2 + cc);
+  }
+  if (resid) {
+    floatx4 rc[NV], rp[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int c = (lane + 64 * j) * 4;
+      const int cc = c < ch ? c : 0;
+      rc[j] = *reinterpret_cast<const floatx4*>(resid + row * ch + cc);
+      rp[j] = *reinterpret_cast<const floatx4*>(resid + prow * ch + cc);
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vc[j][e] = rc[j][e] + vc[j][e];
+        vp[j][e] = rp[j][e] + vp[j][e];
+      }
+      const int c = (lane + 64 * j) * 4;
+      if (sum_out && c < ch) *reinterpret_cast<floatx4*>(sum_out + row * ch + c) = vc[j];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+    if ((lane + 64 * j) * 4 >= ch) vc[j] = vp[j] = (floatx4){};
+  floatx4 cur[NV], prev[NV];
+  ln_row_regs<NV>(vc, ch, lane, wv, bv, cur);
+  if (has_prev) ln_row_regs<NV>(vp, ch, lane, wv, bv, prev);
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int c = (lane + 64 * j) * 4;
@@ -151,9 +224,9 @@ __global__ __launch_bounds__(256) void ln_mix_kernel(const float* __restrict__ x
       }
       const long idx = row * ch + c;
       if (y16) *reinterpret_cast<half4*>(y16 + idx) = xh;
-      if (out0) mix4_store(xh, ph, mix0, out0, c, idx);
-      if (out1) mix4_store(xh, ph, mix1, out1, c, idx);
-      if (out2) mix4_store(xh, ph, mix2, out2, c, idx);
+      if (out0) mix4_store(xh, ph, m0[j], out0, idx);
+      if (out1) mix4_store(xh, ph, m1[j], out1, idx);
+      if (out2) mix4_store(xh, ph, m2[j], out2, idx);
     }
   }
 }
