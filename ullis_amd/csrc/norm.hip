@@ -397,29 +397,54 @@ __global__ __launch_bounds__(256) void ln_bwd_row_kernel(const float* __restrict
   const int wave = threadIdx.x >> 6;
   const long row = (long)blockIdx.x * kRowsPerBlock + wave;
   const bool live = row < rows;
+  // Loads go to in-bounds addresses unconditionally (a dead wave reads the
+  // last row, a chunk past ch reads chunk 0, a missing neighbour row reads
+  // the row itself) and the values are selected afterwards, so no load waits
+  // behind a branch.
+  const long lrow = live ? row : rows - 1;
   floatx4 v[NV], g[NV], old[NV], wv[NV], gmix[NV];
-  const int t = MIX ? (int)(row % time) : 0;
+  const int t = MIX ? (int)(lrow % time) : 0;
+  const bool has_next = t + 1 < time;
+  const long prow = t > 0 ? lrow - 1 : lrow;
+  const long nrow = has_next ? lrow + 1 : lrow;
+  floatx4 xv[NV], gv[NV], nv[NV];
+  half4 xh[NV], ph[NV], mv[NV], wh[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (lane + 64 * j) * 4;
+    const int cc = c < ch ? c : 0;
+    xv[j] = *reinterpret_cast<const floatx4*>(x + lrow * ch + cc);
+    gv[j] = *reinterpret_cast<const floatx4*>(gy + lrow * ch + cc);
+    wh[j] = *reinterpret_cast<const half4*>(w + cc);
+    if constexpr (MIX) {
+      nv[j] = *reinterpret_cast<const floatx4*>(gy + nrow * ch + cc);
+      xh[j] = *reinterpret_cast<const half4*>(x16 + lrow * ch + cc);
+      ph[j] = *reinterpret_cast<const half4*>(x16 + prow * ch + cc);
+      mv[j] = *reinterpret_cast<const half4*>(mix + cc);
+    }
+  }
+  if (accumulate) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int c = (lane + 64 * j) * 4;
+      old[j] = *reinterpret_cast<const floatx4*>(gx + lrow * ch + (c < ch ? c : 0));
+    }
+  }
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int c = (lane + 64 * j) * 4;
     const bool ok = live && c < ch;
-    v[j] = ok ? *reinterpret_cast<const floatx4*>(x + row * ch + c) : (floatx4){};
+    v[j] = ok ? xv[j] : (floatx4){};
     if constexpr (MIX) {
-      floatx4 gs = {}, gn = {};
-      half4 xh = {}, ph = {}, m = {};
-      const bool has_next = t + 1 < time;
-      if (ok) {
-        const long idx = row * ch + c;
-        gs = *reinterpret_cast<const floatx4*>(gy + idx);
-        xh = *reinterpret_cast<const half4*>(x16 + idx);
-        if (t > 0) ph = *reinterpret_cast<const half4*>(x16 + idx - ch);
-        if (has_next) gn = *reinterpret_cast<const floatx4*>(gy + idx + ch);
-        m = *reinterpret_cast<const half4*>(mix + c);
-      }
+      const floatx4 gs = ok ? gv[j] : (floatx4){};
+      const floatx4 gn = ok && has_next ? nv[j] : (floatx4){};
+      const half4 xo = ok ? xh[j] : (half4){};
+      const half4 po = ok && t > 0 ? ph[j] : (half4){};
+      const half4 m = ok ? mv[j] : (half4){};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float xt = (float)xh[e];
-        const float xx = (t == 0 ? 0.0f : (float)ph[e]) - xt;
+        const float xt = (float)xo[e];
+        const float xx = (t == 0 ? 0.0f : (float)po[e]) - xt;
         const float mm = (float)m[e];
         gmix[j][e] = gs[e] * xx;
         float gb = gs[e] - gs[e] * mm;
@@ -427,12 +452,12 @@ __global__ __launch_bounds__(256) void ln_bwd_row_kernel(const float* __restrict
         g[j][e] = gb;
       }
     } else {
-      g[j] = ok ? *reinterpret_cast<const floatx4*>(gy + row * ch + c) : (floatx4){};
+      g[j] = ok ? gv[j] : (floatx4){};
     }
-    old[j] = ok && accumulate ? *reinterpret_cast<const floatx4*>(gx + row * ch + c) : (floatx4){};
-    const half4 wh = c < ch ? *reinterpret_cast<const half4*>(w + c) : (half4){};
+    if (!(ok && accumulate)) old[j] = (floatx4){};
+    const half4 wo = c < ch ? wh[j] : (half4){};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) wv[j][e] = (float)wh[e];
+    for (int e = 0; e < 4; ++e) wv[j][e] = (float)wo[e];
   }
   float s = 0.0f;
 #pragma unroll
