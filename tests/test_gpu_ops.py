@@ -462,6 +462,9 @@ def test_device_copy_kernel(rt, dst_off, src_off, n):
     (5, 7, 100, "uniform"),      # heavy collisions, d not a multiple of 4
     (1, 64, 300, "uniform"),     # one token: a 300-row chain across ballot chunks
     (50000, 256, 513, "uniform"),
+    (3, 8, 40000, "uniform"),    # chains of ~13k rows across several 16384-row walk windows
+    (32768, 1024, 32768, "uniform"),  # config 5 widths
+    (40, 2100, 300, "uniform"),  # wider than one walk's 2048 register-held channels
 ])
 def test_embedding_gather_scatter_sgd_bit_exact(rt, vocab, d, rows, dist):
     rng = np.random.default_rng(vocab + d + rows)

@@ -43,49 +43,111 @@ __global__ __launch_bounds__(256) void embedding_gather_kernel(const uint16_t* t
   }
 }
 
+// Token reads a thread keeps in flight in the scans below.
+constexpr int kScanBatch = 16;
+// Rows of one pass of the walk: their matches are marked in an LDS bitmap
+// (kScatterWindow bits) with one summary bit per non-empty bitmap word.
+constexpr int kScatterWindow = 16384;
+constexpr int kScatterWords = kScatterWindow / 64;
+// Channels a thread carries through the walk in registers (256 threads:
+// widths up to 2048 in one walk, wider tables walk once per 2048 channels).
+constexpr int kScatterChannels = 8;
+
 // Clipped SGD of table[tokens[r]] with g[r] for every row r, in row order for
 // rows that share a token, as the reference's sequential loop applies them.
-// Block r does the work only if r is the first row holding its token; it then
-// walks the later rows with the same token (64 at a time by wave ballot),
-// keeping each channel's value and carry in registers between applications,
-// which is the same arithmetic as storing and reloading them.
+// Block r does the work only if r is the first row holding its token: the
+// block checks rows [0, r) for its token (kScanBatch reads in flight per
+// thread), then marks the rows [r, rows) holding it in an LDS bitmap and
+// applies their gradients in row order, each channel's value and carry kept
+// in registers between applications (the same arithmetic as storing and
+// reloading them).
 __global__ __launch_bounds__(256) void embedding_scatter_sgd_kernel(uint16_t* table,
                                                                     float* residual, int d,
                                                                     const uint32_t* tokens,
                                                                     int rows, uint32_t vocab,
                                                                     const float* g, float lr,
                                                                     const uint32_t* abort) {
+  __shared__ unsigned long long s_bits[kScatterWords];
+  __shared__ unsigned long long s_sum[kScatterWords / 64];
   const int r = blockIdx.x;
+  const int t = threadIdx.x;
   if (abort && *abort) return;  // refused step
   const uint32_t id = tokens[r];
   if (id >= vocab) return;
-  const int lane = threadIdx.x & 63;
-  for (int base = 0; base < r; base += 64) {
-    const int j = base + lane;
-    if (__ballot(j < r && tokens[j] == id)) return;  // an earlier row owns this token
-  }
-  const long row0 = (long)id * d;
-  for (int c0 = 0; c0 < d; c0 += 256) {
-    const int c = c0 + threadIdx.x;
-    const bool active = c < d;
-    uint16_t v = 0;
-    float res = 0.0f;
-    if (active) {
-      v = table[row0 + c];
-      res = residual[row0 + c];
+  bool earlier = false;
+  for (int base = 0; base < r; base += 256 * kScanBatch) {
+    uint32_t tk[kScanBatch];
+#pragma unroll
+    for (int u = 0; u < kScanBatch; ++u) {
+      const int j = base + u * 256 + t;
+      tk[u] = tokens[j < r ? j : r - 1];  // past r - 1: row r - 1 again, also an earlier row
     }
-    for (int base = r; base < rows; base += 64) {
-      const int j = base + lane;
-      unsigned long long m = __ballot(j < rows && tokens[j] == id);
-      while (m) {
-        const int k = __builtin_ctzll(m);
-        m &= m - 1;
-        if (active) clipped_sgd_one(v, res, g[(long)(base + k) * d + c], lr);
+#pragma unroll
+    for (int u = 0; u < kScanBatch; ++u) earlier = earlier || tk[u] == id;
+  }
+  if (__syncthreads_or(earlier)) return;  // an earlier row owns this token
+  for (int cg = 0; cg < d; cg += 256 * kScatterChannels) {
+    uint16_t v[kScatterChannels];
+    float res[kScatterChannels];
+    const long row0 = (long)id * d;
+#pragma unroll
+    for (int k = 0; k < kScatterChannels; ++k) {
+      const int c = cg + k * 256 + t;
+      v[k] = 0;
+      res[k] = 0.0f;
+      if (c < d) {
+        v[k] = table[row0 + c];
+        res[k] = residual[row0 + c];
       }
     }
-    if (active) {
-      table[row0 + c] = v;
-      residual[row0 + c] = res;
+    for (int w0 = r; w0 < rows; w0 += kScatterWindow) {
+      const int wn = rows - w0 < kScatterWindow ? rows - w0 : kScatterWindow;
+      for (int q = t; q < kScatterWords; q += 256) s_bits[q] = 0ull;
+      if (t < kScatterWords / 64) s_sum[t] = 0ull;
+      __syncthreads();
+      for (int base = 0; base < wn; base += 256 * kScanBatch) {
+        uint32_t tk[kScanBatch];
+#pragma unroll
+        for (int u = 0; u < kScanBatch; ++u) {
+          const int j = base + u * 256 + t;
+          tk[u] = tokens[w0 + (j < wn ? j : wn - 1)];
+        }
+#pragma unroll
+        for (int u = 0; u < kScanBatch; ++u) {
+          const int j = base + u * 256 + t;
+          if (j < wn && tk[u] == id) {
+            atomicOr(&s_bits[j >> 6], 1ull << (j & 63));
+            atomicOr(&s_sum[j >> 12], 1ull << ((j >> 6) & 63));
+          }
+        }
+      }
+      __syncthreads();
+      for (int sw = 0; sw < kScatterWords / 64; ++sw) {
+        unsigned long long sm = s_sum[sw];
+        while (sm) {
+          const int q = sw * 64 + __builtin_ctzll(sm);
+          sm &= sm - 1;
+          unsigned long long m = s_bits[q];
+          while (m) {
+            const long j = w0 + q * 64 + __builtin_ctzll(m);
+            m &= m - 1;
+#pragma unroll
+            for (int k = 0; k < kScatterChannels; ++k) {
+              const int c = cg + k * 256 + t;
+              if (c < d) clipped_sgd_one(v[k], res[k], g[j * d + c], lr);
+            }
+          }
+        }
+      }
+      __syncthreads();  // every thread has read the bitmap before the next window clears it
+    }
+#pragma unroll
+    for (int k = 0; k < kScatterChannels; ++k) {
+      const int c = cg + k * 256 + t;
+      if (c < d) {
+        table[row0 + c] = v[k];
+        residual[row0 + c] = res[k];
+      }
     }
   }
 }
