@@ -326,10 +326,11 @@ def test_block_methods_reject_bad_arguments(rt):
     assert lib.ullis_hip_rosa_tape_bytes(t, 0) == 0
 
 
-@pytest.mark.parametrize("d,layers,f,vocab,time",
-                         [(64, 2, 128, 256, 64), (128, 3, 256, 512, 128),
-                          (512, 2, 2048, 8192, 2048), (512, 1, 4096, 512, 8192)])
-def test_block_step_matches_fused_step(rt, d, layers, f, vocab, time):
+@pytest.mark.parametrize("d,layers,f,vocab,time,batch",
+                         [(64, 2, 128, 256, 64, 1), (128, 3, 256, 512, 128, 1),
+                          (512, 2, 2048, 8192, 2048, 1), (512, 1, 4096, 512, 8192, 1),
+                          (64, 1, 128, 256, 4099, 3)])
+def test_block_step_matches_fused_step(rt, d, layers, f, vocab, time, batch):
     """HeronBlockStep (block methods, host residual adds, the automaton
     handed the Q/K/V planes between the projections and O) against the fused
     step on the same arena and inputs: bit-identical, since both run the same
@@ -337,12 +338,13 @@ def test_block_step_matches_fused_step(rt, d, layers, f, vocab, time):
     third case has config 4's widths at two layers). In the last case the
     fused step's value input gradient reads its value^T cache (both operands
     k-contiguous) and the block path the value weight itself (a transposed
-    operand): every output still sums the same products in the same order."""
-    shape = HeronShape(d_model=d, n_layers=layers, dim_ffn=f, vocab=vocab, batch=1, time=time)
+    operand): every output still sums the same products in the same order.
+    The last case has three sequences of an odd length."""
+    shape = HeronShape(d_model=d, n_layers=layers, dim_ffn=f, vocab=vocab, batch=batch, time=time)
     fused = HeronTrainer(rt, shape)
     blocks = HeronBlockStep(rt, shape)
     arena = heron_arena(fused.layout, fused.arena_bytes, shape.dims(), seed=3, random_ln=True)
-    x, labels, idx = step_inputs(shape.rows, d, vocab, layers, 1, time, seed=3)
+    x, labels, idx = step_inputs(shape.rows, d, vocab, layers, batch, time, seed=3)
     nd = shape.rows * d
     words = (nd + 31) // 32
 
