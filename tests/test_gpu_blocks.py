@@ -11,11 +11,13 @@ gradients are compared as max|gpu - ref| / max|ref| <= BLOCK_REL; updates are
 compared as the change of the effective parameter (f16 value + fp32 carry),
 which is -lr * clip(g), <= UPDATE_REL; sign bits as mismatch fractions (an
 output or latent within rounding of zero may land on either side). Each case
-writes its measured drift to gpurun_out/block_drift/<case>.json; the maxima
+writes its measured drift to block_drift/<case>.json under RESULTS; the maxima
 over the cases were 9.1e-4 (the key scale gradient), 7.6e-4 (the key latent
 step) and 5.8e-4 for everything else, and no updated weight sign bit
 differed. The bounds are those maxima with a margin under 2x.
 """
+import pathlib
+
 import numpy as np
 import pytest
 
@@ -23,6 +25,9 @@ from oracle import cpu_ref as o
 from ullis_amd.heron_blocks import HeronBlockStep
 from ullis_amd.runtime import HeronShape, HeronTrainer
 from ullis_amd.synth import f16, heron_arena, pack_bits, step_inputs, tensor_view, unpack_bits
+
+# results folder of a GPU run (the one a remote run's outputs come back from)
+RESULTS = pathlib.Path(__file__).resolve().parent.parent / "gpurun_out"
 
 pytestmark = pytest.mark.gpu
 
@@ -44,12 +49,11 @@ def rel(a, r):
 
 
 def record_drift(case: str, drift: dict) -> None:
-    """Writes one case's measured drift to gpurun_out/block_drift/<case>.json
+    """Writes one case's measured drift to RESULTS/block_drift/<case>.json
     (the figures the bounds above rest on)."""
     import json
-    import pathlib
 
-    out = pathlib.Path(__file__).resolve().parent.parent / "gpurun_out" / "block_drift"
+    out = RESULTS / "block_drift"
     out.mkdir(parents=True, exist_ok=True)
     (out / f"{case}.json").write_text(json.dumps(drift, indent=1, sort_keys=True))
 

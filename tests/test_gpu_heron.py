@@ -5,7 +5,7 @@ The GPU keeps GEMM operands in fp16 (LayerNorm outputs, CMix activations,
 ROSA y) while the oracle carries fp32 activations, so composed outputs differ
 by accumulated fp16 rounding. Per-op bounds are in test_gpu_ops.py; here each
 output tensor is compared with max|gpu - ref| / max|ref|. Every case writes
-its measured drift to gpurun_out/step_drift/<case>.json. Over the six cases
+its measured drift to step_drift/<case>.json under RESULTS. Over the six cases
 (up to config 4's full depth, L12, and config 5's widths, D1024 V32768) the
 measured maxima were: mean CE 2.2e-5, any row's CE 2.5e-4, g_emb 3.5e-4,
 updated f16 parameters 7.6e-4 (the ROSA O scales), Q/K/V sign bit-planes
@@ -120,12 +120,14 @@ SMALL = [
 ]
 
 ROOT = pathlib.Path(__file__).resolve().parent.parent
+# results folder of a GPU run (the one a remote run's outputs come back from)
+RESULTS = ROOT / "gpurun_out"
 
 
 def record_drift(case: str, drift: dict) -> None:
     """Writes the measured composed drift of one case to
-    gpurun_out/step_drift/<case>.json (the figures the bounds above rest on)."""
-    out = ROOT / "gpurun_out" / "step_drift"
+    RESULTS/step_drift/<case>.json (the figures the bounds above rest on)."""
+    out = RESULTS / "step_drift"
     out.mkdir(parents=True, exist_ok=True)
     (out / f"{case}.json").write_text(json.dumps(drift, indent=1, sort_keys=True))
 
