@@ -136,7 +136,7 @@ __device__ __forceinline__ void ln_row_regs(const floatx4 (&v)[NV], int ch, int 
 // (prev - x) * mix), prev = 0 at t = 0 (time_shift_mix on the fp16 LayerNorm
 // output).
 __device__ __forceinline__ void mix4_store(const half4& x, const half4& p, const half4& m,
-                                             uint16_t* out, long idx) {
+                                           uint16_t* out, long idx) {
   half4 o;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -154,8 +154,9 @@ __device__ __forceinline__ void mix4_store(const half4& x, const half4& p, const
 // y16 (optional) also receives the fp16 LayerNorm output. With resid, the
 // LayerNorm input is resid + x (a residual add), which sum_out receives.
 // Every load of both rows, the LayerNorm weights and the mix vectors is
-// issued before the first is used, so their round trips overlap (loaded
-// row by row, each row waited for its chunks, then its weights, in turn).
+// issued before the first is used, so their round trips overlap instead of
+// following one another (a row's chunks, then its weights, then the next
+// row's).
 template <int NV>
 __global__ __launch_bounds__(256) void ln_mix_kernel(const float* __restrict__ x, long rows,
                                                      int time, int ch,
