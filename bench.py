@@ -59,7 +59,7 @@ TRAFFIC_BYTES = {
 # it reports also holds the ramp of the first workgroups and the end-of-kernel
 # cache writeback (about 2.4 us a launch here), which the stamps cannot see,
 # and the profiler slows the step. Re-measure when the kernels change.
-ROCPROF_AVG_US = {"value_backward": 25.78, "key_backward": 24.99}
+ROCPROF_AVG_US = {"value_backward": 23.73, "key_backward": 22.15}
 
 # Launch classes with a roofline object in the bench line: the step's dominant
 # launch (the value backward pair, fp16) and its dominant packed +-1 launch

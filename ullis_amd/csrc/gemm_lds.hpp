@@ -155,6 +155,25 @@ struct OpKM {
       dma16(p + (long)(k0 + kr) * ld + m, stage + (wave * kInst + t) * 1024);
     }
   }
+  // issue() through registers: the same chunks into r (rload), then into the
+  // stage at the places the DMA writes them (rstore).
+  __device__ __forceinline__ void rload(u32x4 (&r)[kInst], int row0, int k0, int wave,
+                                        int lane) const {
+#pragma unroll
+    for (int t = 0; t < kInst; ++t) {
+      const int id = (wave * kInst + t) * 64 + lane;
+      const int kr = id / CPR, pos = id % CPR;
+      const int c = pos ^ swz(kr);
+      const int m = min(row0 + 8 * c, rows - 8);
+      r[t] = *reinterpret_cast<const u32x4*>(p + (long)(k0 + kr) * ld + m);
+    }
+  }
+  __device__ __forceinline__ void rstore(const u32x4 (&r)[kInst], char* stage, int wave,
+                                         int lane) const {
+#pragma unroll
+    for (int t = 0; t < kInst; ++t)
+      *reinterpret_cast<u32x4*>(stage + (wave * kInst + t) * 1024 + lane * 16) = r[t];
+  }
   __device__ __forceinline__ half8 frag(const char* stage, const char*, int base, int ks16,
                                         int lane, int) const {
     const int g = lane >> 4, q = lane & 15;
@@ -397,6 +416,11 @@ struct OpBitsX {
   __device__ __forceinline__ Raw lut(const Pre& p, const char*) const { return p; }
   __device__ __forceinline__ half8 fix(const Raw& r) const { return r; }
 };
+
+template <class O>
+inline constexpr bool kIsKM = false;
+template <int R, int B, int W>
+inline constexpr bool kIsKM<OpKM<R, B, W>> = true;
 
 // Operands that expand a landed stage in LDS before its fragments are read.
 template <class O, class = void>
@@ -856,14 +880,54 @@ __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const
     a.issue(st, m0, kbeg + kt * BK, wave, lane);
     b.issue(st + OA::kBytes, n0, kbeg + kt * BK, wave, lane);
   };
+  // Two transposed operands on a two-stage ring (the 64x64 weight gradients)
+  // are staged through registers instead of the DMA: a stage's loads go out
+  // three steps before its MFMAs, and are stored into LDS the step before
+  // (config 4's value backward pair 22.0 -> 20.4 us). The register ring has
+  // two slots, so that K loop runs in pairs of steps (slot indices stay
+  // compile-time), with an odd last step peeled off; every other operand pair
+  // keeps the one-step loop (the pairs cost config 5's head logits, on this
+  // loop over sign bits, 11 -> 15 ms).
+  constexpr bool kRegStage = kIsKM<OA> && kIsKM<OB> && NS == 2;
+  u32x4 ra0[OA::kInst], ra1[OA::kInst], rb0[OB::kInst], rb1[OB::kInst];
+  if constexpr (kRegStage) {
+    // stage 0 through the registers into LDS, then stages 1 and 2 into them
+    a.rload(ra1, m0, kbeg, wave, lane);
+    b.rload(rb1, n0, kbeg, wave, lane);
+    a.rstore(ra1, smem, wave, lane);
+    b.rstore(rb1, smem + OA::kBytes, wave, lane);
+    const int k1 = 1 < nk ? 1 : nk - 1, k2 = 2 < nk ? 2 : nk - 1;
+    a.rload(ra1, m0, kbeg + k1 * BK, wave, lane);
+    b.rload(rb1, n0, kbeg + k1 * BK, wave, lane);
+    a.rload(ra0, m0, kbeg + k2 * BK, wave, lane);
+    b.rload(rb0, n0, kbeg + k2 * BK, wave, lane);
+  } else {
 #pragma unroll
-  for (int s = 0; s < NS - 1; ++s)
-    if (s < nk) issue(s);
+    for (int s = 0; s < NS - 1; ++s)
+      if (s < nk) issue(s);
+  }
 
-  for (int kt = 0; kt < nk; ++kt) {
-    // Stage kt is complete once at most the later stages' loads are in flight.
-    wait_stages<IPS, NS - 2>(nk - 1 - kt);
-    if (kt + NS - 1 < nk) issue(kt + NS - 1);
+  // One K step: P is the parity of kt (which register slot holds stage kt + 1).
+  auto step = [&](int kt, auto parity) {
+    if constexpr (kRegStage) {
+      constexpr int P = decltype(parity)::value;
+      // every wave's stores of stage kt are done, and its reads of stage
+      // kt - 1 (the slot stage kt + 1 now takes)
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      const int k3 = kt + 3 < nk ? kt + 3 : nk - 1;  // past the end: the last stage again
+      char* st1 = smem + ((kt + 1) % NS) * STAGE;
+      auto& rsa = P == 0 ? ra1 : ra0;
+      auto& rsb = P == 0 ? rb1 : rb0;
+      a.rstore(rsa, st1, wave, lane);
+      b.rstore(rsb, st1 + OA::kBytes, wave, lane);
+      a.rload(rsa, m0, kbeg + k3 * BK, wave, lane);
+      b.rload(rsb, n0, kbeg + k3 * BK, wave, lane);
+    } else {
+      (void)parity;
+      // Stage kt is complete once at most the later stages' loads are in flight.
+      wait_stages<IPS, NS - 2>(nk - 1 - kt);
+      if (kt + NS - 1 < nk) issue(kt + NS - 1);
+    }
     if constexpr (kExpands<OA> || kExpands<OB>) {
       // the stage's words have landed for every wave: expand them, then
       // barrier again (LDS writes only; the loads in flight stay in flight)
@@ -928,6 +992,16 @@ __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
+  };
+  if constexpr (kRegStage) {
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+      step(kt, std::integral_constant<int, 0>{});
+      step(kt + 1, std::integral_constant<int, 1>{});
+    }
+    if (kt < nk) step(kt, std::integral_constant<int, 0>{});
+  } else {
+    for (int kt = 0; kt < nk; ++kt) step(kt, std::integral_constant<int, 0>{});
   }
   wait_barrier<0>();  // every wave is done reading the ring
   if constexpr (kHasSplit<Epi>) epi.set_split(kz);
