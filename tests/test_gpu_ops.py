@@ -126,7 +126,9 @@ def test_binary_linear_backward_parity(rt, rows, in_f, out_f):
 # sum_i sign(o, i) G(o, i), g_bias = column sums of gy and gx = gy . (scale *
 # sign) (the oracle's ucr_packed_backward_ste, src/model.rs:745-796).
 @pytest.mark.parametrize("rows,in_f,out_f",
-                         [(16384, 1024, 1024), (16384, 256, 4096), (32768, 1024, 1024)])
+                         [(16384, 1024, 1024), (16384, 256, 4096), (32768, 1024, 1024),
+                          # 4 row splits of 384 rows: the last split is empty
+                          (1152, 256, 256)])
 def test_weight_gradients_over_many_rows(rt, rows, in_f, out_f):
     rng = np.random.default_rng(rows + in_f + 3 * out_f)
     x16, bits, scale, _ = rand_case(rng, rows, in_f, out_f)

@@ -892,15 +892,18 @@ __device__ __forceinline__ void gemm_lds_body(char* smem, int bid, int kz, const
   u32x4 ra0[OA::kInst], ra1[OA::kInst], rb0[OB::kInst], rb1[OB::kInst];
   if constexpr (kRegStage) {
     // stage 0 through the registers into LDS, then stages 1 and 2 into them
-    a.rload(ra1, m0, kbeg, wave, lane);
-    b.rload(rb1, n0, kbeg, wave, lane);
-    a.rstore(ra1, smem, wave, lane);
-    b.rstore(rb1, smem + OA::kBytes, wave, lane);
-    const int k1 = 1 < nk ? 1 : nk - 1, k2 = 2 < nk ? 2 : nk - 1;
-    a.rload(ra1, m0, kbeg + k1 * BK, wave, lane);
-    b.rload(rb1, n0, kbeg + k1 * BK, wave, lane);
-    a.rload(ra0, m0, kbeg + k2 * BK, wave, lane);
-    b.rload(rb0, n0, kbeg + k2 * BK, wave, lane);
+    // (none for a block with an empty K range: its loop does not run)
+    if (nk > 0) {
+      a.rload(ra1, m0, kbeg, wave, lane);
+      b.rload(rb1, n0, kbeg, wave, lane);
+      a.rstore(ra1, smem, wave, lane);
+      b.rstore(rb1, smem + OA::kBytes, wave, lane);
+      const int k1 = 1 < nk ? 1 : nk - 1, k2 = 2 < nk ? 2 : nk - 1;
+      a.rload(ra1, m0, kbeg + k1 * BK, wave, lane);
+      b.rload(rb1, n0, kbeg + k1 * BK, wave, lane);
+      a.rload(ra0, m0, kbeg + k2 * BK, wave, lane);
+      b.rload(rb0, n0, kbeg + k2 * BK, wave, lane);
+    }
   } else {
 #pragma unroll
     for (int s = 0; s < NS - 1; ++s)
