@@ -50,7 +50,7 @@ FP16_PEAK_TFLOPS = 2516.6  # dense fp16 MFMA, MI355X
 # kernel (FETCH_SIZE reads half the bytes copied: x2.0; WRITE_SIZE x1.0).
 # Summary: profiles/value_backward_hbm_traffic.txt. Re-measure when the kernel changes.
 TRAFFIC_BYTES = {
-    "value_backward": (21648.5 * 2.0 + 12649.5 * 1.0) * 1024,
+    "value_backward": (21661.5 * 2.0 + 12294.0 * 1.0) * 1024,
 }
 
 # rocprofv3 kernel-trace average of the same launches in the timed pass of
